@@ -1,0 +1,185 @@
+/* lrm_hip.h — the C ABI of liblrm_hip.so, the MI355X (gfx950) HIP device and Qwen3 executor for enderPeer/rosylnalive.
+ *
+ * Every function returns an int status (LRM_OK = 0) unless stated; on failure lrm_last_error() holds a message on the
+ * calling thread. LRM_E_CONTRACT is the reference's GpuContractException (src/Lrm.Gpu.Core/Errors.fs:7-13), raised by
+ * the same host-side checks before any device work; LRM_E_HIP is a device or HIP API failure (the reference's
+ * backend-specific exception). Calls on one device come from one thread at a time (src/Lrm.Gpu.Core/Backend.fs:138).
+ * No PyTorch or HIP types cross this boundary: plain pointers, sizes and opaque handles only.
+ *
+ * Each declaration names the reference interface it replaces (file:line in enderPeer/rosylnalive).
+ */
+#ifndef LRM_HIP_H
+#define LRM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LRM_OK 0
+#define LRM_E_CONTRACT 1 /* GpuContractException */
+#define LRM_E_HIP 2      /* device lost, HIP API failure */
+#define LRM_E_ARG 3      /* invalid argument to the executor or a helper */
+#define LRM_E_INTERNAL 4
+
+#define LRM_ABI_VERSION 1
+
+/* Message of the last failure on this thread (never NULL). */
+const char *lrm_last_error(void);
+int lrm_abi_version(void);
+
+/* ======================================================================== contract helpers (host only, no GPU)
+ * The shared checks of Lrm.Gpu.Core, exported so a host that builds its own tables (the F# side) and tests can use the
+ * exact rules the device enforces. */
+
+/* Kernels.all / catalog.json (src/Lrm.Gpu.Core/Kernels.g.fs:27-285): ids 0..13 are the reference catalog, 14.. are
+ * this backend's appended bf16 kernels. kind: 1 token, 2 u32, 3 i32, 4 f32; access: 1 read, 2 write, 3 readwrite,
+ * 4 meta; dtype_mask: bit (1 << DType code). */
+int lrm_catalog_count(void);
+int lrm_catalog_find(const char *name); /* id, or -1 */
+int lrm_catalog_kernel(uint32_t id, char *name, int name_cap, uint32_t threads[3], int *linear, int *field_count);
+int lrm_catalog_field(uint32_t id, int field, char *name, int name_cap, int *kind, int *access, uint32_t *dtype_mask);
+
+/* Grid.physical (src/Lrm.Gpu.Core/ArgBlock.fs:368-387): folds a linear grid above 65,535 groups. */
+int lrm_grid_physical(int linear, int64_t x, int64_t y, int64_t z, uint32_t out[3]);
+
+/* TensorRow.create and debugIdOf (src/Lrm.Gpu.Core/TensorTable.fs:60-230). */
+int lrm_tensor_row(int slot, uint64_t byte_offset, uint32_t dtype, const uint32_t *dims, int rank, uint32_t flags,
+                   const char *name, uint32_t out_words[16]);
+uint32_t lrm_debug_id(const char *name);
+
+/* HeapPlanner (src/Lrm.Gpu.Core/HeapLayout.fs:433-525). */
+typedef struct lrm_planner lrm_planner;
+int lrm_planner_create(uint64_t page_bytes, lrm_planner **out);
+int lrm_planner_allocate(lrm_planner *p, uint32_t arena, uint64_t bytes, int32_t *page_index, uint64_t *offset);
+int lrm_planner_build(lrm_planner *p, uint32_t *arenas, uint64_t *page_bytes, int capacity, int *pages);
+void lrm_planner_destroy(lrm_planner *p);
+
+/* TensorTable and SealedTable (src/Lrm.Gpu.Core/TensorTable.fs:378-474), over a layout given as HeapLayout.ofPages
+ * (src/Lrm.Gpu.Core/HeapLayout.fs:302-420): pages[i] = (arena code, bytes). */
+typedef struct lrm_table lrm_table;
+int lrm_table_create(const uint32_t *arenas, const uint64_t *page_bytes, int pages, lrm_table **out);
+int lrm_table_add(lrm_table *t, const char *name, int slot, uint64_t byte_offset, uint32_t dtype, const uint32_t *dims,
+                  int rank, uint32_t flags, uint32_t *token);
+int lrm_table_add_view(lrm_table *t, const char *name, uint32_t source, const uint32_t *dims, int rank,
+                       uint64_t element_offset, uint32_t *token);
+int lrm_table_seal(lrm_table *t, uint8_t *image_out /* 1 MiB */);
+void lrm_table_destroy(lrm_table *t);
+
+/* Dispatch.prepare (src/Lrm.Gpu.Core/Dispatch.fs:149-173) against a sealed image and layout: checks the block and
+ * writes the dispatched words (word 0 = physical x), the logical grid and the physical grid. */
+int lrm_prepare(const uint8_t *table_image, const uint32_t *arenas, const uint64_t *page_bytes, int pages,
+                uint32_t kernel, const uint32_t in_words[32], uint32_t out_words[32], int64_t grid[3],
+                uint32_t physical[3]);
+
+/* ======================================================================== the device
+ * IGpuBackendProvider.Enumerate / Create (src/Lrm.Gpu.Core/Backend.fs:156-161), DeviceInfo (Backend.fs:9-31). */
+typedef struct lrm_hip_device_info {
+    int32_t index;
+    char name[128];
+    char arch[64]; /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    uint32_t vendor_id; /* 0x1002 */
+    uint32_t pci_device_id;
+    char pci_bus[32];
+    char driver[64];
+    int64_t memory_bytes;
+    int32_t compute_units;
+} lrm_hip_device_info;
+
+int lrm_hip_enumerate(lrm_hip_device_info *infos, int capacity, int *count);
+
+typedef struct lrm_hip_device lrm_hip_device;
+#define LRM_HIP_TIME_DISPATCHES 1u /* DeviceOptions.TimeDispatches (Backend.fs:38-55) */
+int lrm_hip_create(int index, uint32_t flags, lrm_hip_device **out);
+int lrm_hip_destroy(lrm_hip_device *d); /* IDisposable: waits for outstanding work */
+int lrm_hip_info(lrm_hip_device *d, lrm_hip_device_info *out);
+
+/* IGpuHeap (Backend.fs:111-122): CreateHeap once, WriteTable once before the first dispatch, Upload/Download wait for
+ * all submitted work first. */
+int lrm_hip_create_heap(lrm_hip_device *d, const uint32_t *arenas, const uint64_t *page_bytes, int pages);
+int lrm_hip_write_table(lrm_hip_device *d, const void *image, uint64_t bytes);
+int lrm_hip_upload(lrm_hip_device *d, int slot, uint64_t offset, const void *src, uint64_t bytes);
+int lrm_hip_download(lrm_hip_device *d, int slot, uint64_t offset, void *dst, uint64_t bytes);
+
+/* IGpuBackend.LoadKernels / IKernelSet (Backend.fs:104-108,144-147): the gfx950 code objects are part of this
+ * library; the shader-set hash is the SHA-256 of the library file. Runs the fp32 denormal probe
+ * (Backend.fs:457-547): mode 1 preserve, 2 flush, 3 mixed. */
+int lrm_hip_load_kernels(lrm_hip_device *d, uint8_t shader_set_hash[32]);
+int lrm_hip_contains(lrm_hip_device *d, uint32_t kernel); /* 1 or 0 */
+int lrm_hip_denormal_probe(lrm_hip_device *d, int *mode, uint32_t results[7]);
+
+/* ICommandList (Backend.fs:125-136) and IGpuBackend.Begin/Submit/Wait (Backend.fs:148-153). A list created with
+ * reusable = 1 is an extension for replay: it is captured into a HIP graph at its first submission and every
+ * submission (with `repeat` >= 1) replays it; it may not hold timers. One-shot lists are closed by Submit. */
+typedef struct lrm_hip_list lrm_hip_list;
+int lrm_hip_begin(lrm_hip_device *d, int reusable, lrm_hip_list **out);
+int lrm_hip_dispatch(lrm_hip_list *l, uint32_t kernel, const uint32_t words[32]);
+int lrm_hip_barrier(lrm_hip_list *l);
+int lrm_hip_copy(lrm_hip_list *l, int src_slot, uint64_t src_offset, int dst_slot, uint64_t dst_offset, uint64_t bytes);
+int lrm_hip_begin_timer(lrm_hip_list *l, const char *name, int *timer);
+int lrm_hip_end_timer(lrm_hip_list *l, int timer);
+int lrm_hip_submit(lrm_hip_device *d, lrm_hip_list *l, uint32_t repeat, uint64_t *fence);
+int lrm_hip_wait(lrm_hip_device *d, uint64_t fence, int *dispatches, int *timers);
+int lrm_hip_timer(lrm_hip_device *d, uint64_t fence, int index, char *name, int name_cap, int64_t *start_ns,
+                  int64_t *duration_ns);
+int lrm_hip_release(lrm_hip_device *d, lrm_hip_list *l); /* frees a reusable list */
+
+/* ======================================================================== the Qwen3 executor
+ * The counterpart of the planned Lrm.Gpu.Exec GpuForwardOps and Lrm.Models.Qwen Forward/Greedy (docs/dev-plan.md:
+ * 166-170,205-209,289-290), whose only existing form is tests/Lrm.Tensor.Tests/TinyModel.fs:144-236. mode 0 runs the
+ * reference catalog kernels in fp32 (parity with CpuRef F32); mode 1 runs the bf16 fast path. */
+typedef struct lrm_qwen_config {
+    int32_t layers, hidden, heads, kv_heads, head_dim, intermediate, vocab, max_pos;
+    float eps;
+    int32_t mode;       /* 0 fp32 catalog, 1 bf16 fast */
+    int32_t max_tokens; /* rows per forward chunk */
+    int32_t batch;      /* sequences (1) */
+    int32_t taps;       /* mode 0: keep every ActivationNames tap (src/Lrm.Tensor/Goldens.fs:288-322) */
+} lrm_qwen_config;
+
+typedef struct lrm_qwen lrm_qwen;
+/* inv_freq_bits: the pinned float32 inverse frequencies, head_dim / 2 words (Rope.fs:218-251). */
+int lrm_qwen_create(lrm_hip_device *d, const lrm_qwen_config *cfg, const uint32_t *inv_freq_bits, int half,
+                    lrm_qwen **out);
+int lrm_qwen_destroy(lrm_qwen *q);
+/* Weights by Hugging Face name, bf16 bits (TinyModel.fs:79-101 names; tied lm_head = model.embed_tokens.weight). */
+int lrm_qwen_set_weight(lrm_qwen *q, const char *name, const uint16_t *data, uint64_t elems);
+int lrm_qwen_read_weight(lrm_qwen *q, const char *name, uint16_t *out, uint64_t elems);
+/* TinyModel.forward (TinyModel.fs:144-204): ids at positions pos0 .. pos0 + t - 1; writes the cache; the last
+ * logits_rows rows of logits (f32 [logits_rows, vocab]) when logits != NULL; *argmax = argmax of the last row
+ * (0xFFFFFFFF for a row holding a NaN, argmaxRows semantics). */
+int lrm_qwen_forward(lrm_qwen *q, int seq, int pos0, const int32_t *ids, int t, float *logits, int logits_rows,
+                     uint32_t *argmax);
+/* TinyModel.greedy (TinyModel.fs:219-236): prefill then steps - 1 decode steps; mode 1 decodes on device. */
+int lrm_qwen_greedy(lrm_qwen *q, const int32_t *prompt, int prompt_len, int steps, int32_t *out_ids);
+/* On-device decode (mode 1): state = (token id at position pos), run `steps` recorded decode steps (one HIP graph
+ * replay each), read the ids they produced (out_ids[s] = the id chosen by step s). */
+int lrm_qwen_decode_set(lrm_qwen *q, const int32_t *ids, const int32_t *pos);
+int lrm_qwen_decode_run(lrm_qwen *q, int steps);
+int lrm_qwen_decode_ids(lrm_qwen *q, int32_t *out, int count);
+/* Rows of the logits buffer: after a decode step, row 0 holds that step's logits. */
+int lrm_qwen_read_logits(lrm_qwen *q, float *out, int rows);
+double lrm_qwen_last_ms(lrm_qwen *q); /* device time of the last forward / decode run, ms */
+int lrm_qwen_token(lrm_qwen *q, const char *name, uint32_t *token);
+lrm_hip_device *lrm_qwen_device(lrm_qwen *q);
+int lrm_qwen_tap_count(lrm_qwen *q);
+int lrm_qwen_tap_info(lrm_qwen *q, int i, char *name, int name_cap, int *width);
+int lrm_qwen_read_tap(lrm_qwen *q, int i, float *out, int rows);
+/* KV cache rows (which: 0 = K after norm and RoPE, 1 = V) as f32 [rows, kv_heads * head_dim]. */
+int lrm_qwen_read_cache(lrm_qwen *q, int seq, int layer, int which, int row0, int rows, float *out);
+int lrm_qwen_write_cache(lrm_qwen *q, int seq, int layer, int which, int row0, int rows, const float *in);
+int lrm_qwen_fill_cache_random(lrm_qwen *q, uint64_t seed, int rows);
+
+/* ======================================================================== inputs
+ * Synthetic N(0, std) values (counter-based, thread-count independent) and the T_spec RoPE table. */
+uint64_t lrm_stream_of(const char *name);
+int lrm_synth_normal_f32(uint64_t seed, uint64_t stream, uint64_t n, float std, float *out);
+int lrm_synth_normal_bf16(uint64_t seed, uint64_t stream, uint64_t n, float std, uint16_t *out);
+int lrm_rope_table(const uint32_t *inv_freq_bits, int half, int max_pos, float *cos_out, float *sin_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

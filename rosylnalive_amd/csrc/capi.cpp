@@ -1,0 +1,573 @@
+// extern "C" entry points of liblrm_hip.so (include/lrm_hip.h): thin wrappers that map C++ exceptions to status codes
+// and a thread-local message.
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/lrm_hip.h"
+#include "contract.hpp"
+#include "device.hpp"
+#include "qwen_exec.hpp"
+
+using namespace lrm;
+
+static thread_local std::string g_err;
+
+template <class F>
+static int guard(F&& f) {
+    try {
+        f();
+        return LRM_OK;
+    } catch (const ContractError& e) {
+        g_err = e.what();
+        return LRM_E_CONTRACT;
+    } catch (const HipError& e) {
+        g_err = e.what();
+        return LRM_E_HIP;
+    } catch (const std::invalid_argument& e) {
+        g_err = e.what();
+        return LRM_E_ARG;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return LRM_E_INTERNAL;
+    } catch (...) {
+        g_err = "unknown failure";
+        return LRM_E_INTERNAL;
+    }
+}
+
+static void need_ptr(const void* p, const char* what) {
+    if (!p) throw std::invalid_argument(std::string(what) + " is NULL");
+}
+
+static void copy_str(char* dst, int cap, const char* src) {
+    if (!dst || cap <= 0) return;
+    std::snprintf(dst, size_t(cap), "%s", src);
+}
+
+static HeapLayout layout_of(const uint32_t* arenas, const uint64_t* bytes, int pages) {
+    if (pages < 0 || (pages > 0 && (!arenas || !bytes))) throw std::invalid_argument("bad page list");
+    std::vector<std::pair<uint32_t, uint64_t>> kb;
+    for (int i = 0; i < pages; ++i) kb.emplace_back(arenas[i], bytes[i]);
+    return HeapLayout::of_pages(kb);
+}
+
+struct lrm_planner {
+    HeapPlanner p;
+};
+struct lrm_table {
+    TensorTable t;
+};
+struct lrm_hip_device {
+    Device d;
+    lrm_hip_device(int index, uint32_t flags) : d(index, flags) {}
+};
+struct lrm_hip_list {
+    CommandList* l;
+    lrm_hip_device* owner;
+};
+struct lrm_qwen {
+    QwenExec q;
+    lrm_hip_device* dev;
+    lrm_qwen(lrm_hip_device* d, const QwenConfig& c, const uint32_t* inv) : q(d->d, c, inv), dev(d) {}
+};
+
+extern "C" {
+
+const char* lrm_last_error(void) { return g_err.c_str(); }
+int lrm_abi_version(void) { return LRM_ABI_VERSION; }
+
+// ---------------------------------------------------------------- contract helpers
+
+int lrm_catalog_count(void) { return catalog_size(); }
+int lrm_catalog_find(const char* name) { return name ? catalog_find(name) : -1; }
+
+int lrm_catalog_kernel(uint32_t id, char* name, int cap, uint32_t threads[3], int* linear, int* field_count) {
+    return guard([&] {
+        if (id >= uint32_t(catalog_size())) contract_fail("kernel id %u is not in the catalog", id);
+        const KernelSpec& k = catalog()[id];
+        copy_str(name, cap, k.name);
+        if (threads)
+            for (int i = 0; i < 3; ++i) threads[i] = uint32_t(k.threads[i]);
+        if (linear) *linear = k.linear;
+        if (field_count) *field_count = int(k.fields.size());
+    });
+}
+
+int lrm_catalog_field(uint32_t id, int field, char* name, int cap, int* kind, int* access, uint32_t* mask) {
+    return guard([&] {
+        if (id >= uint32_t(catalog_size())) contract_fail("kernel id %u is not in the catalog", id);
+        const KernelSpec& k = catalog()[id];
+        if (field < 0 || field >= int(k.fields.size())) contract_fail("kernel %s has no field %d", k.name, field);
+        const FieldSpec& f = k.fields[size_t(field)];
+        copy_str(name, cap, f.name);
+        if (kind) *kind = int(f.kind);
+        if (access) *access = int(f.access);
+        if (mask) *mask = f.dtype_mask;
+    });
+}
+
+int lrm_grid_physical(int linear, int64_t x, int64_t y, int64_t z, uint32_t out[3]) {
+    return guard([&] {
+        need_ptr(out, "out");
+        Physical p = grid_physical(linear != 0, Grid3{x, y, z});
+        out[0] = p.x;
+        out[1] = p.y;
+        out[2] = p.z;
+    });
+}
+
+int lrm_tensor_row(int slot, uint64_t off, uint32_t dtype, const uint32_t* dims, int rank, uint32_t flags,
+                   const char* name, uint32_t out[16]) {
+    return guard([&] {
+        need_ptr(out, "out");
+        if (rank < 0 || (rank > 0 && !dims)) throw std::invalid_argument("bad dims");
+        TensorRow r = TensorRow::create(slot, off, dtype, std::vector<uint32_t>(dims, dims + rank), flags, name ? name : "");
+        std::memcpy(out, r.w.data(), 64);
+    });
+}
+
+uint32_t lrm_debug_id(const char* name) { return debug_id_of(name ? name : ""); }
+
+int lrm_planner_create(uint64_t page_bytes, lrm_planner** out) {
+    return guard([&] {
+        need_ptr(out, "out");
+        *out = new lrm_planner{HeapPlanner(page_bytes)};
+    });
+}
+
+int lrm_planner_allocate(lrm_planner* p, uint32_t arena, uint64_t bytes, int32_t* page, uint64_t* offset) {
+    return guard([&] {
+        need_ptr(p, "planner");
+        Placement pl = p->p.allocate(arena, bytes);
+        if (page) *page = pl.page;
+        if (offset) *offset = pl.offset;
+    });
+}
+
+int lrm_planner_build(lrm_planner* p, uint32_t* arenas, uint64_t* bytes, int cap, int* pages) {
+    return guard([&] {
+        need_ptr(p, "planner");
+        HeapLayout l = p->p.build();
+        if (pages) *pages = int(l.pages.size());
+        for (size_t i = 0; i < l.pages.size() && int(i) < cap; ++i) {
+            if (arenas) arenas[i] = l.pages[i].arena;
+            if (bytes) bytes[i] = l.pages[i].bytes;
+        }
+    });
+}
+
+void lrm_planner_destroy(lrm_planner* p) { delete p; }
+
+int lrm_table_create(const uint32_t* arenas, const uint64_t* bytes, int pages, lrm_table** out) {
+    return guard([&] {
+        need_ptr(out, "out");
+        *out = new lrm_table{TensorTable(layout_of(arenas, bytes, pages))};
+    });
+}
+
+int lrm_table_add(lrm_table* t, const char* name, int slot, uint64_t off, uint32_t dtype, const uint32_t* dims, int rank,
+                  uint32_t flags, uint32_t* token) {
+    return guard([&] {
+        need_ptr(t, "table");
+        if (rank < 0 || (rank > 0 && !dims)) throw std::invalid_argument("bad dims");
+        uint32_t tok = t->t.add(name ? name : "", slot, off, dtype, std::vector<uint32_t>(dims, dims + rank), flags);
+        if (token) *token = tok;
+    });
+}
+
+int lrm_table_add_view(lrm_table* t, const char* name, uint32_t source, const uint32_t* dims, int rank, uint64_t eoff,
+                       uint32_t* token) {
+    return guard([&] {
+        need_ptr(t, "table");
+        if (rank < 0 || (rank > 0 && !dims)) throw std::invalid_argument("bad dims");
+        uint32_t tok = t->t.add_view(name ? name : "", source, std::vector<uint32_t>(dims, dims + rank), eoff);
+        if (token) *token = tok;
+    });
+}
+
+int lrm_table_seal(lrm_table* t, uint8_t* image) {
+    return guard([&] {
+        need_ptr(t, "table");
+        t->t.seal();
+        if (image) std::memcpy(image, t->t.image().data(), kTableBytes);
+    });
+}
+
+void lrm_table_destroy(lrm_table* t) { delete t; }
+
+int lrm_prepare(const uint8_t* image, const uint32_t* arenas, const uint64_t* bytes, int pages, uint32_t kernel,
+                const uint32_t in[32], uint32_t out[32], int64_t grid[3], uint32_t physical[3]) {
+    return guard([&] {
+        need_ptr(image, "table image");
+        need_ptr(in, "words");
+        HeapLayout layout = layout_of(arenas, bytes, pages);
+        (void)layout;
+        PreparedDispatch pd = prepare(SealedTableView{image}, int(kernel), in);
+        if (out) std::memcpy(out, pd.words.data(), 128);
+        if (grid) {
+            grid[0] = pd.grid.x;
+            grid[1] = pd.grid.y;
+            grid[2] = pd.grid.z;
+        }
+        if (physical) {
+            physical[0] = pd.physical.x;
+            physical[1] = pd.physical.y;
+            physical[2] = pd.physical.z;
+        }
+    });
+}
+
+// ---------------------------------------------------------------- device
+
+static void fill_info(const DeviceInfo& s, lrm_hip_device_info* o) {
+    std::memset(o, 0, sizeof *o);
+    o->index = s.index;
+    copy_str(o->name, sizeof o->name, s.name);
+    copy_str(o->arch, sizeof o->arch, s.arch);
+    o->vendor_id = s.vendor_id;
+    o->pci_device_id = s.pci_device_id;
+    copy_str(o->pci_bus, sizeof o->pci_bus, s.pci_bus);
+    copy_str(o->driver, sizeof o->driver, s.driver);
+    o->memory_bytes = s.memory_bytes;
+    o->compute_units = s.compute_units;
+}
+
+int lrm_hip_enumerate(lrm_hip_device_info* infos, int cap, int* count) {
+    return guard([&] {
+        auto all = Device::enumerate();
+        if (count) *count = int(all.size());
+        for (size_t i = 0; i < all.size() && int(i) < cap && infos; ++i) fill_info(all[i], &infos[i]);
+    });
+}
+
+int lrm_hip_create(int index, uint32_t flags, lrm_hip_device** out) {
+    return guard([&] {
+        need_ptr(out, "out");
+        *out = new lrm_hip_device(index, flags);
+    });
+}
+
+int lrm_hip_destroy(lrm_hip_device* d) {
+    return guard([&] { delete d; });
+}
+
+int lrm_hip_info(lrm_hip_device* d, lrm_hip_device_info* out) {
+    return guard([&] {
+        need_ptr(d, "device");
+        need_ptr(out, "out");
+        fill_info(d->d.info(), out);
+    });
+}
+
+int lrm_hip_create_heap(lrm_hip_device* d, const uint32_t* arenas, const uint64_t* bytes, int pages) {
+    return guard([&] {
+        need_ptr(d, "device");
+        d->d.create_heap(layout_of(arenas, bytes, pages));
+    });
+}
+
+int lrm_hip_write_table(lrm_hip_device* d, const void* image, uint64_t bytes) {
+    return guard([&] {
+        need_ptr(d, "device");
+        need_ptr(image, "image");
+        d->d.write_table(image, bytes);
+    });
+}
+
+int lrm_hip_upload(lrm_hip_device* d, int slot, uint64_t off, const void* src, uint64_t bytes) {
+    return guard([&] {
+        need_ptr(d, "device");
+        need_ptr(src, "src");
+        d->d.upload(slot, off, src, bytes);
+    });
+}
+
+int lrm_hip_download(lrm_hip_device* d, int slot, uint64_t off, void* dst, uint64_t bytes) {
+    return guard([&] {
+        need_ptr(d, "device");
+        need_ptr(dst, "dst");
+        d->d.download(slot, off, dst, bytes);
+    });
+}
+
+int lrm_hip_load_kernels(lrm_hip_device* d, uint8_t hash[32]) {
+    return guard([&] {
+        need_ptr(d, "device");
+        auto h = d->d.load_kernels();
+        if (hash) std::memcpy(hash, h.data(), 32);
+    });
+}
+
+int lrm_hip_contains(lrm_hip_device* d, uint32_t kernel) {
+    if (!d) return 0;
+    return d->d.kernels_loaded() && d->d.contains(int(kernel)) ? 1 : 0;
+}
+
+int lrm_hip_denormal_probe(lrm_hip_device* d, int* mode, uint32_t results[7]) {
+    return guard([&] {
+        need_ptr(d, "device");
+        if (!d->d.kernels_loaded()) contract_fail("the denormal probe runs after LoadKernels");
+        if (mode) *mode = d->d.denormal_mode();
+        if (results) std::memcpy(results, d->d.denormal_results().data(), 28);
+    });
+}
+
+int lrm_hip_begin(lrm_hip_device* d, int reusable, lrm_hip_list** out) {
+    return guard([&] {
+        need_ptr(d, "device");
+        need_ptr(out, "out");
+        *out = new lrm_hip_list{d->d.begin(reusable != 0), d};
+    });
+}
+
+int lrm_hip_dispatch(lrm_hip_list* l, uint32_t kernel, const uint32_t words[32]) {
+    return guard([&] {
+        need_ptr(l, "list");
+        need_ptr(words, "words");
+        l->l->dispatch(int(kernel), words);
+    });
+}
+
+int lrm_hip_barrier(lrm_hip_list* l) {
+    return guard([&] {
+        need_ptr(l, "list");
+        l->l->barrier();
+    });
+}
+
+int lrm_hip_copy(lrm_hip_list* l, int ss, uint64_t so, int ds, uint64_t dof, uint64_t bytes) {
+    return guard([&] {
+        need_ptr(l, "list");
+        l->l->copy(ss, so, ds, dof, bytes);
+    });
+}
+
+int lrm_hip_begin_timer(lrm_hip_list* l, const char* name, int* timer) {
+    return guard([&] {
+        need_ptr(l, "list");
+        int t = l->l->begin_timer(name ? name : "");
+        if (timer) *timer = t;
+    });
+}
+
+int lrm_hip_end_timer(lrm_hip_list* l, int timer) {
+    return guard([&] {
+        need_ptr(l, "list");
+        l->l->end_timer(timer);
+    });
+}
+
+int lrm_hip_submit(lrm_hip_device* d, lrm_hip_list* l, uint32_t repeat, uint64_t* fence) {
+    return guard([&] {
+        need_ptr(d, "device");
+        need_ptr(l, "list");
+        if (l->owner != d) contract_fail("the command list belongs to another backend");
+        uint64_t f = d->d.submit(l->l, repeat);
+        if (fence) *fence = f;
+    });
+}
+
+int lrm_hip_wait(lrm_hip_device* d, uint64_t fence, int* dispatches, int* timers) {
+    return guard([&] {
+        need_ptr(d, "device");
+        const Completion& c = d->d.wait(fence);
+        if (dispatches) *dispatches = c.dispatches;
+        if (timers) *timers = int(c.timers.size());
+    });
+}
+
+int lrm_hip_timer(lrm_hip_device* d, uint64_t fence, int index, char* name, int cap, int64_t* start, int64_t* dur) {
+    return guard([&] {
+        need_ptr(d, "device");
+        const Completion& c = d->d.wait(fence);
+        if (index < 0 || index >= int(c.timers.size())) contract_fail("submission has no timer %d", index);
+        const TimerResult& t = c.timers[size_t(index)];
+        copy_str(name, cap, t.name.c_str());
+        if (start) *start = t.start_ns;
+        if (dur) *dur = t.duration_ns;
+    });
+}
+
+int lrm_hip_release(lrm_hip_device* d, lrm_hip_list* l) {
+    return guard([&] {
+        need_ptr(d, "device");
+        need_ptr(l, "list");
+        d->d.release(l->l);
+        delete l;
+    });
+}
+
+// ---------------------------------------------------------------- executor
+
+int lrm_qwen_create(lrm_hip_device* d, const lrm_qwen_config* c, const uint32_t* inv, int half, lrm_qwen** out) {
+    return guard([&] {
+        need_ptr(d, "device");
+        need_ptr(c, "config");
+        need_ptr(inv, "inv_freq_bits");
+        need_ptr(out, "out");
+        if (half * 2 != c->head_dim) throw std::invalid_argument("inv_freq_bits must hold head_dim / 2 words");
+        QwenConfig qc{c->layers, c->hidden, c->heads, c->kv_heads, c->head_dim, c->intermediate, c->vocab, c->max_pos,
+                      c->eps,    c->mode,   c->max_tokens, c->batch < 1 ? 1 : c->batch, c->taps};
+        *out = new lrm_qwen(d, qc, inv);
+    });
+}
+
+int lrm_qwen_destroy(lrm_qwen* q) {
+    return guard([&] { delete q; });
+}
+
+int lrm_qwen_set_weight(lrm_qwen* q, const char* name, const uint16_t* data, uint64_t elems) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(name, "name");
+        need_ptr(data, "data");
+        q->q.set_weight(name, data, elems);
+    });
+}
+
+int lrm_qwen_read_weight(lrm_qwen* q, const char* name, uint16_t* out, uint64_t elems) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(name, "name");
+        need_ptr(out, "out");
+        q->q.read_weight(name, out, elems);
+    });
+}
+
+int lrm_qwen_forward(lrm_qwen* q, int seq, int pos0, const int32_t* ids, int t, float* logits, int rows, uint32_t* am) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(ids, "ids");
+        uint32_t a = q->q.forward(seq, pos0, ids, t, logits, logits ? rows : 0);
+        if (am) *am = a;
+    });
+}
+
+int lrm_qwen_greedy(lrm_qwen* q, const int32_t* prompt, int plen, int steps, int32_t* out) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(prompt, "prompt");
+        need_ptr(out, "out_ids");
+        q->q.greedy(prompt, plen, steps, out);
+    });
+}
+
+int lrm_qwen_decode_set(lrm_qwen* q, const int32_t* ids, const int32_t* pos) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(ids, "ids");
+        need_ptr(pos, "pos");
+        q->q.set_decode_state(ids, pos);
+    });
+}
+
+int lrm_qwen_decode_run(lrm_qwen* q, int steps) {
+    return guard([&] {
+        need_ptr(q, "model");
+        q->q.run_decode_steps(steps);
+    });
+}
+
+int lrm_qwen_decode_ids(lrm_qwen* q, int32_t* out, int count) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(out, "out");
+        q->q.read_decode_ids(out, count);
+    });
+}
+
+int lrm_qwen_read_logits(lrm_qwen* q, float* out, int rows) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(out, "out");
+        uint32_t tok = q->q.token("logits");
+        TensorRow r = q->dev->d.table().row(tok);
+        uint64_t bytes = uint64_t(rows) * uint64_t(q->q.config().vocab) * 4;
+        if (rows < 0 || bytes > r.extent_bytes()) throw std::invalid_argument("logits rows out of range");
+        q->dev->d.download(int(r.slot()), r.offset(), out, bytes);
+    });
+}
+
+double lrm_qwen_last_ms(lrm_qwen* q) { return q ? q->q.last_ms() : -1.0; }
+
+int lrm_qwen_token(lrm_qwen* q, const char* name, uint32_t* token) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(name, "name");
+        uint32_t t = q->q.token(name);
+        if (token) *token = t;
+    });
+}
+
+lrm_hip_device* lrm_qwen_device(lrm_qwen* q) { return q ? q->dev : nullptr; }
+
+int lrm_qwen_tap_count(lrm_qwen* q) { return q ? q->q.tap_count() : 0; }
+
+int lrm_qwen_tap_info(lrm_qwen* q, int i, char* name, int cap, int* width) {
+    return guard([&] {
+        need_ptr(q, "model");
+        copy_str(name, cap, q->q.tap_name(i).c_str());
+        if (width) *width = q->q.tap_width(i);
+    });
+}
+
+int lrm_qwen_read_tap(lrm_qwen* q, int i, float* out, int rows) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(out, "out");
+        q->q.read_tap(i, out, rows);
+    });
+}
+
+int lrm_qwen_read_cache(lrm_qwen* q, int seq, int layer, int which, int row0, int rows, float* out) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(out, "out");
+        q->q.read_cache(seq, layer, which, row0, rows, out);
+    });
+}
+
+int lrm_qwen_write_cache(lrm_qwen* q, int seq, int layer, int which, int row0, int rows, const float* in) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(in, "in");
+        q->q.write_cache(seq, layer, which, row0, rows, in);
+    });
+}
+
+int lrm_qwen_fill_cache_random(lrm_qwen* q, uint64_t seed, int rows) {
+    return guard([&] {
+        need_ptr(q, "model");
+        q->q.fill_cache_random(seed, rows);
+    });
+}
+
+// ---------------------------------------------------------------- inputs
+
+uint64_t lrm_stream_of(const char* name) { return stream_of(name ? name : ""); }
+
+int lrm_synth_normal_f32(uint64_t seed, uint64_t stream, uint64_t n, float std_, float* out) {
+    return guard([&] {
+        need_ptr(out, "out");
+        synth_normal_f32(seed, stream, n, std_, out);
+    });
+}
+
+int lrm_synth_normal_bf16(uint64_t seed, uint64_t stream, uint64_t n, float std_, uint16_t* out) {
+    return guard([&] {
+        need_ptr(out, "out");
+        synth_normal_bf16(seed, stream, n, std_, out);
+    });
+}
+
+int lrm_rope_table(const uint32_t* inv, int half, int max_pos, float* c, float* s) {
+    return guard([&] {
+        need_ptr(inv, "inv_freq_bits");
+        need_ptr(c, "cos");
+        need_ptr(s, "sin");
+        rope_table(inv, half, max_pos, c, s);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,171 @@
+// The HIP device behind the reference's Lrm.Gpu.Core interfaces (src/Lrm.Gpu.Core/Backend.fs:104-161):
+// IGpuBackend (Device), IGpuHeap (the heap methods of Device), ICommandList (CommandList), IKernelSet (load/contains).
+//
+// MI355X-first choices, all invisible to callers of the contract:
+//   - one in-order HIP stream per device, so Barrier() costs nothing and Copy() is ordered on both sides;
+//   - the sealed table is kept on the host too: every token is resolved to a device pointer when a dispatch is
+//     recorded, and kernels receive plain pointers and the scalar argument words;
+//   - a fence is a hipEvent recorded after a submission; Wait synchronises it and returns the stored Completion;
+//   - a command list created reusable is captured into a hipGraph at its first submission and replayed by every later
+//     submission (the decode step of the executor): zero host work per replay.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <array>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "contract.hpp"
+
+namespace lrm {
+
+struct HipError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void hip_check(hipError_t e, const char* what);
+
+// The launch function of one catalog kernel: pointers per field (nullptr for non-token fields), the prepared words.
+using LaunchFn = void (*)(const PreparedDispatch& pd, void* const* ptr, hipStream_t stream);
+// One table per kernel source file; entry i is catalog id i or nullptr.
+const LaunchFn* catalog_launchers();  // ids 0..13
+const LaunchFn* fast_launchers();     // ids 14..
+int fast_first_id();
+
+struct DeviceInfo {
+    int index;
+    char name[128];
+    char arch[64];
+    uint32_t vendor_id;
+    uint32_t pci_device_id;
+    char pci_bus[32];
+    char driver[64];
+    int64_t memory_bytes;
+    int compute_units;
+};
+
+struct TimerResult {
+    std::string name;
+    int64_t start_ns;
+    int64_t duration_ns;
+};
+
+struct Completion {
+    uint64_t submission;
+    int dispatches;
+    std::vector<TimerResult> timers;
+};
+
+class Device;
+
+class CommandList {
+  public:
+    void dispatch(int kernel, const uint32_t* words);
+    void barrier();
+    void copy(int src_slot, uint64_t src_off, int dst_slot, uint64_t dst_off, uint64_t bytes);
+    int begin_timer(const std::string& name);
+    void end_timer(int timer);
+    int dispatch_count() const { return dispatches_; }
+    bool reusable() const { return reusable_; }
+    ~CommandList();
+
+  private:
+    friend class Device;
+    struct Cmd {
+        enum Kind { Launch, Copy, TimerBegin, TimerEnd } kind;
+        PreparedDispatch pd;
+        std::vector<void*> ptr;
+        void* src = nullptr;
+        void* dst = nullptr;
+        uint64_t bytes = 0;
+        int timer = -1;
+    };
+    CommandList(Device* d, bool reusable) : dev_(d), reusable_(reusable) {}
+    void check_open() const;
+    Device* dev_;
+    bool reusable_;
+    bool closed_ = false;      // a one-shot list after Submit
+    std::vector<Cmd> cmds_;
+    std::vector<std::string> timer_names_;
+    std::vector<int> open_timers_;
+    int dispatches_ = 0;
+    hipGraph_t graph_ = nullptr;
+    hipGraphExec_t exec_ = nullptr;
+};
+
+class Device {
+  public:
+    enum Flags : uint32_t { TimeDispatches = 1 };
+    static std::vector<DeviceInfo> enumerate();
+    Device(int index, uint32_t flags);
+    ~Device();
+
+    const DeviceInfo& info() const { return info_; }
+
+    // IGpuHeap
+    void create_heap(const HeapLayout& layout);
+    void write_table(const void* image, uint64_t bytes);
+    void upload(int slot, uint64_t offset, const void* src, uint64_t bytes);
+    void download(int slot, uint64_t offset, void* dst, uint64_t bytes);
+    const HeapLayout& layout() const;
+    bool table_written() const { return !table_host_.empty(); }
+    SealedTableView table() const;
+
+    // IKernelSet
+    std::array<uint8_t, 32> load_kernels();
+    bool kernels_loaded() const { return loaded_; }
+    bool contains(int kernel) const;
+    const std::array<uint8_t, 32>& shader_set_hash() const { return shader_hash_; }
+    // fp32 denormal mode measured by the probe after load_kernels (gpu-backend.md "fp32 denormals"): 0 unknown,
+    // 1 preserve, 2 flush, 3 mixed.
+    int denormal_mode() const { return denormal_mode_; }
+    const std::array<uint32_t, 7>& denormal_results() const { return probe_results_; }
+
+    // IGpuBackend
+    CommandList* begin(bool reusable = false);
+    uint64_t submit(CommandList* list, uint32_t repeat = 1);
+    const Completion& wait(uint64_t fence);
+    void release(CommandList* list);  // frees a list (one-shot lists are released by wait of their fence)
+
+    hipStream_t stream() const { return stream_; }
+    void* slot_ptr(int slot) const;
+    void* resolve(uint32_t token) const;  // device pointer of a token's first byte
+
+  private:
+    friend class CommandList;
+    void run(CommandList* l);
+    void run_probe();
+    DeviceInfo info_{};
+    int index_;
+    uint32_t flags_;
+    hipStream_t stream_ = nullptr;
+    hipEvent_t epoch_ = nullptr;
+    bool heap_created_ = false;
+    HeapLayout layout_;
+    std::vector<void*> pages_;  // slot i at pages_[i], slot 0 = the table buffer
+    std::vector<uint8_t> table_host_;
+    bool loaded_ = false;
+    std::array<uint8_t, 32> shader_hash_{};
+    int denormal_mode_ = 0;
+    std::array<uint32_t, 7> probe_results_{};
+    uint64_t next_fence_ = 1;
+    struct Pending {
+        hipEvent_t done;
+        std::vector<std::pair<hipEvent_t, hipEvent_t>> timer_events;
+        std::vector<std::string> timer_names;
+        int dispatches;
+        CommandList* owned;  // one-shot list to free after completion
+    };
+    std::map<uint64_t, Pending> pending_;
+    std::map<uint64_t, Completion> done_;
+    std::vector<std::unique_ptr<CommandList>> lists_;
+    // dispatch timing (TimeDispatches)
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> dispatch_events_;
+};
+
+}  // namespace lrm

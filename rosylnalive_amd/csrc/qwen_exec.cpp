@@ -1,0 +1,726 @@
+// The Qwen3 executor (see qwen_exec.hpp).
+#include "qwen_exec.hpp"
+
+#include <omp.h>
+#include <quadmath.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstring>
+
+namespace lrm {
+
+static uint32_t fbits(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+}
+
+static void arg_fail(const char* fmt, ...) __attribute__((format(printf, 1, 2), noreturn));
+static void arg_fail(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    throw std::invalid_argument(buf);
+}
+
+// ---------------------------------------------------------------- T_spec (Rope.fs:146-161, 218-251)
+// The correctly rounded float64 cos/sin of a float32: binary128 evaluation, accepted only when the value is farther
+// than 2^-100 (relative) from a float64 rounding boundary, so a binary128 error of a few ulps cannot cross it.
+static bool round_certain(__float128 v, double* out) {
+    double d = double(v);
+    if (v == __float128(d)) {
+        *out = d;
+        return true;
+    }
+    __float128 lo = (__float128(d) + __float128(std::nextafter(d, -INFINITY))) / 2;
+    __float128 hi = (__float128(d) + __float128(std::nextafter(d, INFINITY))) / 2;
+    __float128 tol = fabsq(v) * __float128(0x1p-100);
+    if (v - lo > tol && hi - v > tol) {
+        *out = d;
+        return true;
+    }
+    return false;
+}
+
+void rope_table(const uint32_t* inv, int half, int max_pos, float* cos_out, float* sin_out) {
+    if (half < 1 || max_pos < 1 || max_pos > (1 << 24)) arg_fail("rope table: half %d, max_pos %d", half, max_pos);
+    int bad = 0;
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int pos = 0; pos < max_pos; ++pos) {
+        for (int j = 0; j < half; ++j) {
+            float f;
+            std::memcpy(&f, &inv[j], 4);
+            volatile float fp = float(pos);
+            float x = fp * f;
+            double c, s;
+            if (!std::isfinite(x)) {
+                c = s = NAN;
+            } else if (std::fabs(x) < 0x1p-27f) {
+                c = 1.0;
+                s = double(x);
+            } else {
+                __float128 sq, cq;
+                sincosq(__float128(std::fabs(x)), &sq, &cq);
+                if (!round_certain(cq, &c) || !round_certain(sq, &s)) {
+#pragma omp atomic write
+                    bad = 1;
+                }
+                if (x < 0) s = -s;
+            }
+            cos_out[size_t(pos) * half + j] = float(c);
+            sin_out[size_t(pos) * half + j] = float(s);
+        }
+    }
+    if (bad) throw std::runtime_error("rope table: a cos/sin rounding could not be certified");
+}
+
+// ---------------------------------------------------------------- synthetic inputs
+
+static uint64_t splitmix(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+uint64_t stream_of(const char* name) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (const char* p = name; *p; ++p) h = (h ^ uint8_t(*p)) * 0x100000001b3ull;
+    return h;
+}
+
+void synth_normal_f32(uint64_t seed, uint64_t stream, uint64_t n, float std_, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t pi = 0; pi < int64_t((n + 1) / 2); ++pi) {
+        uint64_t i = uint64_t(pi) * 2;
+        uint64_t h = splitmix(seed ^ splitmix(stream ^ splitmix(i >> 1)));
+        double u1 = (double((h >> 11) & ((1ull << 26) - 1)) + 0.5) / double(1ull << 26);
+        double u2 = double(h >> 38) / double(1ull << 26);
+        double r = std::sqrt(-2.0 * std::log(u1));
+        out[i] = float(std_ * r * std::cos(6.283185307179586 * u2));
+        if (i + 1 < n) out[i + 1] = float(std_ * r * std::sin(6.283185307179586 * u2));
+    }
+}
+
+static uint16_t narrow_rne(float f) {
+    uint32_t u = fbits(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u & 0x80000000u) ? 0xFFC0 : 0x7FC0;
+    return uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+void synth_normal_bf16(uint64_t seed, uint64_t stream, uint64_t n, float std_, uint16_t* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t pi = 0; pi < int64_t((n + 1) / 2); ++pi) {
+        uint64_t i = uint64_t(pi) * 2;
+        uint64_t h = splitmix(seed ^ splitmix(stream ^ splitmix(i >> 1)));
+        double u1 = (double((h >> 11) & ((1ull << 26) - 1)) + 0.5) / double(1ull << 26);
+        double u2 = double(h >> 38) / double(1ull << 26);
+        double r = std::sqrt(-2.0 * std::log(u1));
+        out[i] = narrow_rne(float(std_ * r * std::cos(6.283185307179586 * u2)));
+        if (i + 1 < n) out[i + 1] = narrow_rne(float(std_ * r * std::sin(6.283185307179586 * u2)));
+    }
+}
+
+// ---------------------------------------------------------------- plan
+
+static const char* kLayerWeights[11] = {"input_layernorm.weight", "self_attn.q_proj.weight", "self_attn.k_proj.weight",
+                                        "self_attn.v_proj.weight", "self_attn.o_proj.weight", "self_attn.q_norm.weight",
+                                        "self_attn.k_norm.weight", "post_attention_layernorm.weight",
+                                        "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight"};
+
+static const char* kLayerTaps[18] = {"input_layernorm.out", "attn.q_proj.out", "attn.k_proj.out", "attn.v_proj.out",
+                                     "attn.q_norm.out", "attn.k_norm.out", "attn.q_rope", "attn.k_rope",
+                                     "attn.v_cache", "attn.o_proj.in", "attn.o_proj.out", "resid_mid",
+                                     "post_attention_layernorm.out", "mlp.gate.out", "mlp.up.out", "mlp.down.in",
+                                     "mlp.down.out", "out"};
+
+static std::string lname(int i, const char* n) { return "model.layers." + std::to_string(i) + "." + n; }
+
+void QwenExec::add(const std::string& name, uint32_t arena, uint32_t dtype, std::vector<uint32_t> dims, uint32_t flags) {
+    uint64_t elems = 1;
+    for (uint32_t d : dims) elems *= d;
+    uint64_t bytes = (elems * uint64_t(dtype_size(dtype)) + 3) / 4 * 4;
+    Tensor t{};
+    t.place = planner_.allocate(arena, bytes);
+    t.dtype = dtype;
+    t.dims = std::move(dims);
+    t.flags = flags;
+    tensors_[name] = t;
+    order_.push_back(name);
+}
+
+void QwenExec::add_view(const std::string& name, const std::string& of, std::vector<uint32_t> dims, uint64_t elem_offset) {
+    Tensor t{};
+    t.dims = std::move(dims);
+    t.view_of = of;
+    t.view_offset = elem_offset;
+    t.dtype = tensors_.at(of).dtype;
+    tensors_[name] = t;
+    order_.push_back(name);
+}
+
+const QwenExec::Tensor& QwenExec::t(const std::string& name) const {
+    auto it = tensors_.find(name);
+    if (it == tensors_.end()) arg_fail("no tensor '%s' in the plan", name.c_str());
+    return it->second;
+}
+
+uint32_t QwenExec::token(const std::string& name) const { return t(name).token; }
+
+QwenExec::QwenExec(Device& dev, const QwenConfig& cfg, const uint32_t* inv_freq_bits) : dev_(dev), cfg_(cfg) {
+    const QwenConfig& c = cfg_;
+    if (c.layers < 1 || c.hidden < 1 || c.heads < 1 || c.kv_heads < 1 || c.head_dim < 2 || c.intermediate < 1 ||
+        c.vocab < 1 || c.max_pos < 1 || c.max_tokens < 1)
+        arg_fail("a Qwen3 config needs positive sizes");
+    if (c.heads % c.kv_heads) arg_fail("kv_heads must divide heads");
+    if (c.head_dim % 2) arg_fail("head_dim must be even");
+    if (c.mode == 1) {
+        if (c.head_dim != 128 || c.heads != 2 * c.kv_heads)
+            arg_fail("the bf16 fast path takes head_dim 128 and two query heads per KV head");
+        if (c.hidden % 512 || c.intermediate % 64 || c.hidden > 8192)
+            arg_fail("the bf16 fast path takes hidden a multiple of 512 (<= 8192) and intermediate a multiple of 64");
+        if (c.max_pos % 64) arg_fail("the bf16 fast path takes max_pos a multiple of 64");
+        if (c.batch != 1) arg_fail("batched decode is not built yet: batch must be 1");
+    }
+    if (!dev_.kernels_loaded()) dev_.load_kernels();
+    plan();
+    upload_rope(inv_freq_bits);
+}
+
+QwenExec::~QwenExec() {
+    if (decode_list_) dev_.release(decode_list_);
+}
+
+void QwenExec::plan() {
+    const QwenConfig& c = cfg_;
+    const uint32_t H = c.hidden, QC = c.heads * c.head_dim, KC = c.kv_heads * c.head_dim, I = c.intermediate,
+                   V = c.vocab, MT = c.max_tokens, MP = c.max_pos, HD = c.head_dim;
+    const bool fast = c.mode == 1;
+    // pass one: placements (HeapLayout.fs:433-525); weights first, in contract arena order
+    add("model.embed_tokens.weight", Weights, BF16, {V, H}, ReadOnly);
+    add("model.norm.weight", Weights, BF16, {H}, ReadOnly);
+    for (int i = 0; i < c.layers; ++i) {
+        add(lname(i, kLayerWeights[0]), Weights, BF16, {H}, ReadOnly);
+        if (fast) {
+            add("L" + std::to_string(i) + ".qkv_proj", Weights, BF16, {QC + 2 * KC, H}, ReadOnly);
+        } else {
+            add(lname(i, kLayerWeights[1]), Weights, BF16, {QC, H}, ReadOnly);
+            add(lname(i, kLayerWeights[2]), Weights, BF16, {KC, H}, ReadOnly);
+            add(lname(i, kLayerWeights[3]), Weights, BF16, {KC, H}, ReadOnly);
+        }
+        add(lname(i, kLayerWeights[4]), Weights, BF16, {H, QC}, ReadOnly);
+        add(lname(i, kLayerWeights[5]), Weights, BF16, {HD}, ReadOnly);
+        add(lname(i, kLayerWeights[6]), Weights, BF16, {HD}, ReadOnly);
+        add(lname(i, kLayerWeights[7]), Weights, BF16, {H}, ReadOnly);
+        if (fast) {
+            add("L" + std::to_string(i) + ".gate_up_proj", Weights, BF16, {2 * I, H}, ReadOnly);
+        } else {
+            add(lname(i, kLayerWeights[8]), Weights, BF16, {I, H}, ReadOnly);
+            add(lname(i, kLayerWeights[9]), Weights, BF16, {I, H}, ReadOnly);
+        }
+        add(lname(i, kLayerWeights[10]), Weights, BF16, {H, I}, ReadOnly);
+    }
+    add("rope.cos", Rope, F32, {MP, HD / 2}, ReadOnly);
+    add("rope.sin", Rope, F32, {MP, HD / 2}, ReadOnly);
+    for (int i = 0; i < c.layers; ++i) {
+        std::string p = "L" + std::to_string(i);
+        if (fast) {
+            add(p + ".k_cache", KvCache, BF16, {uint32_t(c.kv_heads), MP, HD});
+            add(p + ".v_cache", KvCache, BF16, {uint32_t(c.kv_heads), HD, MP});
+        } else {
+            add(p + ".k_cache", KvCache, F32, {MP, KC});
+            add(p + ".v_cache", KvCache, F32, {MP, KC});
+        }
+    }
+    add("ids", Activations, U32, {MT});
+    add("x", Activations, F32, {MT, H});
+    const uint32_t LC = std::min<uint32_t>(MT, 512);  // logits rows per lm_head dispatch (K2-0001's row cap, raised)
+    if (fast) {
+        add("h", Activations, BF16, {MT, H});
+        add("q", Activations, BF16, {MT, QC});
+        add("o", Activations, BF16, {MT, QC});
+        add("a", Activations, BF16, {MT, I});
+        add("dec.x", Activations, F32, {H});
+        add("dec.q", Activations, F32, {QC});
+        add("dec.o", Activations, F32, {QC});
+        add("dec.a", Activations, F32, {I});
+        add("dec.qkv", Scratch, F32, {QC + 2 * KC});
+        add("dec.attn_partials", Scratch, F32, {uint32_t(c.heads) * (MP / 64) * 130});
+        add("dec.lm_partials", Scratch, F32, {2 * 1024});
+        add("dec.counters_qkv", Scratch, U32, {uint32_t(c.heads + 2 * c.kv_heads)});
+        add("dec.counters_attn", Scratch, U32, {uint32_t(c.kv_heads)});
+        add("dec.counters_lm", Scratch, U32, {4});
+        add("dec.state", Scratch, U32, {4});
+        add("dec.out_ids", Logits, U32, {MP});
+    } else {
+        for (const char* n : {"h", "oo", "r", "h2", "dd", "f"}) add(n, Activations, F32, {MT, H});
+        for (const char* n : {"q", "qn", "qr", "o"}) add(n, Activations, F32, {MT, QC});
+        for (const char* n : {"k", "v", "kn", "kr"}) add(n, Activations, F32, {MT, KC});
+        for (const char* n : {"g", "u", "d"}) add(n, Activations, F32, {MT, I});
+        add("f_last", Activations, F32, {LC, H});
+    }
+    add("logits", Logits, F32, {LC, V});
+    add("argmax", Logits, U32, {LC});
+    if (!fast && c.taps) {
+        auto tap = [&](const std::string& n, uint32_t wdt) {
+            add("tap." + n, Taps, F32, {MT, wdt});
+            tap_names_.push_back(n);
+            tap_widths_.push_back(int(wdt));
+        };
+        tap("embed.out", H);
+        for (int i = 0; i < c.layers; ++i) {
+            std::string p = "L" + std::to_string(i) + ".";
+            uint32_t w[18] = {H, QC, KC, KC, QC, KC, QC, KC, KC, QC, H, H, H, I, I, I, H, H};
+            for (int k = 0; k < 18; ++k) tap(p + kLayerTaps[k], w[k]);
+        }
+        tap("final_norm.out", H);
+        tap("logits", V);
+    }
+    if (fast) {
+        for (int i = 0; i < c.layers; ++i) {
+            std::string p = "L" + std::to_string(i);
+            add_view(lname(i, kLayerWeights[1]), p + ".qkv_proj", {QC, H}, 0);
+            add_view(lname(i, kLayerWeights[2]), p + ".qkv_proj", {KC, H}, uint64_t(QC) * H);
+            add_view(lname(i, kLayerWeights[3]), p + ".qkv_proj", {KC, H}, uint64_t(QC + KC) * H);
+            add_view(lname(i, kLayerWeights[8]), p + ".gate_up_proj", {I, H}, 0);
+            add_view(lname(i, kLayerWeights[9]), p + ".gate_up_proj", {I, H}, uint64_t(I) * H);
+        }
+    }
+    // pass two: the layout, the table, the heap
+    HeapLayout layout = planner_.build();
+    table_.reset(new TensorTable(layout));
+    for (const std::string& n : order_) {
+        Tensor& tt = tensors_[n];
+        if (tt.view_of.empty())
+            tt.token = table_->add_placed(n, planner_, tt.place, tt.dtype, tt.dims, tt.flags);
+        else
+            tt.token = table_->add_view(n, tensors_[tt.view_of].token, tt.dims, tt.view_offset);
+    }
+    table_->seal();
+    dev_.create_heap(layout);
+    dev_.write_table(table_->image().data(), kTableBytes);
+    for (int i = 0; i < c.layers; ++i)
+        for (int k = 0; k < 11; ++k) weight_names_.push_back(lname(i, kLayerWeights[k]));
+    weight_names_.push_back("model.embed_tokens.weight");
+    weight_names_.push_back("model.norm.weight");
+}
+
+void QwenExec::upload_tensor(const std::string& name, const void* data, uint64_t bytes, uint64_t byte_offset) {
+    TensorRow r = dev_.table().row(token(name));
+    if (byte_offset + bytes > r.extent_bytes()) arg_fail("%s holds %llu bytes", name.c_str(), (unsigned long long)r.extent_bytes());
+    dev_.upload(int(r.slot()), r.offset() + byte_offset, data, bytes);
+}
+
+void QwenExec::download_tensor(const std::string& name, void* out, uint64_t bytes, uint64_t byte_offset) {
+    TensorRow r = dev_.table().row(token(name));
+    if (byte_offset + bytes > r.extent_bytes()) arg_fail("%s holds %llu bytes", name.c_str(), (unsigned long long)r.extent_bytes());
+    dev_.download(int(r.slot()), r.offset() + byte_offset, out, bytes);
+}
+
+void QwenExec::upload_rope(const uint32_t* inv) {
+    const int half = cfg_.head_dim / 2, mp = cfg_.max_pos;
+    std::vector<float> cs(size_t(mp) * half), sn(size_t(mp) * half);
+    rope_table(inv, half, mp, cs.data(), sn.data());
+    upload_tensor("rope.cos", cs.data(), cs.size() * 4);
+    upload_tensor("rope.sin", sn.data(), sn.size() * 4);
+}
+
+std::vector<std::string> QwenExec::weight_names() const { return weight_names_; }
+
+void QwenExec::set_weight(const std::string& name, const uint16_t* data, uint64_t elems) {
+    const Tensor& tt = t(name);
+    uint64_t n = 1;
+    for (uint32_t d : tt.dims) n *= d;
+    if (tt.dtype != BF16 || n != elems) arg_fail("weight %s holds %llu bf16 elements, not %llu", name.c_str(), (unsigned long long)n, (unsigned long long)elems);
+    upload_tensor(name, data, elems * 2);
+}
+
+void QwenExec::read_weight(const std::string& name, uint16_t* out, uint64_t elems) {
+    const Tensor& tt = t(name);
+    uint64_t n = 1;
+    for (uint32_t d : tt.dims) n *= d;
+    if (n != elems) arg_fail("weight %s holds %llu elements", name.c_str(), (unsigned long long)n);
+    download_tensor(name, out, elems * 2);
+}
+
+uint32_t QwenExec::dispatch(CommandList* l, const char* kernel, std::vector<uint32_t> fields) {
+    int id = catalog_find(kernel);
+    if (id < 0) arg_fail("no kernel %s", kernel);
+    uint32_t words[32] = {0};
+    if (fields.size() > 31) arg_fail("too many fields");
+    for (size_t i = 0; i < fields.size(); ++i) words[i + 1] = fields[i];
+    l->dispatch(id, words);
+    return uint32_t(id);
+}
+
+void QwenExec::tap_copy(CommandList* l, const std::string& name, uint32_t src, int rows, int width) {
+    if (!cfg_.taps || cfg_.mode != 0) return;
+    TensorRow s = dev_.table().row(src), d = dev_.table().row(token("tap." + name));
+    l->copy(int(s.slot()), s.offset(), int(d.slot()), d.offset(), uint64_t(rows) * width * 4);
+}
+
+// ---------------------------------------------------------------- forward
+
+uint32_t QwenExec::forward(int seq, int pos0, const int32_t* ids, int t_, float* logits, int logits_rows) {
+    const QwenConfig& c = cfg_;
+    if (seq != 0) arg_fail("sequence %d: one sequence is planned", seq);
+    if (t_ < 1 || pos0 < 0 || pos0 + t_ > c.max_pos)
+        arg_fail("positions %d .. %d outside max_pos %d", pos0, pos0 + t_ - 1, c.max_pos);
+    if (logits_rows < 0 || logits_rows > t_) arg_fail("logits_rows %d outside 0 .. %d", logits_rows, t_);
+    uint32_t am = 0xFFFFFFFFu;
+    // chunked prefill: max_tokens rows at a time, the cache carrying the earlier chunks
+    for (int c0 = 0; c0 < t_; c0 += c.max_tokens) {
+        int n = std::min(c.max_tokens, t_ - c0);
+        int want = std::max(0, logits_rows - (t_ - (c0 + n)));  // logits rows that fall in this chunk
+        std::vector<uint32_t> u(static_cast<size_t>(n));
+        for (int i = 0; i < n; ++i) u[size_t(i)] = uint32_t(ids[c0 + i]);
+        upload_tensor("ids", u.data(), uint64_t(n) * 4);
+        float* lg = logits ? logits + size_t(logits_rows - want) * c.vocab : nullptr;
+        if (c.mode == 1)
+            am = forward_fast(seq, pos0 + c0, n, lg, std::max(want, 1));
+        else
+            am = forward_fp32(pos0 + c0, n, lg, std::max(want, 1));
+    }
+    last_t_ = t_;
+    return am;
+}
+
+uint32_t QwenExec::forward_fp32(int pos0, int T, float* logits, int lr) {
+    const QwenConfig& c = cfg_;
+    const uint32_t H = c.hidden, QC = c.heads * c.head_dim, KC = c.kv_heads * c.head_dim, I = c.intermediate,
+                   V = c.vocab, HD = c.head_dim, U = uint32_t(T);
+    const uint32_t eps = fbits(c.eps);
+    const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
+    CommandList* l = dev_.begin();
+    hipEvent_t e0, e1;
+    hip_check(hipEventCreate(&e0), "event");
+    hip_check(hipEventCreate(&e1), "event");
+    auto tk = [&](const std::string& n) { return token(n); };
+    dispatch(l, "embed_gather_bf16", {tk("ids"), tk("model.embed_tokens.weight"), tk("x"), U, H, V});
+    tap_copy(l, "embed.out", tk("x"), T, int(H));
+    for (int i = 0; i < c.layers; ++i) {
+        std::string p = "L" + std::to_string(i) + ".";
+        auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
+        dispatch(l, "rmsnorm_rows", {tk("x"), w(0), tk("h"), U, H, eps});
+        tap_copy(l, p + "input_layernorm.out", tk("h"), T, int(H));
+        l->barrier();
+        dispatch(l, "matmul_bf16w", {tk("h"), w(1), tk("q"), U, QC, H});
+        dispatch(l, "matmul_bf16w", {tk("h"), w(2), tk("k"), U, KC, H});
+        dispatch(l, "matmul_bf16w", {tk("h"), w(3), tk("v"), U, KC, H});
+        tap_copy(l, p + "attn.q_proj.out", tk("q"), T, int(QC));
+        tap_copy(l, p + "attn.k_proj.out", tk("k"), T, int(KC));
+        tap_copy(l, p + "attn.v_proj.out", tk("v"), T, int(KC));
+        l->barrier();
+        dispatch(l, "rmsnorm_rows", {tk("q"), w(5), tk("qn"), U * c.heads, HD, eps});
+        dispatch(l, "rmsnorm_rows", {tk("k"), w(6), tk("kn"), U * c.kv_heads, HD, eps});
+        tap_copy(l, p + "attn.q_norm.out", tk("qn"), T, int(QC));
+        tap_copy(l, p + "attn.k_norm.out", tk("kn"), T, int(KC));
+        l->barrier();
+        dispatch(l, "rope_apply", {tk("qn"), tk("rope.cos"), tk("rope.sin"), tk("qr"), U * c.heads, uint32_t(c.heads), HD, uint32_t(pos0)});
+        dispatch(l, "rope_apply", {tk("kn"), tk("rope.cos"), tk("rope.sin"), tk("kr"), U * c.kv_heads, uint32_t(c.kv_heads), HD, uint32_t(pos0)});
+        tap_copy(l, p + "attn.q_rope", tk("qr"), T, int(QC));
+        tap_copy(l, p + "attn.k_rope", tk("kr"), T, int(KC));
+        l->barrier();
+        dispatch(l, "copy_rows", {tk("kr"), tk(p + "k_cache"), U, KC, 0, uint32_t(pos0), KC, KC});
+        dispatch(l, "copy_rows", {tk("v"), tk(p + "v_cache"), U, KC, 0, uint32_t(pos0), KC, KC});
+        if (c.taps) {
+            TensorRow s = dev_.table().row(tk(p + "v_cache")), d = dev_.table().row(tk("tap." + p + "attn.v_cache"));
+            l->copy(int(s.slot()), s.offset() + uint64_t(pos0) * KC * 4, int(d.slot()), d.offset(), uint64_t(T) * KC * 4);
+        }
+        l->barrier();
+        dispatch(l, "attention_gqa_causal", {tk("qr"), tk(p + "k_cache"), tk(p + "v_cache"), tk("o"), U, 0,
+                                             uint32_t(pos0), uint32_t(c.heads), uint32_t(c.kv_heads), HD, scale});
+        tap_copy(l, p + "attn.o_proj.in", tk("o"), T, int(QC));
+        l->barrier();
+        dispatch(l, "matmul_bf16w", {tk("o"), w(4), tk("oo"), U, H, QC});
+        tap_copy(l, p + "attn.o_proj.out", tk("oo"), T, int(H));
+        l->barrier();
+        dispatch(l, "add", {tk("x"), tk("oo"), tk("r"), U * H});
+        tap_copy(l, p + "resid_mid", tk("r"), T, int(H));
+        l->barrier();
+        dispatch(l, "rmsnorm_rows", {tk("r"), w(7), tk("h2"), U, H, eps});
+        tap_copy(l, p + "post_attention_layernorm.out", tk("h2"), T, int(H));
+        l->barrier();
+        dispatch(l, "matmul_bf16w", {tk("h2"), w(8), tk("g"), U, I, H});
+        dispatch(l, "matmul_bf16w", {tk("h2"), w(9), tk("u"), U, I, H});
+        tap_copy(l, p + "mlp.gate.out", tk("g"), T, int(I));
+        tap_copy(l, p + "mlp.up.out", tk("u"), T, int(I));
+        l->barrier();
+        dispatch(l, "silu_mul", {tk("g"), tk("u"), tk("d"), U * I});
+        tap_copy(l, p + "mlp.down.in", tk("d"), T, int(I));
+        l->barrier();
+        dispatch(l, "matmul_bf16w", {tk("d"), w(10), tk("dd"), U, H, I});
+        tap_copy(l, p + "mlp.down.out", tk("dd"), T, int(H));
+        l->barrier();
+        dispatch(l, "add", {tk("r"), tk("dd"), tk("x"), U * H});
+        tap_copy(l, p + "out", tk("x"), T, int(H));
+        l->barrier();
+    }
+    dispatch(l, "rmsnorm_rows", {tk("x"), tk("model.norm.weight"), tk("f"), U, H, eps});
+    tap_copy(l, "final_norm.out", tk("f"), T, int(H));
+    l->barrier();
+    const uint32_t LR = uint32_t(c.taps ? T : lr);
+    if (LR > dev_.table().row(tk("logits")).count() / V) arg_fail("%u logits rows exceed the logits tensor", LR);
+    dispatch(l, "copy_rows", {tk("f"), tk("f_last"), LR, H, U - LR, 0, H, H});
+    l->barrier();
+    dispatch(l, "matmul_bf16w", {tk("f_last"), tk("model.embed_tokens.weight"), tk("logits"), LR, V, H});
+    if (c.taps) tap_copy(l, "logits", tk("logits"), T, int(V));
+    l->barrier();
+    dispatch(l, "argmax_rows", {tk("logits"), tk("argmax"), LR, V});
+    hip_check(hipEventRecord(e0, dev_.stream()), "event");
+    uint64_t f = dev_.submit(l);
+    hip_check(hipEventRecord(e1, dev_.stream()), "event");
+    dev_.wait(f);
+    dev_.release(l);
+    float ms = 0;
+    hip_check(hipEventElapsedTime(&ms, e0, e1), "event");
+    last_ms_ = ms;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (logits) download_tensor("logits", logits, uint64_t(lr) * V * 4, uint64_t(LR - uint32_t(lr)) * V * 4);
+    uint32_t am = 0;
+    download_tensor("argmax", &am, 4, uint64_t(LR - 1) * 4);
+    return am;
+}
+
+uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr) {
+    (void)seq;
+    const QwenConfig& c = cfg_;
+    const uint32_t H = c.hidden, QC = c.heads * c.head_dim, I = c.intermediate, V = c.vocab, HD = c.head_dim,
+                   MP = c.max_pos, U = uint32_t(T);
+    const uint32_t eps = fbits(c.eps);
+    const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
+    auto tk = [&](const std::string& n) { return token(n); };
+    const uint32_t LC = dev_.table().row(tk("logits")).count() / V;
+    CommandList* l = dev_.begin();
+    dispatch(l, "embed_gather_bf16", {tk("ids"), tk("model.embed_tokens.weight"), tk("x"), U, H, V});
+    for (int i = 0; i < c.layers; ++i) {
+        std::string p = "L" + std::to_string(i) + ".";
+        auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
+        dispatch(l, "rmsnorm_rows_bf16", {tk("x"), w(0), tk("h"), U, H, eps, 0});
+        dispatch(l, "gemm_qkv_rope", {tk("h"), tk("L" + std::to_string(i) + ".qkv_proj"), w(5), w(6), tk("rope.cos"),
+                                      tk("rope.sin"), tk("q"), tk(p + "k_cache"), tk(p + "v_cache"), U, H,
+                                      uint32_t(c.heads), uint32_t(c.kv_heads), uint32_t(pos0), MP, eps});
+        dispatch(l, "attention_prefill_bf16", {tk("q"), tk(p + "k_cache"), tk(p + "v_cache"), tk("o"), U,
+                                               uint32_t(pos0), uint32_t(c.heads), uint32_t(c.kv_heads), MP, scale});
+        dispatch(l, "gemm_residual", {tk("o"), w(4), tk("x"), U, H, QC});
+        dispatch(l, "rmsnorm_rows_bf16", {tk("x"), w(7), tk("h"), U, H, eps, 0});
+        dispatch(l, "gemm_swiglu", {tk("h"), tk("L" + std::to_string(i) + ".gate_up_proj"), tk("a"), U, I, H});
+        dispatch(l, "gemm_residual", {tk("a"), w(10), tk("x"), U, H, I});
+    }
+    // logits of the last lr rows, LC rows per lm_head dispatch
+    hipEvent_t e0, e1;
+    hip_check(hipEventCreate(&e0), "event");
+    hip_check(hipEventCreate(&e1), "event");
+    hip_check(hipEventRecord(e0, dev_.stream()), "event");
+    uint64_t f = dev_.submit(l);
+    dev_.wait(f);
+    dev_.release(l);
+    uint32_t am = 0;
+    for (int r0 = T - lr; r0 < T; r0 += int(LC)) {
+        uint32_t n = uint32_t(std::min(int(LC), T - r0));
+        CommandList* l2 = dev_.begin();
+        dispatch(l2, "rmsnorm_rows_bf16", {tk("x"), tk("model.norm.weight"), tk("h"), n, H, eps, uint32_t(r0)});
+        dispatch(l2, "gemm_f32", {tk("h"), tk("model.embed_tokens.weight"), tk("logits"), n, V, H});
+        dispatch(l2, "argmax_rows", {tk("logits"), tk("argmax"), n, V});
+        uint64_t f2 = dev_.submit(l2);
+        dev_.wait(f2);
+        dev_.release(l2);
+        if (r0 + int(n) == T) {
+            hip_check(hipEventRecord(e1, dev_.stream()), "event");
+            hip_check(hipEventSynchronize(e1), "event");
+        }
+        if (logits) download_tensor("logits", logits + size_t(r0 - (T - lr)) * V, uint64_t(n) * V * 4);
+        download_tensor("argmax", &am, 4, uint64_t(n - 1) * 4);
+    }
+    float ms = 0;
+    hip_check(hipEventElapsedTime(&ms, e0, e1), "event");
+    last_ms_ = ms;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return am;
+}
+
+// ---------------------------------------------------------------- decode (fast mode)
+
+void QwenExec::record_decode_fast() {
+    const QwenConfig& c = cfg_;
+    const uint32_t H = c.hidden, QC = c.heads * c.head_dim, I = c.intermediate, V = c.vocab, HD = c.head_dim,
+                   MP = c.max_pos;
+    const uint32_t eps = fbits(c.eps);
+    const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
+    auto tk = [&](const std::string& n) { return token(n); };
+    CommandList* l = dev_.begin(true);
+    dispatch(l, "embed_dec", {tk("model.embed_tokens.weight"), tk("dec.state"), tk("dec.x"), H, V});
+    for (int i = 0; i < c.layers; ++i) {
+        std::string p = "L" + std::to_string(i) + ".";
+        auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
+        dispatch(l, "gemv_qkv_rope_dec", {tk("dec.x"), w(0), tk("L" + std::to_string(i) + ".qkv_proj"), w(5), w(6),
+                                          tk("rope.cos"), tk("rope.sin"), tk("dec.q"), tk(p + "k_cache"),
+                                          tk(p + "v_cache"), tk("dec.qkv"), tk("dec.counters_qkv"), tk("dec.state"), H,
+                                          uint32_t(c.heads), uint32_t(c.kv_heads), MP, eps});
+        dispatch(l, "attention_decode_bf16", {tk("dec.q"), tk(p + "k_cache"), tk(p + "v_cache"), tk("dec.o"),
+                                              tk("dec.attn_partials"), tk("dec.counters_attn"), tk("dec.state"),
+                                              uint32_t(c.heads), uint32_t(c.kv_heads), MP, scale});
+        dispatch(l, "gemv_residual_dec", {tk("dec.o"), w(4), tk("dec.x"), H, QC});
+        dispatch(l, "gemv_swiglu_dec", {tk("dec.x"), w(7), tk("L" + std::to_string(i) + ".gate_up_proj"), tk("dec.a"),
+                                        I, H, eps});
+        dispatch(l, "gemv_residual_dec", {tk("dec.a"), w(10), tk("dec.x"), H, I});
+    }
+    dispatch(l, "lmhead_argmax_dec", {tk("dec.x"), tk("model.norm.weight"), tk("model.embed_tokens.weight"),
+                                      tk("logits"), tk("dec.lm_partials"), tk("dec.counters_lm"), tk("dec.state"),
+                                      tk("dec.out_ids"), V, H, eps, 1, MP});
+    decode_list_ = l;
+}
+
+void QwenExec::set_decode_state(const int32_t* ids, const int32_t* pos) {
+    if (cfg_.mode != 1) arg_fail("on-device decode needs the fast mode");
+    uint32_t st[4] = {uint32_t(pos[0]), uint32_t(ids[0]), 0, 0};
+    if (pos[0] < 0 || pos[0] >= cfg_.max_pos) arg_fail("decode position %d outside max_pos %d", pos[0], cfg_.max_pos);
+    upload_tensor("dec.state", st, 16);
+}
+
+void QwenExec::run_decode_steps(int steps) {
+    if (cfg_.mode != 1) arg_fail("on-device decode needs the fast mode");
+    if (steps < 1) return;
+    uint32_t st[4];
+    download_tensor("dec.state", st, 16);
+    if (int64_t(st[0]) + steps > cfg_.max_pos) arg_fail("%d decode steps from position %u pass max_pos %d", steps, st[0], cfg_.max_pos);
+    if (!decode_list_) record_decode_fast();
+    hipEvent_t e0, e1;
+    hip_check(hipEventCreate(&e0), "event");
+    hip_check(hipEventCreate(&e1), "event");
+    hip_check(hipEventRecord(e0, dev_.stream()), "event");
+    uint64_t f = dev_.submit(decode_list_, uint32_t(steps));
+    hip_check(hipEventRecord(e1, dev_.stream()), "event");
+    dev_.wait(f);
+    float ms = 0;
+    hip_check(hipEventElapsedTime(&ms, e0, e1), "event");
+    last_ms_ = ms;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+}
+
+void QwenExec::read_decode_ids(int32_t* out, int count) {
+    if (count < 0 || count > cfg_.max_pos) arg_fail("count %d", count);
+    download_tensor("dec.out_ids", out, uint64_t(count) * 4);
+}
+
+void QwenExec::greedy(const int32_t* prompt, int plen, int steps, int32_t* out) {
+    const QwenConfig& c = cfg_;
+    if (plen < 1 || steps < 1) arg_fail("greedy: empty prompt or no steps");
+    if (plen + steps - 1 > c.max_pos) arg_fail("greedy: %d positions exceed max_pos %d", plen + steps - 1, c.max_pos);
+    uint32_t id = forward(0, 0, prompt, plen, nullptr, 1);
+    if (id == 0xFFFFFFFFu) throw std::runtime_error("greedy: argmax of a row that holds a NaN");
+    out[0] = int32_t(id);
+    if (steps == 1) return;
+    if (c.mode == 1) {
+        int32_t pos = plen;
+        int32_t i0 = int32_t(id);
+        set_decode_state(&i0, &pos);
+        uint32_t st[4] = {uint32_t(plen), id, 1, 0};
+        upload_tensor("dec.state", st, 16);
+        run_decode_steps(steps - 1);
+        std::vector<int32_t> ids(static_cast<size_t>(steps));
+        read_decode_ids(ids.data(), steps);
+        for (int s = 1; s < steps; ++s) {
+            if (uint32_t(ids[size_t(s)]) == 0xFFFFFFFFu) throw std::runtime_error("greedy: argmax of a row that holds a NaN");
+            out[s] = ids[size_t(s)];
+        }
+        return;
+    }
+    for (int s = 1; s < steps; ++s) {
+        int32_t cur = out[s - 1];
+        uint32_t nx = forward(0, plen + s - 1, &cur, 1, nullptr, 1);
+        if (nx == 0xFFFFFFFFu) throw std::runtime_error("greedy: argmax of a row that holds a NaN");
+        out[s] = int32_t(nx);
+    }
+}
+
+void QwenExec::decode_batch(const int32_t*, const int32_t*, int, int32_t*) {
+    arg_fail("batched decode is not built yet");
+}
+
+// ---------------------------------------------------------------- taps and caches
+
+int QwenExec::tap_count() const { return int(tap_names_.size()); }
+std::string QwenExec::tap_name(int i) const { return tap_names_.at(size_t(i)); }
+int QwenExec::tap_width(int i) const { return tap_widths_.at(size_t(i)); }
+
+void QwenExec::read_tap(int i, float* out, int rows) {
+    if (i < 0 || i >= tap_count()) arg_fail("tap %d of %d", i, tap_count());
+    if (rows < 0 || rows > cfg_.max_tokens) arg_fail("tap rows %d", rows);
+    download_tensor("tap." + tap_names_[size_t(i)], out, uint64_t(rows) * tap_widths_[size_t(i)] * 4);
+}
+
+static float widen16(uint16_t b) {
+    uint32_t u = uint32_t(b) << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+void QwenExec::read_cache(int seq, int layer, int which, int row0, int rows, float* out) {
+    const QwenConfig& c = cfg_;
+    if (seq != 0 || layer < 0 || layer >= c.layers || row0 < 0 || rows < 0 || row0 + rows > c.max_pos)
+        arg_fail("cache rows out of range");
+    const int KC = c.kv_heads * c.head_dim, HD = c.head_dim, MP = c.max_pos;
+    std::string n = "L" + std::to_string(layer) + (which ? ".v_cache" : ".k_cache");
+    if (c.mode == 0) {
+        download_tensor(n, out, uint64_t(rows) * KC * 4, uint64_t(row0) * KC * 4);
+        return;
+    }
+    std::vector<uint16_t> all(size_t(c.kv_heads) * MP * HD);
+    download_tensor(n, all.data(), all.size() * 2);
+    for (int r = 0; r < rows; ++r)
+        for (int h = 0; h < c.kv_heads; ++h)
+            for (int d = 0; d < HD; ++d) {
+                size_t src = which ? (size_t(h) * HD + d) * MP + row0 + r : (size_t(h) * MP + row0 + r) * HD + d;
+                out[size_t(r) * KC + h * HD + d] = widen16(all[src]);
+            }
+}
+
+void QwenExec::write_cache(int seq, int layer, int which, int row0, int rows, const float* in) {
+    const QwenConfig& c = cfg_;
+    if (seq != 0 || layer < 0 || layer >= c.layers || row0 < 0 || rows < 0 || row0 + rows > c.max_pos)
+        arg_fail("cache rows out of range");
+    const int KC = c.kv_heads * c.head_dim, HD = c.head_dim, MP = c.max_pos;
+    std::string n = "L" + std::to_string(layer) + (which ? ".v_cache" : ".k_cache");
+    if (c.mode == 0) {
+        upload_tensor(n, in, uint64_t(rows) * KC * 4, uint64_t(row0) * KC * 4);
+        return;
+    }
+    std::vector<uint16_t> all(size_t(c.kv_heads) * MP * HD);
+    download_tensor(n, all.data(), all.size() * 2);
+    for (int r = 0; r < rows; ++r)
+        for (int h = 0; h < c.kv_heads; ++h)
+            for (int d = 0; d < HD; ++d) {
+                size_t dst = which ? (size_t(h) * HD + d) * MP + row0 + r : (size_t(h) * MP + row0 + r) * HD + d;
+                all[dst] = narrow_rne(in[size_t(r) * KC + h * HD + d]);
+            }
+    upload_tensor(n, all.data(), all.size() * 2);
+}
+
+void QwenExec::fill_cache_random(uint64_t seed, int rows) {
+    const QwenConfig& c = cfg_;
+    if (c.mode != 1) arg_fail("fill_cache_random needs the bf16 cache of the fast mode");
+    if (rows < 0 || rows > c.max_pos) arg_fail("rows %d", rows);
+    // Whole caches are filled (positions past `rows` are never read before they are written).
+    CommandList* l = dev_.begin();
+    float one = 1.0f;
+    for (int i = 0; i < c.layers; ++i)
+        for (int which = 0; which < 2; ++which) {
+            std::string n = "L" + std::to_string(i) + (which ? ".v_cache" : ".k_cache");
+            uint32_t cnt = dev_.table().row(token(n)).count();
+            uint64_t st = stream_of(n.c_str());
+            dispatch(l, "fill_normal_bf16", {token(n), cnt, uint32_t(seed), uint32_t(seed >> 32), uint32_t(st),
+                                             uint32_t(st >> 32), fbits(one)});
+        }
+    dev_.wait(dev_.submit(l));
+    dev_.release(l);
+}
+
+}  // namespace lrm
