@@ -1,0 +1,229 @@
+"""Benchmark of the Qwen3 forward hot path on one MI355X, printing one JSON line.
+
+Headline (value): batch-1 greedy decode tok/s of a Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads,
+head_dim 128, SwiGLU 3072, vocab 151936, tied embeddings, random N(0, 0.02) bf16 weights, norm weights 1): a 128-token
+prompt, then W warmup steps and exactly K timed decode steps (one step = one token: the recorded decode step replayed
+as a HIP graph, position and token in device memory). Defaults K = 256, W = 8: context 136 .. 392.
+
+Also measured in the same run (extra keys): 512-token prefill with all 512 x 151936 logits, 2048-token prefill with
+last-row logits, decode at 4096 context, the isolated GQA prefill attention at T = 2048, the roofline of the dominant
+decode kernel (the fused gate/up SwiGLU GEMV, timed with HIP events on the device stream), and the oracle timed on the
+host cores on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+FP32_PEAK_TFLOPS = 157.3
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0 or 128 + args.warmup + args.steps > 4096:
+        print("steps + warmup must keep the context within 4096", file=sys.stderr)
+        sys.exit(2)
+
+    from oracle import cpuref
+    from rosylnalive_amd.gpu_core import ArgBlock, HipBackend
+    from rosylnalive_amd.qwen import QwenConfig, QwenModel, inv_freq_bits, synthetic_ids, synthetic_weights
+
+    cfg = QwenConfig.qwen3_0_6b(max_pos=4096 + 256)
+    L, H, QH, KVH, HD, I, V = cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.intermediate, cfg.vocab
+    weight_bytes = cfg.param_count() * 2
+    lin_params_layer = (QH * HD + 2 * KVH * HD) * H + H * QH * HD + 2 * I * H + H * I
+
+    t0 = time.time()
+    weights = synthetic_weights(cfg, seed=args.seed)
+    log(f"weights generated in {time.time() - t0:.1f} s ({weight_bytes / 1e9:.3f} GB bf16)")
+    backend = HipBackend(0)
+    model = QwenModel(backend, cfg, mode="fast", max_tokens=2048)
+    model.load_weights(weights)
+    log(f"model resident after {time.time() - t0:.1f} s on {backend.info.name} ({backend.info.arch})")
+
+    def kv_bytes(ctx):
+        return 2 * L * KVH * ctx * HD * 2
+
+    # ---------------------------------------------------------------- headline: decode, context 128 + ...
+    prompt = synthetic_ids(args.seed, "bench/prompt", 128, V)
+    _, first = model.forward(prompt, 0, logits_rows=1)
+    model.decode_set(int(first), 128)
+    if args.warmup:
+        model.decode_run(args.warmup)
+    ctx0 = 128 + args.warmup
+    t1 = time.perf_counter()
+    model.decode_run(args.steps)
+    wall = time.perf_counter() - t1
+    dev_ms = model.last_ms()
+    tok_s = args.steps / (dev_ms / 1e3)
+    step_bytes = sum(weight_bytes + kv_bytes(ctx0 + s + 1) for s in range(args.steps))
+    log(f"decode: {args.steps} steps in {dev_ms:.2f} ms device ({wall * 1e3:.2f} ms wall): {tok_s:.1f} tok/s, "
+        f"{step_bytes / (dev_ms / 1e3) / 1e9:.0f} GB/s algorithmic")
+
+    # ---------------------------------------------------------------- dominant kernel roofline (gate/up SwiGLU GEMV)
+    tok = model.token
+    reps = 4
+    cl = backend.begin()
+    tm = cl.begin_timer("gpu.gemv_swiglu_dec")
+    for _ in range(reps):
+        for i in range(L):
+            cl.dispatch("gemv_swiglu_dec", ArgBlock.encode(
+                "gemv_swiglu_dec", x=tok("dec.x"), norm=tok(f"model.layers.{i}.post_attention_layernorm.weight"),
+                w=tok(f"L{i}.gate_up_proj"), y=tok("dec.a"), inter=I, hidden=H, eps=cfg.eps))
+    cl.end_timer(tm)
+    comp = backend.wait(backend.submit(cl))
+    cl.release()
+    launches = reps * L
+    k_us = comp.timers[0].duration_ns / 1e3 / launches
+    k_bytes = 2 * I * H * 2 + H * 4 + H * 2 + I * 4
+    k_gbs = k_bytes / (k_us * 1e-6) / 1e9
+    log(f"gemv_swiglu_dec: {k_us:.2f} us per launch, {k_gbs:.0f} GB/s ({k_gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+
+    out = {
+        "metric": "Qwen3-0.6B prefill & decode tok/s on 1 MI355X; % of HBM/MFMA roofline",
+        "value": round(tok_s, 2),
+        "unit": "tok/s (batch-1 greedy decode)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dev_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random N(0,0.02) bf16 weights, norm weights 1, uniform token ids; seed %d)" % args.seed,
+        "config": {
+            "workload": "Qwen3-0.6B-shaped greedy decode with KV cache, batch 1, prompt 128, then %d warmup + %d timed "
+                        "tokens (context %d..%d)" % (args.warmup, args.steps, ctx0 + 1, ctx0 + args.steps),
+            "layers": L, "hidden": H, "heads": f"{QH}/{KVH}", "head_dim": HD, "intermediate": I, "vocab": V,
+            "batch": 1,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_swiglu_dec",
+            "achieved": round(k_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(k_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": k_bytes,
+            "us_per_launch": round(k_us, 3),
+        },
+        "decode_step_roofline": {
+            "bound": "hbm",
+            "achieved": round(step_bytes / (dev_ms / 1e3) / 1e9, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(step_bytes / (dev_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_token": int(step_bytes / args.steps),
+        },
+    }
+
+    if not args.no_extras:
+        # 512-token prefill with every logit row (all 512 x 151936 logits)
+        ids = synthetic_ids(args.seed, "bench/prefill512", 512, V)
+        model.forward(ids, 0, logits_rows=512)
+        best = min((model.forward(ids, 0, logits_rows=512), model.last_ms())[1] for _ in range(3))
+        fl = 2 * 512 * L * lin_params_layer + 2 * 512 * V * H + L * QH * (512 * 513 // 2) * (4 * HD + 3)
+        out["prefill_512_all_logits"] = {"ms": round(best, 3), "tok_s": round(512 / (best / 1e3), 1),
+                                         "tflops": round(fl / (best / 1e3) / 1e12, 1),
+                                         "mfma_frac": round(fl / (best / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                         "flop": fl}
+        log("prefill 512:", out["prefill_512_all_logits"])
+        # 2048-token prefill, last-row logits
+        ids = synthetic_ids(args.seed, "bench/prefill2048", 2048, V)
+        model.forward(ids, 0, logits_rows=1)
+        best = min((model.forward(ids, 0, logits_rows=1), model.last_ms())[1] for _ in range(3))
+        fl = 2 * 2048 * L * lin_params_layer + 2 * V * H + L * QH * (2048 * 2049 // 2) * (4 * HD + 3)
+        out["prefill_2048"] = {"ms": round(best, 3), "tok_s": round(2048 / (best / 1e3), 1),
+                               "tflops": round(fl / (best / 1e3) / 1e12, 1),
+                               "mfma_frac": round(fl / (best / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flop": fl}
+        log("prefill 2048:", out["prefill_2048"])
+        # the isolated GQA prefill attention at T = 2048 on the caches the prefill just wrote (layer 0)
+        cl = backend.begin()
+        tm = cl.begin_timer("gpu.attention_prefill_f16")
+        for i in range(L):
+            cl.dispatch("attention_prefill_f16", ArgBlock.encode(
+                "attention_prefill_f16", q=tok("q"), k_cache=tok(f"L{i}.k_cache"), v_cache=tok(f"L{i}.v_cache"),
+                y=tok("o"), rows=2048, past=0, q_heads=QH, kv_heads=KVH, max_pos=cfg.max_pos,
+                scale=float(np.float32(HD ** -0.5))))
+        cl.end_timer(tm)
+        comp = backend.wait(backend.submit(cl))
+        cl.release()
+        a_us = comp.timers[0].duration_ns / 1e3 / L
+        a_fl = QH * (2048 * 2049 // 2) * (4 * HD + 3)
+        out["attention_prefill_2048"] = {"us": round(a_us, 2), "tflops": round(a_fl / (a_us * 1e-6) / 1e12, 1),
+                                         "mfma_frac": round(a_fl / (a_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                         "flop": a_fl}
+        log("attention 2048:", out["attention_prefill_2048"])
+        # decode at 4096 context: a real 4096-token prefill (two chunks), then 64 decode steps
+        ids = synthetic_ids(args.seed, "bench/ctx4k", 4096, V)
+        _, nxt = model.forward(ids, 0, logits_rows=1)
+        model.decode_set(int(nxt), 4096)
+        model.decode_run(4)
+        model.decode_run(64)
+        d_ms = model.last_ms()
+        b4 = sum(weight_bytes + kv_bytes(4096 + 4 + s + 1) for s in range(64))
+        out["decode_4k"] = {"tok_s": round(64 / (d_ms / 1e3), 1), "ms_per_token": round(d_ms / 64, 4),
+                            "gbs": round(b4 / (d_ms / 1e3) / 1e9, 1),
+                            "hbm_frac": round(b4 / (d_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                            "bytes_per_token": int(b4 / 64)}
+        log("decode 4k:", out["decode_4k"])
+
+    if not args.no_cpu:
+        # the oracle (CpuRef F32 restated in C) on the host's cores: prefill of the same 128-token prompt, then 2
+        # decode steps; decode tok/s reported from the decode steps.
+        threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+        cpuref.set_threads(threads)
+        cos, sin = cpuref.rope_table(inv_freq_bits(HD), 256)
+        ocfg = cfg.oracle_dict()
+        ocfg["max_pos"] = 256
+        orc = cpuref.QwenOracle(ocfg, weights, cos, sin)
+        cache = orc.new_cache()
+        t2 = time.perf_counter()
+        lg = orc.forward(cache, 0, prompt)
+        t_pre = time.perf_counter() - t2
+        nxt = int(np.argmax(lg[-1]))
+        t3 = time.perf_counter()
+        steps = 2
+        for s in range(steps):
+            lg = orc.forward(cache, 128 + s, np.array([nxt], np.int32))
+            nxt = int(np.argmax(lg[-1]))
+        t_dec = time.perf_counter() - t3
+        out["cpu_baseline"] = {"value": round(steps / t_dec, 4), "unit": "tok/s (batch-1 decode)", "cores": threads,
+                               "kind": "port",
+                               "sample": f"oracle (CpuRef F32 in C) on the same weights: 128-token prefill "
+                                         f"({t_pre:.2f} s, {128 / t_pre:.1f} tok/s) then {steps} decode steps "
+                                         f"({t_dec:.2f} s)"}
+        log("cpu baseline:", out["cpu_baseline"])
+
+    model.close()
+    backend.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

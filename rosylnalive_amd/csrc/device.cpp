@@ -5,6 +5,7 @@
 #include <dlfcn.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <iterator>
@@ -326,6 +327,15 @@ void Device::release(CommandList* l) {
         }
 }
 
+// Reusable lists replay as HIP graphs unless LRM_HIP_GRAPHS=0 (for tools that cannot trace stream capture).
+bool Device::graphs_enabled() {
+    static const bool on = [] {
+        const char* v = std::getenv("LRM_HIP_GRAPHS");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
 void Device::run(CommandList* l) {
     for (auto& c : l->cmds_) {
         if (c.kind == CommandList::Cmd::Launch) {
@@ -392,6 +402,11 @@ uint64_t Device::submit(CommandList* l, uint32_t repeat) {
         pend.timer_names = names;
         l->closed_ = true;
         pend.owned = l;
+    } else if (!graphs_enabled()) {
+        // Profilers that cannot follow stream capture: replay by launching the recorded commands directly.
+        if (!l->timer_names_.empty()) contract_fail("a reusable list cannot hold timers");
+        for (uint32_t r = 0; r < repeat; ++r) run(l);
+        HIPC(hipGetLastError());
     } else {
         if (!l->timer_names_.empty()) contract_fail("a reusable list cannot hold timers");
         if (!l->exec_) {

@@ -130,7 +130,7 @@ class Device {
     CommandList* begin(bool reusable = false);
     uint64_t submit(CommandList* list, uint32_t repeat = 1);
     const Completion& wait(uint64_t fence);
-    void release(CommandList* list);  // frees a list (one-shot lists are released by wait of their fence)
+    void release(CommandList* list);  // frees a list; the caller releases every list it began
 
     hipStream_t stream() const { return stream_; }
     void* slot_ptr(int slot) const;
@@ -139,6 +139,7 @@ class Device {
   private:
     friend class CommandList;
     void run(CommandList* l);
+    static bool graphs_enabled();
     void run_probe();
     DeviceInfo info_{};
     int index_;

@@ -179,10 +179,10 @@ QwenExec::QwenExec(Device& dev, const QwenConfig& cfg, const uint32_t* inv_freq_
     if (c.head_dim % 2) arg_fail("head_dim must be even");
     if (c.mode == 1) {
         if (c.head_dim != 128 || c.heads != 2 * c.kv_heads)
-            arg_fail("the bf16 fast path takes head_dim 128 and two query heads per KV head");
-        if (c.hidden % 512 || c.intermediate % 64 || c.hidden > 8192)
-            arg_fail("the bf16 fast path takes hidden a multiple of 512 (<= 8192) and intermediate a multiple of 64");
-        if (c.max_pos % 64) arg_fail("the bf16 fast path takes max_pos a multiple of 64");
+            arg_fail("the fast path takes head_dim 128 and two query heads per KV head");
+        if (c.hidden % 64 || c.intermediate % 64 || c.hidden > 8192 || c.intermediate > 8192 || c.heads * 128 > 8192)
+            arg_fail("the fast path takes hidden and intermediate multiples of 64 up to 8192, and heads * 128 <= 8192");
+        if (c.max_pos % 64) arg_fail("the fast path takes max_pos a multiple of 64");
         if (c.batch != 1) arg_fail("batched decode is not built yet: batch must be 1");
     }
     if (!dev_.kernels_loaded()) dev_.load_kernels();
@@ -223,13 +223,28 @@ void QwenExec::plan() {
         }
         add(lname(i, kLayerWeights[10]), Weights, BF16, {H, I}, ReadOnly);
     }
+    if (fast) {
+        // exact fp16 copies of the matrices for the prefill MFMA GEMMs, written on device from the bf16 originals
+        auto copy16 = [&](const std::string& of, const std::string& name, std::vector<uint32_t> dims) {
+            add(name, Weights, F16, std::move(dims));
+            f16_copy_[of] = name;
+        };
+        copy16("model.embed_tokens.weight", "embed.f16", {V, H});
+        for (int i = 0; i < c.layers; ++i) {
+            std::string p = "L" + std::to_string(i);
+            copy16(p + ".qkv_proj", p + ".qkv_proj.f16", {QC + 2 * KC, H});
+            copy16(lname(i, kLayerWeights[4]), p + ".o_proj.f16", {H, QC});
+            copy16(p + ".gate_up_proj", p + ".gate_up_proj.f16", {2 * I, H});
+            copy16(lname(i, kLayerWeights[10]), p + ".down_proj.f16", {H, I});
+        }
+    }
     add("rope.cos", Rope, F32, {MP, HD / 2}, ReadOnly);
     add("rope.sin", Rope, F32, {MP, HD / 2}, ReadOnly);
     for (int i = 0; i < c.layers; ++i) {
         std::string p = "L" + std::to_string(i);
         if (fast) {
-            add(p + ".k_cache", KvCache, BF16, {uint32_t(c.kv_heads), MP, HD});
-            add(p + ".v_cache", KvCache, BF16, {uint32_t(c.kv_heads), HD, MP});
+            add(p + ".k_cache", KvCache, F16, {uint32_t(c.kv_heads), MP, HD});
+            add(p + ".v_cache", KvCache, F16, {uint32_t(c.kv_heads), HD, MP});
         } else {
             add(p + ".k_cache", KvCache, F32, {MP, KC});
             add(p + ".v_cache", KvCache, F32, {MP, KC});
@@ -239,20 +254,16 @@ void QwenExec::plan() {
     add("x", Activations, F32, {MT, H});
     const uint32_t LC = std::min<uint32_t>(MT, 512);  // logits rows per lm_head dispatch (K2-0001's row cap, raised)
     if (fast) {
-        add("h", Activations, BF16, {MT, H});
-        add("q", Activations, BF16, {MT, QC});
-        add("o", Activations, BF16, {MT, QC});
-        add("a", Activations, BF16, {MT, I});
+        add("h", Activations, F16, {MT, H});
+        add("q", Activations, F16, {MT, QC});
+        add("o", Activations, F16, {MT, QC});
+        add("a", Activations, F16, {MT, I});
         add("dec.x", Activations, F32, {H});
-        add("dec.q", Activations, F32, {QC});
         add("dec.o", Activations, F32, {QC});
         add("dec.a", Activations, F32, {I});
         add("dec.qkv", Scratch, F32, {QC + 2 * KC});
         add("dec.attn_partials", Scratch, F32, {uint32_t(c.heads) * (MP / 64) * 130});
         add("dec.lm_partials", Scratch, F32, {2 * 1024});
-        add("dec.counters_qkv", Scratch, U32, {uint32_t(c.heads + 2 * c.kv_heads)});
-        add("dec.counters_attn", Scratch, U32, {uint32_t(c.kv_heads)});
-        add("dec.counters_lm", Scratch, U32, {4});
         add("dec.state", Scratch, U32, {4});
         add("dec.out_ids", Logits, U32, {MP});
     } else {
@@ -335,7 +346,30 @@ void QwenExec::set_weight(const std::string& name, const uint16_t* data, uint64_
     uint64_t n = 1;
     for (uint32_t d : tt.dims) n *= d;
     if (tt.dtype != BF16 || n != elems) arg_fail("weight %s holds %llu bf16 elements, not %llu", name.c_str(), (unsigned long long)n, (unsigned long long)elems);
+    const std::string& base = tt.view_of.empty() ? name : tt.view_of;
+    if (f16_copy_.count(base)) {
+        // the fp16 copy must hold the same values: |w| >= 65536 has no fp16 counterpart
+        for (uint64_t i = 0; i < elems; ++i) {
+            uint16_t a = data[i] & 0x7FFFu;
+            if (a >= 0x4780u && a < 0x7F80u)
+                arg_fail("weight %s element %llu (bf16 %04x) is outside the fp16 range the fast path computes in",
+                         name.c_str(), (unsigned long long)i, data[i]);
+        }
+        f16_dirty_.insert(base);
+    }
     upload_tensor(name, data, elems * 2);
+}
+
+void QwenExec::sync_f16() {
+    if (f16_dirty_.empty()) return;
+    CommandList* l = dev_.begin();
+    for (const std::string& base : f16_dirty_) {
+        uint32_t n = dev_.table().row(token(base)).count();
+        dispatch(l, "convert_bf16_f16", {token(base), token(f16_copy_.at(base)), n});
+    }
+    dev_.wait(dev_.submit(l));
+    dev_.release(l);
+    f16_dirty_.clear();
 }
 
 void QwenExec::read_weight(const std::string& name, uint16_t* out, uint64_t elems) {
@@ -378,7 +412,8 @@ uint32_t QwenExec::forward(int seq, int pos0, const int32_t* ids, int t_, float*
         std::vector<uint32_t> u(static_cast<size_t>(n));
         for (int i = 0; i < n; ++i) u[size_t(i)] = uint32_t(ids[c0 + i]);
         upload_tensor("ids", u.data(), uint64_t(n) * 4);
-        float* lg = logits ? logits + size_t(logits_rows - want) * c.vocab : nullptr;
+        // only the chunks holding some of the last logits_rows rows write into the caller's buffer
+        float* lg = (logits && want > 0) ? logits + size_t(logits_rows - want) * c.vocab : nullptr;
         if (c.mode == 1)
             am = forward_fast(seq, pos0 + c0, n, lg, std::max(want, 1));
         else
@@ -475,6 +510,7 @@ uint32_t QwenExec::forward_fp32(int pos0, int T, float* logits, int lr) {
     hip_check(hipEventRecord(e1, dev_.stream()), "event");
     dev_.wait(f);
     dev_.release(l);
+    hip_check(hipEventSynchronize(e1), "event");
     float ms = 0;
     hip_check(hipEventElapsedTime(&ms, e0, e1), "event");
     last_ms_ = ms;
@@ -495,21 +531,22 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
     const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
     auto tk = [&](const std::string& n) { return token(n); };
     const uint32_t LC = dev_.table().row(tk("logits")).count() / V;
+    sync_f16();
     CommandList* l = dev_.begin();
     dispatch(l, "embed_gather_bf16", {tk("ids"), tk("model.embed_tokens.weight"), tk("x"), U, H, V});
     for (int i = 0; i < c.layers; ++i) {
-        std::string p = "L" + std::to_string(i) + ".";
+        const std::string p = "L" + std::to_string(i) + ".";
         auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
-        dispatch(l, "rmsnorm_rows_bf16", {tk("x"), w(0), tk("h"), U, H, eps, 0});
-        dispatch(l, "gemm_qkv_rope", {tk("h"), tk("L" + std::to_string(i) + ".qkv_proj"), w(5), w(6), tk("rope.cos"),
-                                      tk("rope.sin"), tk("q"), tk(p + "k_cache"), tk(p + "v_cache"), U, H,
-                                      uint32_t(c.heads), uint32_t(c.kv_heads), uint32_t(pos0), MP, eps});
-        dispatch(l, "attention_prefill_bf16", {tk("q"), tk(p + "k_cache"), tk(p + "v_cache"), tk("o"), U,
-                                               uint32_t(pos0), uint32_t(c.heads), uint32_t(c.kv_heads), MP, scale});
-        dispatch(l, "gemm_residual", {tk("o"), w(4), tk("x"), U, H, QC});
-        dispatch(l, "rmsnorm_rows_bf16", {tk("x"), w(7), tk("h"), U, H, eps, 0});
-        dispatch(l, "gemm_swiglu", {tk("h"), tk("L" + std::to_string(i) + ".gate_up_proj"), tk("a"), U, I, H});
-        dispatch(l, "gemm_residual", {tk("a"), w(10), tk("x"), U, H, I});
+        dispatch(l, "rmsnorm_rows_f16", {tk("x"), w(0), tk("h"), U, H, eps, 0});
+        dispatch(l, "gemm_qkv_rope", {tk("h"), tk(p + "qkv_proj.f16"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
+                                      tk("q"), tk(p + "k_cache"), tk(p + "v_cache"), U, H, uint32_t(c.heads),
+                                      uint32_t(c.kv_heads), uint32_t(pos0), MP, eps});
+        dispatch(l, "attention_prefill_f16", {tk("q"), tk(p + "k_cache"), tk(p + "v_cache"), tk("o"), U,
+                                              uint32_t(pos0), uint32_t(c.heads), uint32_t(c.kv_heads), MP, scale});
+        dispatch(l, "gemm_residual", {tk("o"), tk(p + "o_proj.f16"), tk("x"), U, H, QC});
+        dispatch(l, "rmsnorm_rows_f16", {tk("x"), w(7), tk("h"), U, H, eps, 0});
+        dispatch(l, "gemm_swiglu", {tk("h"), tk(p + "gate_up_proj.f16"), tk("a"), U, I, H});
+        dispatch(l, "gemm_residual", {tk("a"), tk(p + "down_proj.f16"), tk("x"), U, H, I});
     }
     // logits of the last lr rows, LC rows per lm_head dispatch
     hipEvent_t e0, e1;
@@ -521,10 +558,10 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
     dev_.release(l);
     uint32_t am = 0;
     for (int r0 = T - lr; r0 < T; r0 += int(LC)) {
-        uint32_t n = uint32_t(std::min(int(LC), T - r0));
+        const uint32_t n = uint32_t(std::min(int(LC), T - r0));
         CommandList* l2 = dev_.begin();
-        dispatch(l2, "rmsnorm_rows_bf16", {tk("x"), tk("model.norm.weight"), tk("h"), n, H, eps, uint32_t(r0)});
-        dispatch(l2, "gemm_f32", {tk("h"), tk("model.embed_tokens.weight"), tk("logits"), n, V, H});
+        dispatch(l2, "rmsnorm_rows_f16", {tk("x"), tk("model.norm.weight"), tk("h"), n, H, eps, uint32_t(r0)});
+        dispatch(l2, "gemm_f32", {tk("h"), tk("embed.f16"), tk("logits"), n, V, H});
         dispatch(l2, "argmax_rows", {tk("logits"), tk("argmax"), n, V});
         uint64_t f2 = dev_.submit(l2);
         dev_.wait(f2);
@@ -545,34 +582,34 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
 }
 
 // ---------------------------------------------------------------- decode (fast mode)
+// One step: embed the fed-back token; per layer the fused q|k|v GEMV on RMSNorm(x), split-KV attention (q/k norm,
+// RoPE and the cache append inside), the split combine, o_proj + residual, the SwiGLU GEMV pair on RMSNorm(x), down +
+// residual; then the lm_head partial argmaxes and the final argmax, which advances the on-device state.
 
 void QwenExec::record_decode_fast() {
     const QwenConfig& c = cfg_;
-    const uint32_t H = c.hidden, QC = c.heads * c.head_dim, I = c.intermediate, V = c.vocab, HD = c.head_dim,
-                   MP = c.max_pos;
+    const uint32_t H = c.hidden, QC = c.heads * c.head_dim, KC = c.kv_heads * c.head_dim, I = c.intermediate,
+                   V = c.vocab, HD = c.head_dim, MP = c.max_pos;
     const uint32_t eps = fbits(c.eps);
     const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
     auto tk = [&](const std::string& n) { return token(n); };
     CommandList* l = dev_.begin(true);
     dispatch(l, "embed_dec", {tk("model.embed_tokens.weight"), tk("dec.state"), tk("dec.x"), H, V});
     for (int i = 0; i < c.layers; ++i) {
-        std::string p = "L" + std::to_string(i) + ".";
+        const std::string p = "L" + std::to_string(i) + ".";
         auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
-        dispatch(l, "gemv_qkv_rope_dec", {tk("dec.x"), w(0), tk("L" + std::to_string(i) + ".qkv_proj"), w(5), w(6),
-                                          tk("rope.cos"), tk("rope.sin"), tk("dec.q"), tk(p + "k_cache"),
-                                          tk(p + "v_cache"), tk("dec.qkv"), tk("dec.counters_qkv"), tk("dec.state"), H,
-                                          uint32_t(c.heads), uint32_t(c.kv_heads), MP, eps});
-        dispatch(l, "attention_decode_bf16", {tk("dec.q"), tk(p + "k_cache"), tk(p + "v_cache"), tk("dec.o"),
-                                              tk("dec.attn_partials"), tk("dec.counters_attn"), tk("dec.state"),
-                                              uint32_t(c.heads), uint32_t(c.kv_heads), MP, scale});
+        dispatch(l, "gemv_norm_dec", {tk("dec.x"), w(0), tk(p + "qkv_proj"), tk("dec.qkv"), QC + 2 * KC, H, eps});
+        dispatch(l, "attention_decode_f16", {tk("dec.qkv"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
+                                             tk(p + "k_cache"), tk(p + "v_cache"), tk("dec.attn_partials"),
+                                             tk("dec.state"), uint32_t(c.heads), uint32_t(c.kv_heads), MP, eps, scale});
+        dispatch(l, "attention_combine", {tk("dec.attn_partials"), tk("dec.o"), tk("dec.state"), uint32_t(c.heads), MP});
         dispatch(l, "gemv_residual_dec", {tk("dec.o"), w(4), tk("dec.x"), H, QC});
-        dispatch(l, "gemv_swiglu_dec", {tk("dec.x"), w(7), tk("L" + std::to_string(i) + ".gate_up_proj"), tk("dec.a"),
-                                        I, H, eps});
+        dispatch(l, "gemv_swiglu_dec", {tk("dec.x"), w(7), tk(p + "gate_up_proj"), tk("dec.a"), I, H, eps});
         dispatch(l, "gemv_residual_dec", {tk("dec.a"), w(10), tk("dec.x"), H, I});
     }
-    dispatch(l, "lmhead_argmax_dec", {tk("dec.x"), tk("model.norm.weight"), tk("model.embed_tokens.weight"),
-                                      tk("logits"), tk("dec.lm_partials"), tk("dec.counters_lm"), tk("dec.state"),
-                                      tk("dec.out_ids"), V, H, eps, 1, MP});
+    dispatch(l, "lmhead_dec", {tk("dec.x"), tk("model.norm.weight"), tk("model.embed_tokens.weight"), tk("logits"),
+                               tk("dec.lm_partials"), V, H, eps, 1});
+    dispatch(l, "argmax_dec", {tk("dec.lm_partials"), tk("dec.state"), tk("dec.out_ids"), MP});
     decode_list_ = l;
 }
 
@@ -597,6 +634,7 @@ void QwenExec::run_decode_steps(int steps) {
     uint64_t f = dev_.submit(decode_list_, uint32_t(steps));
     hip_check(hipEventRecord(e1, dev_.stream()), "event");
     dev_.wait(f);
+    hip_check(hipEventSynchronize(e1), "event");
     float ms = 0;
     hip_check(hipEventElapsedTime(&ms, e0, e1), "event");
     last_ms_ = ms;
@@ -656,11 +694,42 @@ void QwenExec::read_tap(int i, float* out, int rows) {
     download_tensor("tap." + tap_names_[size_t(i)], out, uint64_t(rows) * tap_widths_[size_t(i)] * 4);
 }
 
-static float widen16(uint16_t b) {
-    uint32_t u = uint32_t(b) << 16;
+// IEEE binary16 <-> binary32 on the host (round to nearest even), for the fp16 caches of the fast mode.
+static float half_to_float(uint16_t h) {
+    const uint32_t sign = uint32_t(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    uint32_t u;
+    if (e == 0x1F) {
+        u = sign | 0x7F800000u | (m << 13);
+    } else if (e == 0) {
+        u = sign | fbits(float(m) * 0x1p-24f);  // zero or a subnormal: m * 2^-24 is exact in binary32
+    } else {
+        u = sign | ((e + 112u) << 23) | (m << 13);
+    }
     float f;
     std::memcpy(&f, &u, 4);
     return f;
+}
+
+static uint16_t float_to_half(float f) {
+    const uint32_t u = fbits(f), sign = (u >> 16) & 0x8000u, a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return uint16_t(sign | 0x7E00u);  // NaN
+    if (a >= 0x477FF000u) return uint16_t(sign | 0x7C00u);  // at or past 65520, the midpoint to infinity
+    if (a <= 0x33000000u) return uint16_t(sign);            // at or below 2^-25, the midpoint to the least subnormal
+    const int e = int(a >> 23) - 127;
+    const uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
+    uint32_t q, rem, half;
+    if (e < -14) {  // subnormal result: units of 2^-24
+        const int sh = -1 - e;  // 14 .. 24
+        q = m >> sh;
+        rem = m & ((1u << sh) - 1);
+        half = 1u << (sh - 1);
+    } else {
+        q = (uint32_t(e + 15) << 10) | ((m >> 13) & 0x3FFu);
+        rem = m & 0x1FFFu;
+        half = 0x1000u;
+    }
+    if (rem > half || (rem == half && (q & 1u))) ++q;  // a carry into the exponent field is the right result
+    return uint16_t(sign | q);
 }
 
 void QwenExec::read_cache(int seq, int layer, int which, int row0, int rows, float* out) {
@@ -679,7 +748,7 @@ void QwenExec::read_cache(int seq, int layer, int which, int row0, int rows, flo
         for (int h = 0; h < c.kv_heads; ++h)
             for (int d = 0; d < HD; ++d) {
                 size_t src = which ? (size_t(h) * HD + d) * MP + row0 + r : (size_t(h) * MP + row0 + r) * HD + d;
-                out[size_t(r) * KC + h * HD + d] = widen16(all[src]);
+                out[size_t(r) * KC + h * HD + d] = half_to_float(all[src]);
             }
 }
 
@@ -699,14 +768,14 @@ void QwenExec::write_cache(int seq, int layer, int which, int row0, int rows, co
         for (int h = 0; h < c.kv_heads; ++h)
             for (int d = 0; d < HD; ++d) {
                 size_t dst = which ? (size_t(h) * HD + d) * MP + row0 + r : (size_t(h) * MP + row0 + r) * HD + d;
-                all[dst] = narrow_rne(in[size_t(r) * KC + h * HD + d]);
+                all[dst] = float_to_half(in[size_t(r) * KC + h * HD + d]);
             }
     upload_tensor(n, all.data(), all.size() * 2);
 }
 
 void QwenExec::fill_cache_random(uint64_t seed, int rows) {
     const QwenConfig& c = cfg_;
-    if (c.mode != 1) arg_fail("fill_cache_random needs the bf16 cache of the fast mode");
+    if (c.mode != 1) arg_fail("fill_cache_random needs the fp16 cache of the fast mode");
     if (rows < 0 || rows > c.max_pos) arg_fail("rows %d", rows);
     // Whole caches are filled (positions past `rows` are never read before they are written).
     CommandList* l = dev_.begin();
@@ -716,7 +785,7 @@ void QwenExec::fill_cache_random(uint64_t seed, int rows) {
             std::string n = "L" + std::to_string(i) + (which ? ".v_cache" : ".k_cache");
             uint32_t cnt = dev_.table().row(token(n)).count();
             uint64_t st = stream_of(n.c_str());
-            dispatch(l, "fill_normal_bf16", {token(n), cnt, uint32_t(seed), uint32_t(seed >> 32), uint32_t(st),
+            dispatch(l, "fill_normal_f16", {token(n), cnt, uint32_t(seed), uint32_t(seed >> 32), uint32_t(st),
                                              uint32_t(st >> 32), fbits(one)});
         }
     dev_.wait(dev_.submit(l));

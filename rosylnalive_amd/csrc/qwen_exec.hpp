@@ -7,14 +7,17 @@
 // Two modes:
 //   Fp32 - the reference catalog kernels (ids 0..13): fp32 activations and an fp32 token-major KV cache, as every
 //          reference GPU keeps. This is the parity path against CpuRef F32.
-//   Fast - the appended bf16 kernels: bf16 activations into MFMA GEMMs, fp32 residual stream, a head-major bf16 KV
-//          cache, fused norm/RoPE/KV-append/SwiGLU/residual epilogues, and the decode step recorded once as a reusable
-//          list (a hipGraph) that reads its position from device memory, with the greedy argmax fed back on device.
+//   Fast - the appended kernels: bf16 weights, fp16 MFMA operands in prefill (an exact on-device fp16 copy of each
+//          matrix, fp16-rounded activations), fp32 residual stream, a head-major fp16 KV cache, fused
+//          norm/RoPE/KV-append/SwiGLU/residual epilogues, and the decode step recorded once as a reusable list (a
+//          hipGraph) that streams the bf16 weights, reads its position from device memory and feeds the greedy argmax
+//          back on device.
 #pragma once
 
 #include <cstdint>
 #include <map>
 #include <memory>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -78,6 +81,7 @@ class QwenExec {
     uint32_t forward_fp32(int pos0, int t, float* logits, int logits_rows);
     uint32_t forward_fast(int seq, int pos0, int t, float* logits, int logits_rows);
     void record_decode_fast();
+    void sync_f16();  // refreshes the fp16 copies of the matrices written since the last forward
     void tap_copy(CommandList* l, const std::string& name, uint32_t src, int t, int width);
     uint32_t dispatch(CommandList* l, const char* kernel, std::vector<uint32_t> fields);
 
@@ -102,6 +106,8 @@ class QwenExec {
     int last_t_ = 0;
     double last_ms_ = 0;
     CommandList* decode_list_ = nullptr;
+    std::map<std::string, std::string> f16_copy_;  // bf16 matrix -> its fp16 copy (Fast mode)
+    std::set<std::string> f16_dirty_;
     void add(const std::string& name, uint32_t arena, uint32_t dtype, std::vector<uint32_t> dims, uint32_t flags = 0);
     void add_view(const std::string& name, const std::string& of, std::vector<uint32_t> dims, uint64_t elem_offset);
     const Tensor& t(const std::string& name) const;

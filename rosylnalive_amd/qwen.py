@@ -142,11 +142,12 @@ def rope_table(head_dim: int, max_pos: int):
 
 class QwenModel:
     """A Qwen3 decoder resident on one HIP device. mode "fp32" runs the reference catalog kernels (the parity path);
-    mode "bf16" runs the fast path (MFMA GEMMs, fused epilogues, on-device greedy decode)."""
+    mode "fast" (alias "bf16": the model's weights stay bf16) runs the fast path: fp16-operand MFMA GEMMs with fused
+    epilogues for prefill, an fp16 KV cache, bf16-weight GEMVs and on-device greedy decode."""
 
-    MODES = {"fp32": 0, "bf16": 1}
+    MODES = {"fp32": 0, "fast": 1, "bf16": 1}
 
-    def __init__(self, backend: Optional[HipBackend], cfg: QwenConfig, mode: str = "bf16", max_tokens: int = 512,
+    def __init__(self, backend: Optional[HipBackend], cfg: QwenConfig, mode: str = "fast", max_tokens: int = 512,
                  taps: bool = False, inv_freq: Optional[Sequence[int]] = None):
         self.backend = backend or HipBackend(0)
         self.cfg = cfg

@@ -42,7 +42,7 @@ def test_abi_version_and_catalog_order():
     L = _native.lib()
     assert L.lrm_abi_version() == 1
     names = [k.name for k in Catalog.all()]
-    # Kernels.all at contracts-v1 (kernel-abi.md "The catalog at contracts-v1"), then the appended bf16 kernels
+    # Kernels.all at contracts-v1 (kernel-abi.md "The catalog at contracts-v1"), then the appended fast-path kernels
     assert names[:14] == ["scale_f32", "table_echo", "args_echo", "groups_echo", "bf16_unpack", "embed_gather_bf16",
                           "rmsnorm_rows", "rope_apply", "silu_mul", "add", "copy_rows", "argmax_rows", "matmul_bf16w",
                           "attention_gqa_causal"]

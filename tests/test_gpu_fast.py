@@ -1,0 +1,354 @@
+"""GPU tests of the fast kernels in isolation, through catalog dispatches: the fp16 MFMA GEMM epilogues, the MFMA
+flash-attention prefill kernel (the isolated-attention workload: T 2048, 16/8 heads, head_dim 128, Q/K RMS-normed
+and RoPE'd first), the decode GEMVs, the split-KV decode attention with its cache append, and the on-device argmax,
+each against the oracle or an float64 restatement on the same rounded inputs.
+"""
+import numpy as np
+import pytest
+
+from gpu_session import Session, written_everywhere
+from oracle import cpuref, metrics
+from rosylnalive_amd.gpu_core import DType, TensorFlags
+from rosylnalive_amd.qwen import inv_freq_bits, synthetic_normal_f32
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16, F16, U32 = DType.F32, DType.BF16, DType.F16, DType.U32
+RO = TensorFlags.READ_ONLY
+
+
+def bf16(a):
+    return cpuref.bf16_narrow(np.asarray(a, np.float32))
+
+
+def widen(b):
+    return cpuref.bf16_widen(b)
+
+
+def f16(a):
+    """float -> fp16 bits (round to nearest even)."""
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def hwiden(h):
+    return np.asarray(h, np.uint16).view(np.float16).astype(np.float32)
+
+
+# ---------------------------------------------------------------- prefill kernels
+
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (512, 1024, 1024), (37, 300, 192), (2048, 2048, 1024)])
+def test_gemm_f32_and_residual(m, n, k):
+    r = np.random.default_rng(m + n + k)
+    a = f16(r.standard_normal((m, k)))
+    w = f16(r.standard_normal((n, k)) * 0.05)
+    x0 = r.standard_normal((m, n)).astype(np.float32)
+    s = Session({"a": (F16, (m, k), 0, a), "w": (F16, (n, k), RO, w), "y": (F32, (m, n), 0, None),
+                 "x": (F32, (m, n), 0, x0)})
+    try:
+        ref = hwiden(a).astype(np.float64) @ hwiden(w).astype(np.float64).T
+        y = s.run("gemm_f32", ["y"], a="a", w="w", y="y", m=m, n=n, k=k)["y"]
+        assert written_everywhere(y)
+        assert metrics.rel_l2(y, ref) < 1e-6, metrics.rel_l2(y, ref)
+        cl = s.backend.begin()
+        cl.dispatch("gemm_residual", s.fields("gemm_residual", a="a", w="w", x="x", m=m, n=n, k=k))
+        s.backend.wait(s.backend.submit(cl))
+        cl.release()
+        assert metrics.rel_l2(s.read("x"), x0 + ref) < 1e-6
+    finally:
+        s.close()
+
+
+def test_gemm_swiglu():
+    m, inter, k = 200, 192, 128
+    r = np.random.default_rng(3)
+    a = f16(r.standard_normal((m, k)))
+    w = f16(r.standard_normal((2 * inter, k)) * 0.1)
+    s = Session({"a": (F16, (m, k), 0, a), "w": (F16, (2 * inter, k), RO, w), "y": (F16, (m, inter), 0, None)})
+    try:
+        y = hwiden(s.run("gemm_swiglu", ["y"], a="a", w="w", y="y", m=m, inter=inter, k=k)["y"])
+        h = hwiden(a).astype(np.float64) @ hwiden(w).astype(np.float64).T
+        g, u = h[:, :inter], h[:, inter:]
+        ref = g / (1 + np.exp(-g)) * u
+        assert metrics.rel_l2(y, ref) < 2e-3
+    finally:
+        s.close()
+
+
+def test_gemm_qkv_rope_epilogue():
+    """q|k|v projection with the per-head RMSNorm + RoPE epilogue and the K / V^T cache writes, against CpuRef F64
+    on the same fp16 operands."""
+    T, pos0, H, max_pos = 100, 37, 256, 256
+    r = np.random.default_rng(11)
+    h = f16(r.standard_normal((T, H)))
+    w = f16(r.standard_normal((32 * 128, H)) * 0.06)
+    qn = bf16(1 + 0.1 * r.standard_normal(128))
+    kn = bf16(1 + 0.1 * r.standard_normal(128))
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), max_pos)
+    s = Session({"h": (F16, h.shape, 0, h), "w": (F16, w.shape, RO, w), "qn": (BF16, (128,), RO, qn),
+                 "kn": (BF16, (128,), RO, kn), "cos": (F32, cos.shape, RO, cos), "sin": (F32, sin.shape, RO, sin),
+                 "q": (F16, (T, 2048), 0, None), "kc": (F16, (8, max_pos, 128), 0, None),
+                 "vc": (F16, (8, 128, max_pos), 0, None)})
+    try:
+        out = s.run("gemm_qkv_rope", ["q", "kc", "vc"], h="h", w="w", q_norm="qn", k_norm="kn", cos_table="cos",
+                    sin_table="sin", q="q", k_cache="kc", v_cache="vc", m=T, hidden=H, q_heads=16, kv_heads=8,
+                    pos0=pos0, max_pos=max_pos, eps=1e-6)
+        proj = hwiden(h).astype(np.float64) @ hwiden(w).astype(np.float64).T
+        qr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(proj[:, :2048].copy(), qn, 1e-6), 16, pos0)
+        kr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(proj[:, 2048:3072].copy(), kn, 1e-6), 8, pos0)
+        v = proj[:, 3072:]
+        kc = hwiden(out["kc"][:, pos0:pos0 + T, :]).transpose(1, 0, 2).reshape(T, 1024)
+        vc = hwiden(out["vc"][:, :, pos0:pos0 + T]).transpose(2, 0, 1).reshape(T, 1024)
+        for got, ref in [(hwiden(out["q"]), qr), (kc, kr), (vc, v)]:
+            assert metrics.max_abs(got, ref) <= 2e-3 * max(1.0, np.abs(ref).max()), metrics.max_abs(got, ref)
+        # rows outside [pos0, pos0 + T) are untouched
+        assert not written_everywhere(out["kc"][:, :pos0, :]) and not written_everywhere(out["vc"][:, :, :pos0])
+    finally:
+        s.close()
+
+
+def _qkv_inputs(T, pos0, max_pos, seed):
+    """Q, K, V ~ N(0, 1) for 16 q heads / 8 kv heads, head_dim 128, with per-head RMSNorm (weight 1) and RoPE
+    (theta 1e6) applied to Q and K at positions pos0.., rounded to fp16 as the fast path stores them."""
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), max_pos)
+    q = synthetic_normal_f32(seed, "attn/q", (T, 16 * 128))
+    k = synthetic_normal_f32(seed, "attn/k", (pos0 + T, 8 * 128))
+    v = synthetic_normal_f32(seed, "attn/v", (pos0 + T, 8 * 128))
+    ones = np.full(128, 0x3F80, np.uint16)
+    qn = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q, ones, 1e-6), 16, pos0)
+    kn = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(k, ones, 1e-6), 8, 0)
+    return f16(qn), f16(kn), f16(v)
+
+
+def _caches(kb, vb, max_pos, fill=0):
+    """Token-major [pos, kvh * 128] fp16 rows -> the fast path's head-major K and transposed V caches; positions past
+    the rows hold `fill`."""
+    P = kb.shape[0]
+    kc = np.full((8, max_pos, 128), fill, np.uint16)
+    vc = np.full((8, 128, max_pos), fill, np.uint16)
+    kc[:, :P, :] = kb.reshape(P, 8, 128).transpose(1, 0, 2)
+    vc[:, :, :P] = vb.reshape(P, 8, 128).transpose(1, 2, 0)
+    return kc, vc
+
+
+@pytest.mark.parametrize("T,past", [(64, 0), (100, 0), (2048, 0), (77, 300)])
+def test_attention_prefill_f16(T, past):
+    max_pos = ((past + T + 63) // 64) * 64 + 64
+    qb, kb, vb = _qkv_inputs(T, past, max_pos, seed=T + past)
+    kc, vc = _caches(kb, vb, max_pos, fill=0x7E00)  # NaN past the context: the kernel must never use it
+    s = Session({"q": (F16, qb.shape, 0, qb), "k": (F16, kc.shape, 0, kc), "v": (F16, vc.shape, 0, vc),
+                 "y": (F16, qb.shape, 0, None)})
+    try:
+        scale = float(cpuref.attention_scale(128, np.float32))
+        y = hwiden(s.run("attention_prefill_f16", ["y"], q="q", k_cache="k", v_cache="v", y="y", rows=T, past=past,
+                         q_heads=16, kv_heads=8, max_pos=max_pos, scale=scale)["y"])
+        qf, kf, vf = hwiden(qb), hwiden(kb), hwiden(vb)
+        ref = cpuref.attention(qf.astype(np.float64), kf, vf, 16, 8, 128, past, float(scale))
+        err, rel = metrics.max_abs(y, ref), metrics.rel_l2(y, ref)
+        print(f"attention prefill T={T} past={past}: max-abs {err:.3g}, relL2 {rel:.3g}", flush=True)
+        assert err <= 1e-2 and rel <= 5e-3
+    finally:
+        s.close()
+
+
+# ---------------------------------------------------------------- decode kernels
+
+def test_convert_bf16_f16_bit_exact():
+    n = 1_000_003
+    r = np.random.default_rng(1)
+    x = bf16(r.standard_normal(n) * np.exp2(r.integers(-30, 17, n)))  # subnormal and overflow ranges included
+    x[:4] = [0x7F80, 0xFF80, 0x7FC0, 0x8000]
+    s = Session({"x": (BF16, (n,), RO, x), "y": (F16, (n,), 0, None)})
+    try:
+        y = s.run("convert_bf16_f16", ["y"], x="x", y="y", n=n)["y"]
+        ref = widen(x).astype(np.float16).view(np.uint16)
+        nan = np.isnan(widen(x))
+        assert np.array_equal(y[~nan], ref[~nan]) and np.isnan(hwiden(y[nan])).all()
+    finally:
+        s.close()
+
+
+def test_rmsnorm_rows_f16():
+    rows, cols, row0 = 37, 1024, 5
+    r = np.random.default_rng(2)
+    x = (r.standard_normal((rows + row0, cols)) * 3).astype(np.float32)
+    w = bf16(1 + 0.1 * r.standard_normal(cols))
+    s = Session({"x": (F32, x.shape, RO, x), "w": (BF16, (cols,), RO, w), "y": (F16, (rows, cols), 0, None)})
+    try:
+        y = hwiden(s.run("rmsnorm_rows_f16", ["y"], x="x", w="w", y="y", rows=rows, cols=cols, eps=1e-6,
+                         x_row0=row0)["y"])
+        ref = cpuref.rmsnorm(x[row0:].astype(np.float64), w, 1e-6)
+        assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -10 + 2.0 ** -24)  # within one fp16 rounding
+    finally:
+        s.close()
+
+
+def _gemv_ref(w, x):
+    return widen(w).astype(np.float64) @ np.asarray(x, np.float64)
+
+
+@pytest.mark.parametrize("n,k", [(4096, 1024), (1000, 2048), (3, 8)])
+def test_gemv_norm_dec(n, k):
+    r = np.random.default_rng(n + k)
+    x = (r.standard_normal(k) * 2).astype(np.float32)
+    nw = bf16(1 + 0.1 * r.standard_normal(k))
+    w = bf16(r.standard_normal((n, k)) * 0.05)
+    s = Session({"x": (F32, (k,), RO, x), "nw": (BF16, (k,), RO, nw), "w": (BF16, (n, k), RO, w),
+                 "y": (F32, (n,), 0, None)})
+    try:
+        y = s.run("gemv_norm_dec", ["y"], x="x", norm="nw", w="w", y="y", n=n, k=k, eps=1e-6)["y"]
+        ref = _gemv_ref(w, cpuref.rmsnorm(x[None].astype(np.float64), nw, 1e-6)[0])
+        assert metrics.rel_l2(y, ref) < 1e-5
+    finally:
+        s.close()
+
+
+@pytest.mark.parametrize("n,k", [(1024, 2048), (1024, 3072), (4096, 1024), (77, 64)])
+def test_gemv_residual_dec(n, k):
+    r = np.random.default_rng(n * 7 + k)
+    a = r.standard_normal(k).astype(np.float32)
+    w = bf16(r.standard_normal((n, k)) * 0.05)
+    x0 = r.standard_normal(n).astype(np.float32)
+    s = Session({"a": (F32, (k,), RO, a), "w": (BF16, (n, k), RO, w), "x": (F32, (n,), 0, x0)})
+    try:
+        s.run_list([("gemv_residual_dec", dict(a="a", w="w", x="x", n=n, k=k))], [], reset={"x": x0})
+        assert metrics.rel_l2(s.read("x"), x0 + _gemv_ref(w, a)) < 1e-5
+    finally:
+        s.close()
+
+
+def test_gemv_swiglu_dec():
+    inter, hidden = 3072, 1024
+    r = np.random.default_rng(9)
+    x = r.standard_normal(hidden).astype(np.float32)
+    nw = bf16(1 + 0.1 * r.standard_normal(hidden))
+    w = bf16(r.standard_normal((2 * inter, hidden)) * 0.05)
+    s = Session({"x": (F32, (hidden,), RO, x), "nw": (BF16, (hidden,), RO, nw), "w": (BF16, w.shape, RO, w),
+                 "y": (F32, (inter,), 0, None)})
+    try:
+        y = s.run("gemv_swiglu_dec", ["y"], x="x", norm="nw", w="w", y="y", inter=inter, hidden=hidden, eps=1e-6)["y"]
+        h = _gemv_ref(w, cpuref.rmsnorm(x[None].astype(np.float64), nw, 1e-6)[0])
+        g, u = h[:inter], h[inter:]
+        assert metrics.rel_l2(y, g / (1 + np.exp(-g)) * u) < 1e-5
+    finally:
+        s.close()
+
+
+def _lm_session(vocab, hidden, e):
+    r = np.random.default_rng(vocab)
+    x = r.standard_normal(hidden).astype(np.float32)
+    nw = bf16(1 + 0.1 * r.standard_normal(hidden))
+    return x, nw, Session({
+        "x": (F32, (hidden,), RO, x), "nw": (BF16, (hidden,), RO, nw), "e": (BF16, e.shape, RO, e),
+        "logits": (F32, (vocab,), 0, None), "part": (F32, (2048,), 0, None), "state": (U32, (4,), 0, None),
+        "ids": (U32, (8,), 0, np.zeros(8, np.uint32))})
+
+
+def _lm_run(s, vocab, hidden, state):
+    return s.run_list([("lmhead_dec", dict(x="x", norm="nw", embed="e", logits="logits", partials="part", vocab=vocab,
+                                          hidden=hidden, eps=1e-6, write_logits=1)),
+                       ("argmax_dec", dict(partials="part", state="state", out_ids="ids", max_steps=8))],
+                      ["logits"], reset={"state": state})
+
+
+def test_lmhead_and_argmax_dec():
+    vocab, hidden = 50021, 1024
+    r = np.random.default_rng(4)
+    e = bf16(r.standard_normal((vocab, hidden)) * 0.05)
+    x, nw, s = _lm_session(vocab, hidden, e)
+    try:
+        out = _lm_run(s, vocab, hidden, np.array([17, 5, 3, 0], np.uint32))
+        ref = _gemv_ref(e, cpuref.rmsnorm(x[None].astype(np.float64), nw, 1e-6)[0])
+        assert metrics.rel_l2(out["logits"], ref) < 1e-5
+        am = int(np.argmax(out["logits"]))
+        assert list(s.read("state")[:3]) == [18, am, 4] and int(s.read("ids")[3]) == am
+        # a tie between two rows resolves to the lower index, across blocks
+        twin = 30001 if am != 30001 else 30002
+        e2 = e.copy()
+        e2[twin] = e2[am]  # the same dot product, the same bits, in another block
+        s.write("e", e2)
+        out2 = _lm_run(s, vocab, hidden, np.array([0, 0, 0, 0], np.uint32))
+        top = np.flatnonzero(out2["logits"] == out2["logits"].max())
+        assert top.size >= 2 and int(s.read("state")[1]) == int(top[0]) == min(am, twin)
+        # a NaN logit gives id 0xFFFFFFFF
+        e3 = e.copy()
+        e3[12345, 7] = 0x7FC0
+        s.write("e", e3)
+        _lm_run(s, vocab, hidden, np.array([0, 0, 0, 0], np.uint32))
+        assert int(s.read("state")[1]) == 0xFFFFFFFF and int(s.read("ids")[0]) == 0xFFFFFFFF
+    finally:
+        s.close()
+
+
+def test_embed_dec():
+    vocab, hidden = 300, 1024
+    e = bf16(np.random.default_rng(5).standard_normal((vocab, hidden)))
+    s = Session({"e": (BF16, e.shape, RO, e), "state": (U32, (4,), 0, np.array([9, 123, 0, 0], np.uint32)),
+                 "x": (F32, (hidden,), 0, None)})
+    try:
+        x = s.run("embed_dec", ["x"], embed="e", state="state", x="x", hidden=hidden, vocab=vocab)["x"]
+        assert x.tobytes() == widen(e[123]).tobytes()
+        s.write("state", np.array([9, vocab, 0, 0], np.uint32))
+        x = s.run("embed_dec", ["x"], embed="e", state="state", x="x", hidden=hidden, vocab=vocab)["x"]
+        assert np.isnan(x).all()
+    finally:
+        s.close()
+
+
+@pytest.mark.parametrize("pos", [0, 63, 64, 383, 1000, 4095])
+def test_attention_decode_f16(pos):
+    """One decode step's attention: raw q|k|v projection in, q/k RMSNorm + RoPE at `pos`, the new key and value
+    appended to the caches, split-KV attention over positions 0..pos, then the split combine."""
+    max_pos = 4096
+    S = max_pos // 64
+    r = np.random.default_rng(pos)
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), max_pos)
+    _, kb, vb = _qkv_inputs(1, pos, max_pos, seed=pos + 1)  # fp16 cache rows for positions 0 .. pos
+    kc, vc = _caches(kb[:pos], vb[:pos], max_pos, fill=0x7E00)  # position pos onwards: NaN until written
+    qkv = (r.standard_normal(4096) * 1.5).astype(np.float32)
+    qn = bf16(1 + 0.1 * r.standard_normal(128))
+    kn = bf16(1 + 0.1 * r.standard_normal(128))
+    state = np.array([pos, 0, 0, 0], np.uint32)
+    s = Session({"qkv": (F32, (4096,), RO, qkv), "qn": (BF16, (128,), RO, qn), "kn": (BF16, (128,), RO, kn),
+                 "cos": (F32, cos.shape, RO, cos), "sin": (F32, sin.shape, RO, sin),
+                 "kc": (F16, kc.shape, 0, kc), "vc": (F16, vc.shape, 0, vc),
+                 "part": (F32, (16 * S * 130,), 0, None), "y": (F32, (2048,), 0, None),
+                 "state": (U32, (4,), RO, state)})
+    try:
+        scale = float(cpuref.attention_scale(128, np.float32))
+        y = s.run_list([("attention_decode_f16", dict(qkv="qkv", q_norm="qn", k_norm="kn", cos_table="cos",
+                                                      sin_table="sin", k_cache="kc", v_cache="vc", partials="part",
+                                                      state="state", q_heads=16, kv_heads=8, max_pos=max_pos,
+                                                      eps=1e-6, scale=scale)),
+                        ("attention_combine", dict(partials="part", y="y", state="state", q_heads=16,
+                                                   max_pos=max_pos))], ["y"])["y"]
+        q64 = qkv[None].astype(np.float64)
+        qr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, :2048].copy(), qn, 1e-6), 16, pos)
+        kr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, 2048:3072].copy(), kn, 1e-6), 8, pos)
+        kc2, vc2 = s.read("kc"), s.read("vc")
+        k_new = hwiden(kc2[:, pos, :]).reshape(1, 1024)
+        v_new = vc2[:, :, pos].reshape(1, 1024)
+        assert np.all(np.abs(k_new - kr) <= np.abs(kr) * 2.0 ** -10 + 2.0 ** -24), "appended key"
+        assert v_new.tobytes() == f16(qkv[3072:]).reshape(1, 1024).tobytes(), "appended value"
+        # other positions are untouched
+        assert np.array_equal(np.delete(kc2, pos, axis=1), np.delete(kc, pos, axis=1))
+        assert np.array_equal(np.delete(vc2, pos, axis=2), np.delete(vc, pos, axis=2))
+        kf = np.concatenate([hwiden(kb[:pos]), k_new]).astype(np.float64)
+        vf = np.concatenate([hwiden(vb[:pos]), hwiden(v_new)]).astype(np.float64)
+        ref = cpuref.attention(qr, kf, vf, 16, 8, 128, pos, scale)
+        err, rel = metrics.max_abs(y, ref), metrics.rel_l2(y, ref)
+        print(f"attention decode pos={pos}: max-abs {err:.3g}, relL2 {rel:.3g}", flush=True)
+        assert err <= 1e-3 and rel <= 1e-4
+    finally:
+        s.close()
+
+
+def test_fill_normal_f16_statistics():
+    n = 1 << 20
+    s = Session({"y": (F16, (n,), 0, None)})
+    try:
+        y = hwiden(s.run("fill_normal_f16", ["y"], y="y", n=n, seed_lo=7, seed_hi=0, stream_lo=3, stream_hi=1,
+                         std=1.0)["y"])
+        assert np.isfinite(y).all() and abs(y.mean()) < 0.01 and abs(y.std() - 1) < 0.01
+        assert np.array_equal(widen(bf16(y)), y), "every value is a bf16 value"
+    finally:
+        s.close()

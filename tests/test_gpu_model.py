@@ -1,0 +1,193 @@
+"""GPU tests of the Qwen3 executor through the C ABI against the oracle and the reference's committed goldens.
+
+fp32 mode (the reference catalog kernels): the tiny-g1 taps against torch32 within the reference's CPU32 floors
+(TinyModelTests.fs:17-23), the 64 greedy ids of both goldens, prefill == token-by-token decode bit for bit, and the
+plumbing config (hd 16, vocab 512) greedy ids equal to the oracle's.
+fast mode (bf16 weights, fp16 MFMA operands and KV cache): logits within max-abs 2e-2 of CpuRef F32 and top-1
+agreement >= 99%, for prefill, chunked prefill and on-device decode.
+"""
+import numpy as np
+import pytest
+
+from conftest import golden
+from oracle import cpuref, metrics
+from rosylnalive_amd.gpu_core import HipBackend
+from rosylnalive_amd.qwen import QwenConfig, QwenModel, inv_freq_bits, synthetic_ids, synthetic_weights
+
+pytestmark = pytest.mark.gpu
+
+CHAIN_REL, LOGIT_MAXABS, LOGIT_KL = 1e-5, 2e-3, 1e-7
+
+
+def tiny_cfg(tiny):
+    c = tiny["cfg"]
+    return QwenConfig(c["layers"], c["hidden"], c["heads"], c["kv_heads"], c["head_dim"], c["intermediate"],
+                      c["vocab"], c["max_pos"], c["eps"])
+
+
+@pytest.fixture(scope="module")
+def tiny_fp32(tiny):
+    m = QwenModel(HipBackend(0), tiny_cfg(tiny), mode="fp32", max_tokens=80, taps=True,
+                  inv_freq=tiny["rope"]["inv_freq.bits"])
+    m.load_weights(tiny["weights"])
+    yield m
+    m.close()
+    m.backend.close()
+
+
+@pytest.mark.parametrize("prompt", ["p0", "p1", "p2"])
+def test_tiny_fp32_taps_match_goldens(tiny, tiny_fp32, prompt):
+    g32 = golden(f"fwd_f32.{prompt}.safetensors")
+    ids = g32["input_ids"].astype(np.int32)
+    logits, am = tiny_fp32.forward(ids, 0)
+    taps = tiny_fp32.taps(ids.size)
+    names = [n for n in cpuref.tap_names(tiny["cfg"]["layers"]) if n in g32]
+    worst = 0.0
+    for n in names:
+        r = metrics.rel_l2(taps[n], g32[n])
+        worst = max(worst, r)
+        assert r <= CHAIN_REL, (n, r)
+    assert metrics.rel_l2(logits, g32["logits"]) <= CHAIN_REL
+    assert metrics.max_abs(logits, g32["logits"]) <= LOGIT_MAXABS
+    assert metrics.kl_max(logits, g32["logits"]) <= LOGIT_KL
+    assert am == int(np.argmax(g32["logits"][-1]))
+    print(f"{prompt}: worst tap relL2 vs torch32 {worst:.3g}", flush=True)
+
+
+@pytest.mark.parametrize("prompt", ["p0", "p1"])
+def test_tiny_fp32_greedy_64_equals_goldens(tiny, tiny_fp32, prompt):
+    g = golden("greedy.safetensors")
+    ids = golden(f"fwd_f32.{prompt}.safetensors")["input_ids"].astype(np.int32)
+    out = tiny_fp32.greedy(ids, 64)
+    assert out.tolist() == g[f"{prompt}.ids.torch32"].tolist()
+    assert out.tolist() == g[f"{prompt}.ids.torch64p"].tolist()
+
+
+def test_tiny_fp32_prefill_equals_decode_bit_for_bit(tiny, tiny_fp32):
+    """Batch invariance of the catalog kernels (docs/contracts/batch-invariance.md): a prefill row equals the same
+    position decoded alone, and so do the caches."""
+    ids = golden("fwd_f32.p2.safetensors")["input_ids"].astype(np.int32)[:40]
+    pre, _ = tiny_fp32.forward(ids, 0)
+    kc = [tiny_fp32.read_cache(l, "k", 0, 40) for l in range(2)]
+    for t in range(ids.size):
+        row, _ = tiny_fp32.forward(ids[t:t + 1], t)
+        assert row.tobytes() == pre[t:t + 1].tobytes(), t
+    for l in range(2):
+        assert tiny_fp32.read_cache(l, "k", 0, 40).tobytes() == kc[l].tobytes()
+
+
+def test_plumbing_config_greedy_equals_oracle():
+    """The plumbing config: 2 layers, hidden 64, 4/2 heads, head_dim 16, SwiGLU 192, vocab 512; N(0, 0.02) weights,
+    norms 1; 16 prompt ids then 8 greedy tokens."""
+    cfg = QwenConfig.tiny_plumbing(max_pos=64)
+    w = synthetic_weights(cfg, seed=11)
+    prompt = synthetic_ids(11, "plumbing/prompt", 16, cfg.vocab)
+    cos, sin = cpuref.rope_table(inv_freq_bits(16), cfg.max_pos)
+    orc = cpuref.QwenOracle(cfg.oracle_dict(), w, cos, sin)
+    ref = orc.greedy(prompt, 8)
+    b = HipBackend(0)
+    try:
+        m = QwenModel(b, cfg, mode="fp32", max_tokens=32)
+        m.load_weights(w)
+        got = m.greedy(prompt, 8)
+        assert got.tolist() == ref.tolist()
+        lg, _ = m.forward(prompt, 0)
+        ol = orc.forward(orc.new_cache(), 0, prompt)
+        rng_ = float(ol.max() - ol.min())
+        assert metrics.max_abs(lg, ol) <= 1e-3 * rng_
+        m.close()
+    finally:
+        b.close()
+
+
+# ---------------------------------------------------------------- fast path
+
+def reduced_0_6b(layers=2, max_pos=512):
+    c = QwenConfig.qwen3_0_6b(max_pos=max_pos)
+    c.layers = layers
+    return c
+
+
+@pytest.fixture(scope="module")
+def fast_setup():
+    cfg = reduced_0_6b(layers=2, max_pos=512)
+    w = synthetic_weights(cfg, seed=5)
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), cfg.max_pos)
+    orc = cpuref.QwenOracle(cfg.oracle_dict(), w, cos, sin)
+    b = HipBackend(0)
+    m = QwenModel(b, cfg, mode="fast", max_tokens=256)
+    m.load_weights(w)
+    yield cfg, w, orc, m
+    m.close()
+    b.close()
+
+
+def test_fast_weights_round_trip(fast_setup):
+    cfg, w, orc, m = fast_setup
+    for name in ["model.layers.1.self_attn.k_proj.weight", "model.layers.0.mlp.up_proj.weight",
+                 "model.embed_tokens.weight"]:
+        assert m.read_weight(name).tobytes() == w[name].tobytes()
+
+
+def test_fast_rejects_weights_outside_fp16(fast_setup):
+    cfg, w, orc, m = fast_setup
+    name = "model.layers.0.self_attn.o_proj.weight"
+    bad = w[name].copy()
+    bad[3, 5] = 0x4780  # 65536: no fp16 counterpart
+    with pytest.raises(Exception, match="fp16 range"):
+        m.set_weight(name, bad)
+    m.set_weight(name, w[name])
+
+
+def test_fast_prefill_logits_within_north_star_bound(fast_setup):
+    cfg, w, orc, m = fast_setup
+    ids = synthetic_ids(5, "fast/prompt", 200, cfg.vocab)
+    lg, am = m.forward(ids, 0)
+    ol = orc.forward(orc.new_cache(), 0, ids)
+    err = metrics.max_abs(lg, ol)
+    top1 = metrics.top1_agreement(lg, ol)
+    print(f"fast prefill vs CpuRef F32: max-abs {err:.4g} (logit range {ol.min():.3g}..{ol.max():.3g}), "
+          f"top-1 {top1:.4f}", flush=True)
+    assert err <= 2e-2 and top1 >= 0.99
+    assert am == int(np.argmax(lg[-1]))
+
+
+def test_fast_chunked_prefill_equals_whole(fast_setup):
+    cfg, w, orc, m = fast_setup
+    ids = synthetic_ids(6, "fast/chunk", 300, cfg.vocab)  # 300 > max_tokens 256: two chunks
+    lg, _ = m.forward(ids, 0, logits_rows=60)
+    ol = orc.forward(orc.new_cache(), 0, ids)[-60:]
+    assert metrics.max_abs(lg, ol) <= 2e-2 and metrics.top1_agreement(lg, ol) >= 0.99
+
+
+def test_fast_decode_on_device_matches_oracle(fast_setup):
+    """Teacher-forced decode: each step's logits (the recorded HIP graph, position and token read from device
+    memory) against CpuRef F32 at the same position."""
+    cfg, w, orc, m = fast_setup
+    prompt = synthetic_ids(7, "fast/decode", 64, cfg.vocab)
+    cont = synthetic_ids(7, "fast/decode/cont", 40, cfg.vocab)
+    seq = np.concatenate([prompt, cont])
+    m.forward(prompt, 0, logits_rows=1)
+    ol = orc.forward(orc.new_cache(), 0, seq)
+    agree, worst = 0, 0.0
+    for i, tok in enumerate(cont):
+        pos = prompt.size + i
+        m.decode_set(int(tok), pos)
+        m.decode_run(1)
+        lg = m.read_logits(1)
+        worst = max(worst, metrics.max_abs(lg, ol[pos:pos + 1]))
+        agree += int(np.argmax(lg[0]) == np.argmax(ol[pos]))
+        assert int(m.decode_ids(1)[0]) == int(np.argmax(lg[0]))
+    print(f"fast decode vs CpuRef F32: worst max-abs {worst:.4g}, top-1 {agree}/{cont.size}", flush=True)
+    assert worst <= 2e-2 and agree >= 0.99 * cont.size - 1e-9
+
+
+def test_fast_greedy_runs_on_device(fast_setup):
+    cfg, w, orc, m = fast_setup
+    prompt = synthetic_ids(8, "fast/greedy", 32, cfg.vocab)
+    out = m.greedy(prompt, 24)
+    # replaying the produced sequence through the prefill path gives the same argmax at every generated step
+    seq = np.concatenate([prompt, out[:-1]])
+    lg, _ = m.forward(seq, 0)
+    agree = np.mean(np.argmax(lg[prompt.size - 1:], axis=1) == out)
+    assert agree >= 0.95, agree
