@@ -90,3 +90,14 @@ def top1_agreement(candidate, reference) -> float:
     a = np.asarray(candidate)
     b = np.asarray(reference)
     return float(np.mean(np.argmax(a, axis=-1) == np.argmax(b, axis=-1)))
+
+
+def top1_flip_gaps(candidate, reference) -> np.ndarray:
+    """For the rows whose argmax disagrees, how far the candidate's choice sits below the reference's maximum in the
+    reference's own logits (0 for an exact tie). A disagreement inside the logit error bound is a near-tie that the
+    bound allows; one beyond it is a wrong answer."""
+    a = np.asarray(candidate)
+    b = np.asarray(reference)
+    ia, ib = np.argmax(a, axis=-1), np.argmax(b, axis=-1)
+    rows = np.flatnonzero(ia != ib)
+    return b[rows, ib[rows]] - b[rows, ia[rows]]

@@ -448,151 +448,182 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
 // ================================================================ decode kernels (one token per step)
 // The step state is device memory: state[0] = the position being decoded, state[1] = its token id, state[2] = the
 // step index. The argmax kernel writes the next id and advances the state, so a recorded step replays unchanged.
+//
+// The GEMVs give each wave whole rows and keep every wave independent (no LDS, no barrier): lane l covers the
+// k-chunks 512 c + 8 l .. + 7, c < NCH, and issues the loads of all its weight chunks and of its slice of the input
+// vector together, so the memory latency is paid once per kernel; the RMSNorm sum of squares and the dot products
+// are then reduced with wave shuffles (every wave holds the whole input vector, 8 values per lane per chunk).
 
 constexpr int kMaxHidden = 8192;
 
-// x (f32, K values) into LDS, multiplied by RMSNorm weight nw when nw != nullptr. red holds blockDim / 64 floats.
-__device__ __forceinline__ void load_x_norm(const float* x, const uint16_t* nw, float eps, int K, float* xs,
-                                            float* red) {
-    float ss = 0.f;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-        float v = x[k];
-        xs[k] = v;
-        ss = fmaf(v, v, ss);
+template <int NCH>
+__device__ __forceinline__ void load_chunks_f32(const float* x, int K, float (&v)[NCH][8]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int k0 = 512 * c + 8 * lane;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+        if (k0 < K) {
+            a = *reinterpret_cast<const float4*>(x + k0);
+            b = *reinterpret_cast<const float4*>(x + k0 + 4);
+        }
+        v[c][0] = a.x, v[c][1] = a.y, v[c][2] = a.z, v[c][3] = a.w;
+        v[c][4] = b.x, v[c][5] = b.y, v[c][6] = b.z, v[c][7] = b.w;
     }
-    if (nw) {
-        ss = wave_sum(ss);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-        __syncthreads();
-        float tot = 0.f;
-        for (int i = 0; i < int(blockDim.x >> 6); ++i) tot += red[i];
-        const float rr = 1.0f / sqrtf(tot / float(K) + eps);
-        for (int k = threadIdx.x; k < K; k += blockDim.x) xs[k] = bf2f(nw[k]) * (xs[k] * rr);
-    }
-    __syncthreads();
 }
 
-// Dot products of R bf16 weight rows with xs (LDS, f32), by one wave: lane l covers k = 512 c + 8 l .. + 7.
-template <int R>
-__device__ __forceinline__ void wave_rows_dot(const uint16_t* const* rows, const float* xs, int K, float* out) {
+template <int NCH>
+__device__ __forceinline__ void load_chunks_16(const uint16_t* row, int K, uint4 (&w)[NCH]) {
     const int lane = threadIdx.x & 63;
-    float acc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.f;
-    for (int k0 = 8 * lane; k0 < K; k0 += 512) {
-        uint4 wv[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) wv[r] = *reinterpret_cast<const uint4*>(rows[r] + k0);
-        const float4 x0 = *reinterpret_cast<const float4*>(xs + k0);
-        const float4 x1 = *reinterpret_cast<const float4*>(xs + k0 + 4);
-        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float wf[8];
-            unpack8(wv[r], wf);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[r] = fmaf(wf[e], xv[e], acc[r]);
-        }
+    for (int c = 0; c < NCH; ++c) {
+        const int k0 = 512 * c + 8 * lane;
+        w[c] = k0 < K ? *reinterpret_cast<const uint4*>(row + k0) : make_uint4(0, 0, 0, 0);
     }
+}
+
+// v <- widen(nw) * (v * r), r = 1 / sqrt(sum(v^2) / K + eps): the RMSNorm of the whole vector (padding lanes hold 0).
+template <int NCH>
+__device__ __forceinline__ void rmsnorm_chunks(float (&v)[NCH][8], const uint4 (&nw)[NCH], int K, float eps) {
+    float ss = 0.f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) out[r] = wave_sum(acc[r]);
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[c][e], v[c][e], ss);
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / float(K) + eps);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        float g[8];
+        unpack8(nw[c], g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[c][e] = g[e] * (v[c][e] * r);
+    }
+}
+
+// The dot product of a bf16 row (in chunks) with the vector v, reduced over the wave.
+template <int NCH>
+__device__ __forceinline__ float dot_chunks(const uint4 (&w)[NCH], const float (&v)[NCH][8]) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        float f[8];
+        unpack8(w[c], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf(f[e], v[c][e], acc);
+    }
+    return wave_sum(acc);
 }
 
 // ---------------------------------------------------------------- 20 gemv_norm_dec: y[n] = w[n] . RMSNorm(x)
-template <int R>
+template <int NCH>
 __global__ __launch_bounds__(256) void k_gemv_norm_dec(const float* x, const uint16_t* nw, const uint16_t* w, float* y,
                                                        int n, int k, float eps) {
-    __shared__ __attribute__((aligned(16))) float xs[kMaxHidden];
-    __shared__ float red[4];
-    load_x_norm(x, nw, eps, k, xs, red);
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + wv) * R;
-    if (row0 >= n) return;
-    const uint16_t* rows[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = w + size_t(min(row0 + r, n - 1)) * k;
-    float out[R];
-    wave_rows_dot<R>(rows, xs, k, out);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-        if (lane == r && row0 + r < n) y[row0 + r] = out[r];
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n) return;
+    uint4 wv[NCH], g[NCH];
+    float xv[NCH][8];
+    load_chunks_16<NCH>(w + size_t(row) * k, k, wv);
+    load_chunks_f32<NCH>(x, k, xv);
+    load_chunks_16<NCH>(nw, k, g);
+    rmsnorm_chunks<NCH>(xv, g, k, eps);
+    const float out = dot_chunks<NCH>(wv, xv);
+    if ((threadIdx.x & 63) == 0) y[row] = out;
 }
 
 // ---------------------------------------------------------------- 21 attention_decode_f16
 // Split-KV decode attention over positions 0 .. pos = state[0]. Block (s, kv head) takes keys [64 s, 64 s + 64) for
-// the two query heads of the group; it applies the q RMSNorm and RoPE to the raw projection itself, and the block whose
-// split holds pos first appends the new key (k RMSNorm + RoPE) and value to the caches. Each block writes, per head,
-// (max, sum, unnormalised output[128]) of its keys in the log2 domain; splits past pos do nothing.
+// the two query heads of the group. It issues the loads of its cached keys and values first, then applies the q
+// RMSNorm and RoPE to the raw projection; the block whose split holds pos also computes the new key (k RMSNorm +
+// RoPE) and value, appends them (fp16) to the caches and uses the same rounded values in place of the stale slot it
+// loaded. Each block writes, per head, (max, sum, unnormalised output[128]) of its keys in the log2 domain; splits
+// past pos do nothing.
 __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16_t* qn, const uint16_t* kn,
                                                   const float* cos_t, const float* sin_t, uint16_t* kc, uint16_t* vc,
                                                   float* part, const uint32_t* state, int qh, int kvh, int max_pos,
                                                   float eps, float scale_log2) {
     __shared__ float qs[2][128];
-    __shared__ float ks_new[128];
+    __shared__ float knew[128];
+    __shared__ float vnew[128];
     __shared__ float ps[2][64];
     __shared__ float stat[2][2];
-    __shared__ float red[4];
+    __shared__ float redq[4], redk[4];
     const int s = blockIdx.x, S = gridDim.x, kvhead = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int pos = int(state[0]);
     if (pos < 0 || pos >= max_pos) return;  // the host keeps decode inside max_pos; never touch memory past the cache
     const int key0 = s * 64;
     const int nkeys = min(64, pos + 1 - key0);
     if (nkeys <= 0) return;
-    const int hh = t >> 7, d = t & 127;  // thread t: head 2 kvhead + hh (q) / k (hh = 0) or v (hh = 1), dim d
-    const float cs = cos_t[size_t(pos) * 64 + (d & 63)], sn = sin_t[size_t(pos) * 64 + (d & 63)];
+    const bool last = s == (pos >> 6);  // uniform over the block
+    const int jnew = pos - key0;        // the new key's slot when `last`
 
-    // q: RMSNorm per head (waves 2 hh, 2 hh + 1), then the rotation of dims (d, d + 64)
-    const float qv = qkv[(kvhead * 2 + hh) * 128 + d];
-    float ss = wave_sum(qv * qv);
-    if (lane == 0) red[wv] = ss;
-    __syncthreads();
-    const float qr = bf2f(qn[d]) * (qv * (1.0f / sqrtf((red[2 * hh] + red[2 * hh + 1]) / 128.0f + eps)));
-    qs[hh][d] = qr;
-    __syncthreads();
-    const float qo = qs[hh][d ^ 64];
-    const float qrot = d < 64 ? qr * cs - qo * sn : qr * cs + qo * sn;
-    __syncthreads();
-    qs[hh][d] = qrot;
-
-    if (s == pos >> 6) {  // uniform over the block
-        const int QC = qh * 128, KC = kvh * 128;
-        const float kvv = qkv[QC + hh * KC + kvhead * 128 + d];  // hh = 0: k, hh = 1: v
-        float sk = wave_sum(kvv * kvv);
-        __syncthreads();  // every wave has read red (the q norm) before it is reused
-        if (lane == 0) red[wv] = sk;
-        __syncthreads();
-        const float kr = bf2f(kn[d]) * (kvv * (1.0f / sqrtf((red[0] + red[1]) / 128.0f + eps)));
-        if (hh == 0) ks_new[d] = kr;
-        __syncthreads();
-        if (hh == 0) {
-            const float ko = ks_new[d ^ 64];
-            const float krot = d < 64 ? kr * cs - ko * sn : kr * cs + ko * sn;
-            kc[(size_t(kvhead) * max_pos + pos) * 128 + d] = f2h(krot);
-        } else {
-            vc[(size_t(kvhead) * 128 + d) * max_pos + pos] = f2h(kvv);
-        }
-    }
-    __syncthreads();  // the q rotation, and this block's own cache writes, are visible to the block below
-
+    // 1) all loads together: this split's keys (thread: 4 keys x 8 dims) and values (4 dims x 8 keys), the raw
+    // projections, the norm weights and the rotation of pos
     const uint16_t* kb = kc + (size_t(kvhead) * max_pos + key0) * 128;
     const int d0 = 8 * (lane & 15);
-    float q0[8], q1[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        q0[e] = qs[0][d0 + e];
-        q1[e] = qs[1][d0 + e];
-    }
     uint4 kv4[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int key = wv * 16 + it * 4 + (lane >> 4);
         kv4[it] = key < nkeys ? *reinterpret_cast<const uint4*>(kb + size_t(key) * 128 + d0) : make_uint4(0, 0, 0, 0);
     }
+    const int sub = t & 7, rg = t >> 3;
+    const uint16_t* vb = vc + size_t(kvhead) * 128 * max_pos + key0 + sub * 8;  // key0 + 63 < max_pos
+    uint4 vv[4];
+#pragma unroll
+    for (int dd = 0; dd < 4; ++dd) vv[dd] = *reinterpret_cast<const uint4*>(vb + size_t(rg + 32 * dd) * max_pos);
+    const int hh = t >> 7, d = t & 127;  // thread t: q head 2 kvhead + hh; new key (hh = 0) or value (hh = 1); dim d
+    const int QC = qh * 128, KC = kvh * 128;
+    const float qv = qkv[(kvhead * 2 + hh) * 128 + d];
+    const float kvv = last ? qkv[QC + hh * KC + kvhead * 128 + d] : 0.f;
+    const float cs = cos_t[size_t(pos) * 64 + (d & 63)], sn = sin_t[size_t(pos) * 64 + (d & 63)];
+    const float qw = bf2f(qn[d]), kw = bf2f(kn[d]);
+
+    // 2) per-head RMSNorm (head hh = waves 2 hh, 2 hh + 1; the new key = waves 0, 1), then the rotation of (d, d + 64)
+    const float sq = wave_sum(qv * qv), sk = wave_sum(kvv * kvv);
+    if (lane == 0) {
+        redq[wv] = sq;
+        redk[wv] = sk;
+    }
+    __syncthreads();
+    const float qr = qw * (qv * (1.0f / sqrtf((redq[2 * hh] + redq[2 * hh + 1]) / 128.0f + eps)));
+    const float kr = kw * (kvv * (1.0f / sqrtf((redk[0] + redk[1]) / 128.0f + eps)));
+    qs[hh][d] = qr;
+    if (hh == 0) knew[d] = kr;
+    __syncthreads();
+    const float qrot = d < 64 ? qr * cs - qs[hh][d + 64] * sn : qr * cs + qs[hh][d - 64] * sn;
+    const float krot = d < 64 ? kr * cs - knew[d + 64] * sn : kr * cs + knew[d - 64] * sn;
+    __syncthreads();
+    qs[hh][d] = qrot;
+    if (last) {
+        if (hh == 0) {
+            const uint16_t kh = f2h(krot);
+            knew[d] = h2f(kh);
+            kc[(size_t(kvhead) * max_pos + pos) * 128 + d] = kh;
+        } else {
+            const uint16_t vh = f2h(kvv);
+            vnew[d] = h2f(vh);
+            vc[(size_t(kvhead) * 128 + d) * max_pos + pos] = vh;
+        }
+    }
+    __syncthreads();
+
+    // 3) scores of the split's keys for both heads
+    float q0[8], q1[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        q0[e] = qs[0][d0 + e];
+        q1[e] = qs[1][d0 + e];
+    }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int key = wv * 16 + it * 4 + (lane >> 4);
         float kf[8];
         unpack8h(kv4[it], kf);
+        if (last && key == jnew) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kf[e] = knew[d0 + e];
+        }
         float a0 = 0.f, a1 = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -622,8 +653,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
         }
     }
     __syncthreads();
-    // P V: thread t covers V^T rows d = (t >> 3) + 32 dd and keys 8 (t & 7) .. + 7 of the split
-    const int sub = t & 7, rg = t >> 3;
+
+    // 4) P V: thread t covers V^T rows d = (t >> 3) + 32 dd and keys 8 (t & 7) .. + 7 of the split
     float e0[8], e1[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -631,10 +662,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
         e1[e] = ps[1][sub * 8 + e];
     }
     const bool full = sub * 8 + 8 <= nkeys;
-    const uint16_t* vb = vc + size_t(kvhead) * 128 * max_pos + key0 + sub * 8;  // key0 + 63 < max_pos
-    uint4 vv[4];
-#pragma unroll
-    for (int dd = 0; dd < 4; ++dd) vv[dd] = *reinterpret_cast<const uint4*>(vb + size_t(rg + 32 * dd) * max_pos);
+    const bool has_new = last && (jnew >> 3) == sub;
     float* myp = part + (size_t(kvhead * 2) * S + s) * 130;  // head 2 kvhead + hh at + hh * S * 130
 #pragma unroll
     for (int dd = 0; dd < 4; ++dd) {
@@ -645,6 +673,11 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
 #pragma unroll
             for (int e = 0; e < 8; ++e)
                 if (sub * 8 + e >= nkeys) vf[e] = 0.f;  // unwritten positions may hold anything
+        }
+        if (has_new) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (sub * 8 + e == jnew) vf[e] = vnew[dim];
         }
         float a0 = 0.f, a1 = 0.f;
 #pragma unroll
@@ -671,98 +704,106 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
 }
 
 // ---------------------------------------------------------------- 22 attention_combine
-// y[h, d] = sum_s 2^(m_s - M) o_s[d] / sum_s 2^(m_s - M) l_s over the splits that hold keys; one block per head.
-__global__ __launch_bounds__(128) void k_attn_combine(const float* part, float* y, const uint32_t* state, int splits,
+// y[h, d] = sum_s 2^(m_s - M) o_s[d] / sum_s 2^(m_s - M) l_s over the splits that hold keys; one block per head, the
+// splits spread over the threads (every load of a pass is independent of the others).
+constexpr int kMaxSplits = 1024;
+__global__ __launch_bounds__(256) void k_attn_combine(const float* part, float* y, const uint32_t* state, int splits,
                                                       int max_pos) {
-    const int h = blockIdx.x, d = threadIdx.x;
+    __shared__ float sc[kMaxSplits];
+    __shared__ float red[4];
+    __shared__ float o_hi[128];
+    const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int pos = int(state[0]);
     if (pos < 0 || pos >= max_pos) return;
     const int used = min(pos / 64 + 1, splits);
     const float* hp = part + size_t(h) * splits * 130;
-    float M = -INFINITY;
-    for (int i = 0; i < used; ++i) M = fmaxf(M, hp[size_t(i) * 130]);
-    float L = 0.f, O = 0.f;
-    for (int i = 0; i < used; ++i) {
-        const float* pi = hp + size_t(i) * 130;
-        const float sc = exp2f(pi[0] - M);
-        L = fmaf(pi[1], sc, L);
-        O = fmaf(pi[2 + d], sc, O);
+    float m = -INFINITY;
+    for (int i = t; i < used; i += 256) m = fmaxf(m, hp[size_t(i) * 130]);
+    m = wave_max(m);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float l = 0.f;
+    for (int i = t; i < used; i += 256) {
+        const float e = exp2f(hp[size_t(i) * 130] - M);
+        sc[i] = e;
+        l = fmaf(hp[size_t(i) * 130 + 1], e, l);
     }
-    y[h * 128 + d] = O / L;
+    l = wave_sum(l);
+    if (lane == 0) red[wv] = l;
+    __syncthreads();
+    const float L = (red[0] + red[1]) + (red[2] + red[3]);
+    const int d = t & 127, par = t >> 7;  // dim d over the splits of parity par
+    float o = 0.f;
+#pragma unroll 4
+    for (int i = par; i < used; i += 2) o = fmaf(hp[size_t(i) * 130 + 2 + d], sc[i], o);
+    if (par == 1) o_hi[d] = o;
+    __syncthreads();
+    if (par == 0) y[h * 128 + d] = (o + o_hi[d]) / L;
 }
 
 // ---------------------------------------------------------------- 23 gemv_residual_dec: x[n] += w[n] . a
-template <int R>
+template <int NCH>
 __global__ __launch_bounds__(256) void k_gemv_resid_dec(const float* a, const uint16_t* w, float* x, int n, int k) {
-    __shared__ __attribute__((aligned(16))) float xs[kMaxHidden];
-    load_x_norm(a, nullptr, 0.f, k, xs, nullptr);
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + wv) * R;
-    if (row0 >= n) return;
-    const uint16_t* rows[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = w + size_t(min(row0 + r, n - 1)) * k;
-    float out[R];
-    wave_rows_dot<R>(rows, xs, k, out);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-        if (lane == r && row0 + r < n) x[row0 + r] += out[r];
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n) return;
+    uint4 wv[NCH];
+    float av[NCH][8];
+    load_chunks_16<NCH>(w + size_t(row) * k, k, wv);
+    load_chunks_f32<NCH>(a, k, av);
+    const float out = dot_chunks<NCH>(wv, av);
+    if ((threadIdx.x & 63) == 0) x[row] += out;
 }
 
 // ---------------------------------------------------------------- 24 gemv_swiglu_dec: a[j] = silu(g_j . h) * (u_j . h)
-template <int R>
+template <int NCH>
 __global__ __launch_bounds__(256) void k_gemv_swiglu_dec(const float* x, const uint16_t* nw, const uint16_t* w,
                                                          float* y, int inter, int hidden, float eps) {
-    __shared__ __attribute__((aligned(16))) float xs[kMaxHidden];
-    __shared__ float red[4];
-    load_x_norm(x, nw, eps, hidden, xs, red);
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int j0 = (blockIdx.x * 4 + wv) * R;
-    if (j0 >= inter) return;
-    const uint16_t* rows[2 * R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int j = min(j0 + r, inter - 1);
-        rows[r] = w + size_t(j) * hidden;
-        rows[R + r] = w + size_t(inter + j) * hidden;
-    }
-    float out[2 * R];
-    wave_rows_dot<2 * R>(rows, xs, hidden, out);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-        if (lane == r && j0 + r < inter) {
-            const float gv = out[r];
-            y[j0 + r] = gv / (1.0f + __expf(-gv)) * out[R + r];
-        }
+    const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (j >= inter) return;
+    uint4 wg[NCH], wu[NCH], g[NCH];
+    float xv[NCH][8];
+    load_chunks_16<NCH>(w + size_t(j) * hidden, hidden, wg);
+    load_chunks_16<NCH>(w + size_t(inter + j) * hidden, hidden, wu);
+    load_chunks_f32<NCH>(x, hidden, xv);
+    load_chunks_16<NCH>(nw, hidden, g);
+    rmsnorm_chunks<NCH>(xv, g, hidden, eps);
+    const float gv = dot_chunks<NCH>(wg, xv);
+    const float uv = dot_chunks<NCH>(wu, xv);
+    if ((threadIdx.x & 63) == 0) y[j] = gv / (1.0f + __expf(-gv)) * uv;
 }
 
 // ---------------------------------------------------------------- 25 lmhead_dec
-// logits[n] = RMSNorm(x) . E[n] (the tied embedding), rows split evenly over the blocks; each block writes its
-// (max, lowest index) pair to partials, index 0xFFFFFFFE when one of its logits is NaN.
+// logits[n] = RMSNorm(x) . E[n] (the tied embedding), rows split evenly over the blocks, 4 rows per wave at a time;
+// each block writes its (max, lowest index) pair to partials, index 0xFFFFFFFE when one of its logits is NaN.
 constexpr uint32_t kLmheadBlocks = 1024;
+template <int NCH>
 __global__ __launch_bounds__(256) void k_lmhead_dec(const float* x, const uint16_t* nw, const uint16_t* e, float* logits,
                                                     float* part, int vocab, int hidden, float eps, int write_logits) {
-    __shared__ __attribute__((aligned(16))) float xs[kMaxHidden];
-    __shared__ float red[4];
     __shared__ float bv[4];
     __shared__ uint32_t bi[4];
-    load_x_norm(x, nw, eps, hidden, xs, red);
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int per_block = (vocab + int(gridDim.x) - 1) / int(gridDim.x);
+    const int r0 = int(blockIdx.x) * per_block, r1 = min(vocab, r0 + per_block);
+    float xv[NCH][8];
+    {
+        uint4 g[NCH];
+        load_chunks_f32<NCH>(x, hidden, xv);
+        load_chunks_16<NCH>(nw, hidden, g);
+        rmsnorm_chunks<NCH>(xv, g, hidden, eps);
+    }
     float best = -INFINITY;
     uint32_t besti = 0xFFFFFFFFu;
     bool nan = false;
-    const int per_block = (vocab + int(gridDim.x) - 1) / int(gridDim.x);
-    const int r0 = int(blockIdx.x) * per_block, r1 = min(vocab, r0 + per_block);
     for (int row = r0 + wv * 4; row < r1; row += 16) {
-        const uint16_t* rows[4];
+        uint4 w4[4][NCH];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) rows[r] = e + size_t(min(row + r, vocab - 1)) * hidden;
-        float out[4];
-        wave_rows_dot<4>(rows, xs, hidden, out);
+        for (int r = 0; r < 4; ++r) load_chunks_16<NCH>(e + size_t(min(row + r, vocab - 1)) * hidden, hidden, w4[r]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+            const float v = dot_chunks<NCH>(w4[r], xv);
             if (row + r >= r1) continue;
-            const float v = out[r];
             if (write_logits && lane == r) logits[row + r] = v;
             if (v != v) {
                 nan = true;
@@ -968,20 +1009,36 @@ static void l_gemm_f32(const PreparedDispatch& pd, void* const* p, hipStream_t s
     hipLaunchKernelGGL(k_gemm<EPI_F32>, dim3((w[5] + GBN - 1) / GBN, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
 }
 
-// The decode GEMVs give each wave R consecutive rows; 4 waves per block.
-static uint32_t gemv_blocks(uint32_t n, uint32_t r) { return (n + 4 * r - 1) / (4 * r); }
-static uint32_t gemv_rows_per_wave(uint32_t n) { return n >= 4096 ? 4 : 1; }
+// The decode GEMVs: one row (or gate/up pair) per wave, 4 waves per block; NCH, the 512-wide k-chunks per lane, is
+// rounded up to one of the compiled widths.
+static uint32_t gemv_blocks(uint32_t rows) { return (rows + 3) / 4; }
+static int nch_bucket(uint32_t k) {
+    const uint32_t c = (k + 511) / 512;
+    for (int b : {1, 2, 3, 4, 6, 8, 12, 16})
+        if (c <= uint32_t(b)) return b;
+    return 0;
+}
+#define NCH_DISPATCH(K, LAUNCH)                 \
+    switch (nch_bucket(K)) {                    \
+        case 1: LAUNCH(1); break;               \
+        case 2: LAUNCH(2); break;               \
+        case 3: LAUNCH(3); break;               \
+        case 4: LAUNCH(4); break;               \
+        case 6: LAUNCH(6); break;               \
+        case 8: LAUNCH(8); break;               \
+        case 12: LAUNCH(12); break;             \
+        case 16: LAUNCH(16); break;             \
+        default: break;                         \
+    }
 
 // 20 gemv_norm_dec: x, norm, w, y, n, k, eps
 static void l_gemv_norm(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    const uint32_t n = w[5], R = gemv_rows_per_wave(n);
-    if (R == 4)
-        hipLaunchKernelGGL(k_gemv_norm_dec<4>, dim3(gemv_blocks(n, 4)), dim3(256), 0, s, (const float*)p[0],
-                           (const uint16_t*)p[1], (const uint16_t*)p[2], (float*)p[3], int(n), int(w[6]), f32_of(w[7]));
-    else
-        hipLaunchKernelGGL(k_gemv_norm_dec<1>, dim3(gemv_blocks(n, 1)), dim3(256), 0, s, (const float*)p[0],
-                           (const uint16_t*)p[1], (const uint16_t*)p[2], (float*)p[3], int(n), int(w[6]), f32_of(w[7]));
+#define L_NORM(N)                                                                                                    \
+    hipLaunchKernelGGL(k_gemv_norm_dec<N>, dim3(gemv_blocks(w[5])), dim3(256), 0, s, (const float*)p[0],            \
+                       (const uint16_t*)p[1], (const uint16_t*)p[2], (float*)p[3], int(w[5]), int(w[6]), f32_of(w[7]))
+    NCH_DISPATCH(w[6], L_NORM)
+#undef L_NORM
 }
 
 // 21 attention_decode_f16: qkv, q_norm, k_norm, cos, sin, k_cache, v_cache, partials, state, q_heads, kv_heads,
@@ -999,36 +1056,39 @@ static void l_attn_dec(const PreparedDispatch& pd, void* const* p, hipStream_t s
 static void l_attn_combine(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     const int max_pos = int(w[5]);
-    hipLaunchKernelGGL(k_attn_combine, dim3(w[4]), dim3(128), 0, s, (const float*)p[0], (float*)p[1],
+    hipLaunchKernelGGL(k_attn_combine, dim3(w[4]), dim3(256), 0, s, (const float*)p[0], (float*)p[1],
                        (const uint32_t*)p[2], max_pos / 64, max_pos);
 }
 
 // 23 gemv_residual_dec: a, w, x, n, k
 static void l_gemv_resid(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    const uint32_t n = w[4], R = gemv_rows_per_wave(n);
-    if (R == 4)
-        hipLaunchKernelGGL(k_gemv_resid_dec<4>, dim3(gemv_blocks(n, 4)), dim3(256), 0, s, (const float*)p[0],
-                           (const uint16_t*)p[1], (float*)p[2], int(n), int(w[5]));
-    else
-        hipLaunchKernelGGL(k_gemv_resid_dec<1>, dim3(gemv_blocks(n, 1)), dim3(256), 0, s, (const float*)p[0],
-                           (const uint16_t*)p[1], (float*)p[2], int(n), int(w[5]));
+#define L_RESID(N)                                                                                                   \
+    hipLaunchKernelGGL(k_gemv_resid_dec<N>, dim3(gemv_blocks(w[4])), dim3(256), 0, s, (const float*)p[0],           \
+                       (const uint16_t*)p[1], (float*)p[2], int(w[4]), int(w[5]))
+    NCH_DISPATCH(w[5], L_RESID)
+#undef L_RESID
 }
 
 // 24 gemv_swiglu_dec: x, norm, w, y, inter, hidden, eps
 static void l_gemv_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    hipLaunchKernelGGL(k_gemv_swiglu_dec<2>, dim3(gemv_blocks(w[5], 2)), dim3(256), 0, s, (const float*)p[0],
-                       (const uint16_t*)p[1], (const uint16_t*)p[2], (float*)p[3], int(w[5]), int(w[6]),
-                       f32_of(w[7]));
+#define L_SWIGLU(N)                                                                                                  \
+    hipLaunchKernelGGL(k_gemv_swiglu_dec<N>, dim3(gemv_blocks(w[5])), dim3(256), 0, s, (const float*)p[0],          \
+                       (const uint16_t*)p[1], (const uint16_t*)p[2], (float*)p[3], int(w[5]), int(w[6]), f32_of(w[7]))
+    NCH_DISPATCH(w[6], L_SWIGLU)
+#undef L_SWIGLU
 }
 
 // 25 lmhead_dec: x, norm, embed, logits, partials, vocab, hidden, eps, write_logits
 static void l_lmhead(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    hipLaunchKernelGGL(k_lmhead_dec, dim3(kLmheadBlocks), dim3(256), 0, s, (const float*)p[0], (const uint16_t*)p[1],
-                       (const uint16_t*)p[2], (float*)p[3], (float*)p[4], int(w[6]), int(w[7]), f32_of(w[8]),
-                       int(w[9]));
+#define L_LM(N)                                                                                                      \
+    hipLaunchKernelGGL(k_lmhead_dec<N>, dim3(kLmheadBlocks), dim3(256), 0, s, (const float*)p[0],                   \
+                       (const uint16_t*)p[1], (const uint16_t*)p[2], (float*)p[3], (float*)p[4], int(w[6]), int(w[7]), \
+                       f32_of(w[8]), int(w[9]))
+    NCH_DISPATCH(w[7], L_LM)
+#undef L_LM
 }
 
 // 26 argmax_dec: partials, state, out_ids, max_steps
@@ -1094,7 +1154,8 @@ static void need_k(const char* k, uint32_t n) {
 }
 
 static void need_max_pos(const char* k, uint32_t mp) {
-    if (mp < 64 || mp % 64) contract_fail("%s: max_pos must be a positive multiple of 64", k);
+    if (mp < 64 || mp % 64 || mp > 64u * kMaxSplits)
+        contract_fail("%s: max_pos must be a multiple of 64 in 64 .. %d", k, 64 * kMaxSplits);
 }
 
 std::vector<KernelSpec> fast_catalog() {
@@ -1178,7 +1239,7 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 20 gemv_norm_dec: x, norm, w, y, n, k, eps
     c.push_back({"gemv_norm_dec", "fast", {256, 1, 1}, true,
-                 [](const uint32_t* w) { return Grid3{gemv_blocks(w[5], gemv_rows_per_wave(w[5])), 1, 1}; },
+                 [](const uint32_t* w) { return Grid3{gemv_blocks(w[5]), 1, 1}; },
                  {TOK_R("x", DT(F32)), TOK_R("norm", DT(BF16)), TOK_R("w", DT(BF16)), TOK_W("y", DT(F32)), U32F("n"),
                   U32F("k"), F32F("eps")},
                  [](const uint32_t* w, const uint32_t* c) {
@@ -1211,7 +1272,7 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 8, 3, "attention_decode_f16", "state");
                  }});
     // 22 attention_combine: partials, y, state, q_heads, max_pos
-    c.push_back({"attention_combine", "fast", {128, 1, 1}, true, [](const uint32_t* w) { return Grid3{w[4], 1, 1}; },
+    c.push_back({"attention_combine", "fast", {256, 1, 1}, true, [](const uint32_t* w) { return Grid3{w[4], 1, 1}; },
                  {TOK_R("partials", DT(F32)), TOK_W("y", DT(F32)), TOK_R("state", DT(U32)), U32F("q_heads"),
                   U32F("max_pos")},
                  [](const uint32_t* w, const uint32_t* c) {
@@ -1223,7 +1284,7 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 23 gemv_residual_dec: a, w, x, n, k
     c.push_back({"gemv_residual_dec", "fast", {256, 1, 1}, true,
-                 [](const uint32_t* w) { return Grid3{gemv_blocks(w[4], gemv_rows_per_wave(w[4])), 1, 1}; },
+                 [](const uint32_t* w) { return Grid3{gemv_blocks(w[4]), 1, 1}; },
                  {TOK_R("a", DT(F32)), TOK_R("w", DT(BF16)), TOK_RW("x", DT(F32)), U32F("n"), U32F("k")},
                  [](const uint32_t* w, const uint32_t* c) {
                      need_k("gemv_residual_dec", w[5]);
@@ -1234,7 +1295,7 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 24 gemv_swiglu_dec: x, norm, w, y, inter, hidden, eps
     c.push_back({"gemv_swiglu_dec", "fast", {256, 1, 1}, true,
-                 [](const uint32_t* w) { return Grid3{gemv_blocks(w[5], 2), 1, 1}; },
+                 [](const uint32_t* w) { return Grid3{gemv_blocks(w[5]), 1, 1}; },
                  {TOK_R("x", DT(F32)), TOK_R("norm", DT(BF16)), TOK_R("w", DT(BF16)), TOK_W("y", DT(F32)),
                   U32F("inter"), U32F("hidden"), F32F("eps")},
                  [](const uint32_t* w, const uint32_t* c) {

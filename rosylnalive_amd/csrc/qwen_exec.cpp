@@ -182,7 +182,7 @@ QwenExec::QwenExec(Device& dev, const QwenConfig& cfg, const uint32_t* inv_freq_
             arg_fail("the fast path takes head_dim 128 and two query heads per KV head");
         if (c.hidden % 64 || c.intermediate % 64 || c.hidden > 8192 || c.intermediate > 8192 || c.heads * 128 > 8192)
             arg_fail("the fast path takes hidden and intermediate multiples of 64 up to 8192, and heads * 128 <= 8192");
-        if (c.max_pos % 64) arg_fail("the fast path takes max_pos a multiple of 64");
+        if (c.max_pos % 64 || c.max_pos > 65536) arg_fail("the fast path takes max_pos a multiple of 64 up to 65536");
         if (c.batch != 1) arg_fail("batched decode is not built yet: batch must be 1");
     }
     if (!dev_.kernels_loaded()) dev_.load_kernels();
@@ -407,13 +407,17 @@ uint32_t QwenExec::forward(int seq, int pos0, const int32_t* ids, int t_, float*
     uint32_t am = 0xFFFFFFFFu;
     // chunked prefill: max_tokens rows at a time, the cache carrying the earlier chunks
     for (int c0 = 0; c0 < t_; c0 += c.max_tokens) {
-        int n = std::min(c.max_tokens, t_ - c0);
-        int want = std::max(0, logits_rows - (t_ - (c0 + n)));  // logits rows that fall in this chunk
+        const int n = std::min(c.max_tokens, t_ - c0);
+        // the requested rows [t - logits_rows, t) that fall in this chunk: a suffix of it, `want` rows long, landing
+        // at row `out0` of the caller's buffer
+        const int first = std::max(c0, t_ - logits_rows);
+        const int want = std::max(0, c0 + n - first);
+        const int out0 = first - (t_ - logits_rows);
         std::vector<uint32_t> u(static_cast<size_t>(n));
         for (int i = 0; i < n; ++i) u[size_t(i)] = uint32_t(ids[c0 + i]);
         upload_tensor("ids", u.data(), uint64_t(n) * 4);
-        // only the chunks holding some of the last logits_rows rows write into the caller's buffer
-        float* lg = (logits && want > 0) ? logits + size_t(logits_rows - want) * c.vocab : nullptr;
+        // only the chunks holding some of the requested rows write into the caller's buffer
+        float* lg = (logits && want > 0) ? logits + size_t(out0) * c.vocab : nullptr;
         if (c.mode == 1)
             am = forward_fast(seq, pos0 + c0, n, lg, std::max(want, 1));
         else
