@@ -24,6 +24,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 FP32_PEAK_TFLOPS = 157.3
+GEMV_SWIGLU_TRAFFIC_BYTES = 12675736  # measured HBM bytes per gemv_swiglu_dec launch at the 0.6B shape
 
 
 def log(*a):
@@ -102,6 +103,14 @@ def main():
     k_gbs = k_bytes / (k_us * 1e-6) / 1e9
     log(f"gemv_swiglu_dec: {k_us:.2f} us per launch, {k_gbs:.0f} GB/s ({k_gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
 
+    # a plain copy of known size (scale_f32 by 1: 8 MiB read, 8 MiB written), the reference that the HBM byte
+    # counters of a profiling run are scaled by
+    cl = backend.begin()
+    n_copy = 2048 * H
+    cl.dispatch("scale_f32", ArgBlock.encode("scale_f32", x=tok("x"), y=tok("logits"), n=n_copy, a=1.0))
+    backend.wait(backend.submit(cl))
+    cl.release()
+
     out = {
         "metric": "Qwen3-0.6B prefill & decode tok/s on 1 MI355X; % of HBM/MFMA roofline",
         "value": round(tok_s, 2),
@@ -128,7 +137,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(k_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            # HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the same counters on the 8 MiB copy
+            # above (profiles/decode_gemv_traffic_qwen3_0.6b.md)
+            "traffic": GEMV_SWIGLU_TRAFFIC_BYTES,
             "bytes_per_launch": k_bytes,
             "us_per_launch": round(k_us, 3),
         },
