@@ -24,6 +24,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <type_traits>
 
 #include "device.hpp"
 #include "fast_common.hpp"
@@ -80,93 +81,122 @@ struct GemmArgs {
     float eps;
 };
 
-template <int EPI>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * (GBM + GBN) * GLD];
+template <int EPI, int BN>
+__global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
+    static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID)), "SwiGLU and QKV pair 128 columns");
+    constexpr int WN = BN / 2, JT = WN / 16, BCH = BN / 32;  // columns per wave, MFMA tiles per wave, B chunks/thread
+    constexpr int STAGE = (GBM + BN) * GLD;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1, g = lane >> 4, c16 = lane & 15;
     const int m0 = blockIdx.y * GBM;
-    const int n0 = blockIdx.x * GBN;
+    const int n0 = blockIdx.x * BN;
 
-    // the rows this thread loads: chunk c = t + 256 i -> row c / 8, 16-byte column (c % 8)
-    const uint16_t* arow[4];
-    const uint16_t* brow[4];
+    // the rows this thread loads: chunk c = t + 256 i -> row c / 8, 16-byte column (c % 8); element offsets from the
+    // matrix base (the caller keeps every matrix under 2^31 elements), -1 for a row past the matrix
+    int aoff[4], boff[BCH];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
-        int m = m0 + r;
-        arow[i] = m < p.M ? p.a + size_t(m) * p.K + kc : nullptr;
+        const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
+        const int m = m0 + r;
+        aoff[i] = m < p.M ? m * p.K + kc : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+        const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
         int n;
         if (EPI == EPI_SWIGLU) {
-            int j = blockIdx.x * 64 + (r & 63);
+            const int j = blockIdx.x * 64 + (r & 63);
             n = j < p.inter ? (r < 64 ? j : p.inter + j) : -1;
         } else {
             n = n0 + r < p.N ? n0 + r : -1;
         }
-        brow[i] = n >= 0 ? p.w + size_t(n) * p.K + kc : nullptr;
+        boff[i] = n >= 0 ? n * p.K + kc : -1;
     }
-    uint4 ra[4], rb[4];
-    auto gload = [&](int k0) {
+    // two register sets: tile j is loaded into set j % 2 two iterations before it is multiplied
+    uint4 ra[2][4], rb[2][BCH];
+    auto gload = [&](auto set, int k0) {
+        constexpr int S = decltype(set)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ra[i] = arow[i] ? *reinterpret_cast<const uint4*>(arow[i] + k0) : make_uint4(0, 0, 0, 0);
-            rb[i] = brow[i] ? *reinterpret_cast<const uint4*>(brow[i] + k0) : make_uint4(0, 0, 0, 0);
-        }
+        for (int i = 0; i < 4; ++i)
+            ra[S][i] = aoff[i] >= 0 ? *reinterpret_cast<const uint4*>(p.a + (aoff[i] + k0)) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < BCH; ++i)
+            rb[S][i] = boff[i] >= 0 ? *reinterpret_cast<const uint4*>(p.w + (boff[i] + k0)) : make_uint4(0, 0, 0, 0);
     };
-    auto sstore = [&](int buf) {
-        uint16_t* As = lds + buf * (GBM + GBN) * GLD;
+    auto sstore = [&](auto set, int buf) {
+        constexpr int S = decltype(set)::value;
+        uint16_t* As = lds + buf * STAGE;
         uint16_t* Bs = As + GBM * GLD;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
-            *reinterpret_cast<uint4*>(As + r * GLD + kc) = ra[i];
-            *reinterpret_cast<uint4*>(Bs + r * GLD + kc) = rb[i];
+            const int c = t + 256 * i;
+            *reinterpret_cast<uint4*>(As + (c >> 3) * GLD + (c & 7) * 8) = ra[S][i];
+        }
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            const int c = t + 256 * i;
+            *reinterpret_cast<uint4*>(Bs + (c >> 3) * GLD + (c & 7) * 8) = rb[S][i];
         }
     };
 
-    f32x4 acc[4][4];
+    f32x4 acc[4][JT];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < JT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nk = p.K / GBK;
-    gload(0);
-    sstore(0);
-    if (nk > 1) gload(GBK);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) {
-            sstore(buf ^ 1);                         // tile kt + 1, whose loads were issued one iteration ago
-            if (kt + 2 < nk) gload((kt + 2) * GBK);  // tile kt + 2 is in flight during this tile's MFMAs
-        }
-        const uint16_t* As = lds + buf * (GBM + GBN) * GLD;
+    auto mma = [&](int buf) {
+        const uint16_t* As = lds + buf * STAGE;
         const uint16_t* Bs = As + GBM * GLD;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            f16x8 af[4], bfr[4];
+            f16x8 af[4], bfr[JT];
             const int kof = ks * 32 + 8 * g;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 af[i] = as_f16x8(*reinterpret_cast<const uint4*>(As + (wm * 64 + i * 16 + c16) * GLD + kof));
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                bfr[j] = as_f16x8(*reinterpret_cast<const uint4*>(Bs + (wn * 64 + j * 16 + c16) * GLD + kof));
+            for (int j = 0; j < JT; ++j)
+                bfr[j] = as_f16x8(*reinterpret_cast<const uint4*>(Bs + (wn * WN + j * 16 + c16) * GLD + kof));
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < JT; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bfr[j], acc[i][j], 0, 0, 0);
         }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    // iteration kt: store tile kt + 1 (set (kt + 1) % 2) into the other LDS buffer, refill that set with tile kt + 3,
+    // multiply tile kt
+    auto step = [&](auto par, int kt, int nk) {
+        constexpr int P = decltype(par)::value;  // kt % 2
+        using Next = std::integral_constant<int, 1 - P>;
+        if (kt + 1 < nk) {
+            sstore(Next{}, 1 - P);
+            if (kt + 3 < nk) gload(Next{}, (kt + 3) * GBK);
+        }
+        mma(P);
         __syncthreads();
+    };
+
+    const int nk = p.K / GBK;
+    gload(S0{}, 0);
+    sstore(S0{}, 0);
+    if (nk > 1) gload(S1{}, GBK);
+    if (nk > 2) gload(S0{}, 2 * GBK);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(S0{}, kt, nk);
+        if (kt + 1 < nk) step(S1{}, kt + 1, nk);
     }
 
     if (EPI == EPI_F32 || EPI == EPI_RESID) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                int n = n0 + wn * 64 + j * 16 + c16;
+            for (int j = 0; j < JT; ++j) {
+                int n = n0 + wn * WN + j * 16 + c16;
                 if (n >= p.N) continue;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -192,31 +222,34 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
     }
     __syncthreads();
     if (wn == 1) return;
-    float hi[4][4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
+    // the partner half of row tile i, read back from LDS
+    auto load_hi = [&](int i, float (&hi)[4][4]) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) hi[i][j][r] = x32[((wm * 16 + i * 4 + j) * 4 + r) * 64 + lane];
+            for (int r = 0; r < 4; ++r) hi[j][r] = x32[((wm * 16 + i * 4 + j) * 4 + r) * 64 + lane];
+    };
 
     if (EPI == EPI_SWIGLU) {
         // a[m, j0 + c] = silu(gate) * up, silu(g) = g / (1 + exp(-g))
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+            float hi[4][4];
+            load_hi(i, hi);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                int col = blockIdx.x * 64 + j * 16 + c16;
+                const int col = blockIdx.x * 64 + j * 16 + c16;
                 if (col >= p.inter) continue;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    int m = m0 + wm * 64 + i * 16 + 4 * g + r;
+                    const int m = m0 + wm * 64 + i * 16 + 4 * g + r;
                     if (m >= p.M) continue;
-                    float gv = acc[i][j][r];
-                    float s = gv / (1.0f + __expf(-gv));
-                    p.y16[size_t(m) * p.inter + col] = f2h(s * hi[i][j][r]);
+                    const float gv = acc[i][j][r];
+                    const float sg = gv / (1.0f + __expf(-gv));
+                    p.y16[size_t(m) * p.inter + col] = f2h(sg * hi[j][r]);
                 }
             }
+        }
         return;
     }
 
@@ -226,12 +259,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
     const uint16_t* nw = is_q ? p.qn : p.kn;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+        float hi[4][4];
+        load_hi(i, hi);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = m0 + wm * 64 + i * 16 + 4 * g + r;  // the same for the 16 lanes of group g
             float ss = 0.f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) ss = fmaf(acc[i][j][r], acc[i][j][r], fmaf(hi[i][j][r], hi[i][j][r], ss));
+            for (int j = 0; j < 4; ++j) ss = fmaf(acc[i][j][r], acc[i][j][r], fmaf(hi[j][r], hi[j][r], ss));
             ss += __shfl_xor(ss, 1, 64);
             ss += __shfl_xor(ss, 2, 64);
             ss += __shfl_xor(ss, 4, 64);
@@ -242,11 +277,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int c = j * 16 + c16;  // 0..63
-                float lo = acc[i][j][r], h2 = hi[i][j][r];
+                float lo = acc[i][j][r], h2 = hi[j][r];
                 if (is_q || is_k) {
-                    float a = bf2f(nw[c]) * (lo * rr);
-                    float b = bf2f(nw[c + 64]) * (h2 * rr);
-                    float cs = p.cos_t[size_t(pos) * 64 + c], sn = p.sin_t[size_t(pos) * 64 + c];
+                    const float a = bf2f(nw[c]) * (lo * rr);
+                    const float b = bf2f(nw[c + 64]) * (h2 * rr);
+                    const float cs = p.cos_t[size_t(pos) * 64 + c], sn = p.sin_t[size_t(pos) * 64 + c];
                     lo = a * cs - b * sn;
                     h2 = b * cs + a * sn;
                 }
@@ -269,46 +304,44 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
 }
 
 // ================================================================ 16 attention_prefill_f16
-// Causal GQA flash attention, two query heads per KV head. A workgroup takes 64 query rows of both heads of one KV
-// group (128 query columns, 32 per wave) and streams 64-key blocks of K and V^T through LDS, shared by both heads;
-// the next block's K and V^T are fetched into registers while the current one is multiplied.
+// Causal GQA flash attention, two query heads per KV head. A workgroup takes 32 query rows of both heads of one KV
+// group (64 query columns: wave w owns head 2 kvhead + w / 2, rows (w % 2) * 16 .. + 15, one MFMA column tile) and
+// streams 64-key blocks of K and V^T through LDS, shared by the four waves; the next block's K and V^T are fetched
+// into registers while the current one is multiplied. Blocks are issued longest first, and 32-row tiles give twice
+// as many blocks as CUs at T = 2048, so the causal triangle packs onto the CUs.
 // S^T = K Q^T (A = K rows from LDS, B = Q^T from registers) puts one query per lane column, so the online-softmax
 // statistics stay per lane; P^T is then already in the B-operand layout of O^T = V^T P^T once the key slots of the
 // k-step are ordered {4g .. 4g + 3, 16 + 4g .. 16 + 4g + 3}; V^T is read in the same order, so the sum runs over the
 // same keys.
+constexpr int kAttnRows = 32;
 __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                                       uint16_t* y, int T, int past, int qh, int max_pos,
                                                       float scale_log2) {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[64 * 136];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[128 * 72];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, g = lane >> 4, c16 = lane & 15;
-    const int ntile = (T + 63) / 64;
-    const int row0 = (ntile - 1 - int(blockIdx.x)) * 64;  // the longest tiles start first
+    const int ntile = (T + kAttnRows - 1) / kAttnRows;
+    const int row0 = (ntile - 1 - int(blockIdx.x)) * kAttnRows;  // the longest tiles start first
     const int kvhead = blockIdx.y;
     const int head = kvhead * 2 + (w >> 1);
-    const int wrow0 = row0 + (w & 1) * 32;
+    const int row = row0 + (w & 1) * 16 + c16;  // this lane's query row
     const int QC = qh * 128;
 
-    f16x8 qf[2][4];
+    f16x8 qf[4];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        int row = wrow0 + nt * 16 + c16;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (row < T) v = *reinterpret_cast<const uint4*>(q + size_t(row) * QC + head * 128 + ks * 32 + 8 * g);
-            qf[nt][ks] = as_f16x8(v);
-        }
+    for (int ks = 0; ks < 4; ++ks) {
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (row < T) v = *reinterpret_cast<const uint4*>(q + size_t(row) * QC + head * 128 + ks * 32 + 8 * g);
+        qf[ks] = as_f16x8(v);
     }
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
-    f32x4 o[8][2];
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 o[8];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int last_row = min(row0 + 63, T - 1);
+    const int last_row = min(row0 + kAttnRows - 1, T - 1);
     const int kend = past + last_row + 1;  // keys [0, kend) are visible to some row of the tile; kend <= max_pos
+    const int qpos = past + row;
     const uint16_t* kbase = kc + size_t(kvhead) * max_pos * 128;
     const uint16_t* vbase = vc + size_t(kvhead) * 128 * max_pos;
 
@@ -316,13 +349,13 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
     auto fetch = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int c = t + 256 * i, key = c >> 4, dc = (c & 15) * 8;
+            const int c = t + 256 * i, key = c >> 4, dc = (c & 15) * 8;
             rk[i] = kb + key < kend ? *reinterpret_cast<const uint4*>(kbase + size_t(kb + key) * 128 + dc)
                                     : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int c = t + 256 * i, d = c >> 3, k8 = (c & 7) * 8;
+            const int c = t + 256 * i, d = c >> 3, k8 = (c & 7) * 8;
             uint4 v = make_uint4(0, 0, 0, 0);
             if (kb + k8 < kend) {  // kb + k8 + 7 < max_pos: kb, k8 are multiples of 64 and 8, max_pos of 64
                 v = *reinterpret_cast<const uint4*>(vbase + size_t(d) * max_pos + kb + k8);
@@ -343,103 +376,80 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int c = t + 256 * i;
+            const int c = t + 256 * i;
             *reinterpret_cast<uint4*>(Ks + (c >> 4) * 136 + (c & 15) * 8) = rk[i];
             *reinterpret_cast<uint4*>(Vt + (c >> 3) * 72 + (c & 7) * 8) = rv[i];
         }
         __syncthreads();
         if (kb + 64 < kend) fetch(kb + 64);  // in flight during this block's MFMAs
 
-        f32x4 s[4][2];
+        f32x4 s[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) s[kt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kt = 0; kt < 4; ++kt) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
-                f16x8 a = as_f16x8(*reinterpret_cast<const uint4*>(Ks + (kt * 16 + c16) * 136 + ks * 32 + 8 * g));
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-                    s[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[nt][ks], s[kt][nt], 0, 0, 0);
+                const f16x8 a = as_f16x8(*reinterpret_cast<const uint4*>(Ks + (kt * 16 + c16) * 136 + ks * 32 + 8 * g));
+                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ks], s[kt], 0, 0, 0);
             }
 
-        uint32_t pb[2][2][4];  // [kk][nt]: the B operand of O^T for the keys of k-step kk, packed f16 pairs
+        float mloc = -INFINITY;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const int row = wrow0 + nt * 16 + c16;
-            const int qpos = past + row;
-            float mloc = -INFINITY;
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    int key = kb + kt * 16 + 4 * g + r;
-                    float v = s[kt][nt][r] * scale_log2;
-                    if (row >= T || key > qpos) v = -INFINITY;
-                    s[kt][nt][r] = v;
-                    mloc = fmaxf(mloc, v);
-                }
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-            const float m_new = fmaxf(m_run[nt], mloc);
-            const float m_use = m_new == -INFINITY ? 0.f : m_new;
-            const float alpha = exp2f(m_run[nt] - m_use);
-            float lsum = 0.f;
-            float pv[4][4];
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    pv[kt][r] = exp2f(s[kt][nt][r] - m_use);
-                    lsum += pv[kt][r];
-                }
-            lsum += __shfl_xor(lsum, 16, 64);
-            lsum += __shfl_xor(lsum, 32, 64);
-            l_run[nt] = l_run[nt] * alpha + lsum;
-            m_run[nt] = m_new;
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) o[dt][nt][r] *= alpha;
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                pb[kk][nt][0] = pack2h(pv[2 * kk][0], pv[2 * kk][1]);
-                pb[kk][nt][1] = pack2h(pv[2 * kk][2], pv[2 * kk][3]);
-                pb[kk][nt][2] = pack2h(pv[2 * kk + 1][0], pv[2 * kk + 1][1]);
-                pb[kk][nt][3] = pack2h(pv[2 * kk + 1][2], pv[2 * kk + 1][3]);
+            for (int r = 0; r < 4; ++r) {
+                const int key = kb + kt * 16 + 4 * g + r;
+                float v = s[kt][r] * scale_log2;
+                if (row >= T || key > qpos) v = -INFINITY;
+                s[kt][r] = v;
+                mloc = fmaxf(mloc, v);
             }
-        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = exp2f(m_run - m_use);
+        float lsum = 0.f;
+        float pv[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pv[kt][r] = exp2f(s[kt][r] - m_use);
+                lsum += pv[kt][r];
+            }
+        lsum += __shfl_xor(lsum, 16, 64);
+        lsum += __shfl_xor(lsum, 32, 64);
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[dt][r] *= alpha;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            f16x8 bq[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-                bq[nt] = as_f16x8(make_uint4(pb[kk][nt][0], pb[kk][nt][1], pb[kk][nt][2], pb[kk][nt][3]));
+            const f16x8 bq = as_f16x8(make_uint4(pack2h(pv[2 * kk][0], pv[2 * kk][1]), pack2h(pv[2 * kk][2], pv[2 * kk][3]),
+                                                 pack2h(pv[2 * kk + 1][0], pv[2 * kk + 1][1]),
+                                                 pack2h(pv[2 * kk + 1][2], pv[2 * kk + 1][3])));
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
                 const uint16_t* vr = Vt + (dt * 16 + c16) * 72 + kk * 32 + 4 * g;
-                uint2 lo = *reinterpret_cast<const uint2*>(vr);
-                uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-                f16x8 a = as_f16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-                    o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[nt], o[dt][nt], 0, 0, 0);
+                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+                const f16x8 a = as_f16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, o[dt], 0, 0, 0);
             }
         }
     }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int row = wrow0 + nt * 16 + c16;
-        if (row >= T) continue;
-        const float inv = 1.0f / l_run[nt];
+    if (row < T) {
+        const float inv = 1.0f / l_run;
         uint16_t* yr = y + size_t(row) * QC + head * 128;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             uint2 v;
-            v.x = pack2h(o[dt][nt][0] * inv, o[dt][nt][1] * inv);
-            v.y = pack2h(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
+            v.x = pack2h(o[dt][0] * inv, o[dt][1] * inv);
+            v.y = pack2h(o[dt][2] * inv, o[dt][3] * inv);
             *reinterpret_cast<uint2*>(yr + dt * 16 + 4 * g) = v;
         }
     }
@@ -929,6 +939,75 @@ __global__ void k_convert_bf16_f16(const uint16_t* x, uint16_t* y, uint64_t n) {
     }
 }
 
+// ---------------------------------------------------------------- 30 argmax_rows_partial, 31 argmax_rows_final
+// argmaxRows over logits rows in two passes: block (b, r) reduces columns [b per, (b + 1) per) of row r to (max, lowest
+// index) or a NaN mark, then one wave per row merges the kArgmaxParts pairs: the lowest index of the row maximum, or
+// 0xFFFFFFFF for a row holding a NaN (CpuRef.argmaxRows semantics, CpuRef.fs:453-467).
+constexpr int kArgmaxParts = 64;
+
+struct ArgBest {
+    float v;
+    uint32_t i;  // 0xFFFFFFFF: none yet
+};
+
+__device__ __forceinline__ ArgBest arg_merge(ArgBest a, ArgBest b) {
+    if (b.i != 0xFFFFFFFFu && (a.i == 0xFFFFFFFFu || b.v > a.v || (b.v == a.v && b.i < a.i))) return b;
+    return a;
+}
+
+__device__ __forceinline__ ArgBest arg_wave(ArgBest a) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        ArgBest b{__shfl_xor(a.v, o, 64), uint32_t(__shfl_xor(int(a.i), o, 64))};
+        a = arg_merge(a, b);
+    }
+    return a;
+}
+
+__global__ __launch_bounds__(256) void k_argmax_partial(const float* x, float* part, int rows, int cols) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    __shared__ int snan;
+    const int r = blockIdx.y, b = blockIdx.x, t = threadIdx.x;
+    if (t == 0) snan = 0;
+    __syncthreads();
+    const int per = (cols + kArgmaxParts - 1) / kArgmaxParts;
+    const int c0 = b * per, c1 = min(cols, c0 + per);
+    const float* xr = x + size_t(r) * cols;
+    ArgBest best{0.f, 0xFFFFFFFFu};
+    bool nan = false;
+    for (int c = c0 + t; c < c1; c += 256) {  // increasing per thread: the first of equal values is kept
+        const float v = xr[c];
+        if (v != v)
+            nan = true;
+        else if (best.i == 0xFFFFFFFFu || v > best.v)
+            best = ArgBest{v, uint32_t(c)};
+    }
+    if (nan) snan = 1;
+    best = arg_wave(best);
+    if ((t & 63) == 0) {
+        sv[t >> 6] = best.v;
+        si[t >> 6] = best.i;
+    }
+    __syncthreads();
+    if (t == 0) {
+        ArgBest a{sv[0], si[0]};
+        for (int i = 1; i < 4; ++i) a = arg_merge(a, ArgBest{sv[i], si[i]});
+        float* pp = part + (size_t(r) * kArgmaxParts + b) * 2;
+        pp[0] = a.v;
+        reinterpret_cast<uint32_t*>(pp)[1] = snan ? 0xFFFFFFFEu : a.i;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_argmax_final(const float* part, uint32_t* out, int rows) {
+    const int r = blockIdx.x, t = threadIdx.x;
+    const float* pp = part + (size_t(r) * kArgmaxParts + t) * 2;
+    const uint32_t i = reinterpret_cast<const uint32_t*>(pp)[1];
+    const bool nan = __any(i == 0xFFFFFFFEu);
+    ArgBest a = arg_wave(ArgBest{pp[0], i == 0xFFFFFFFEu ? 0xFFFFFFFFu : i});
+    if (t == 0) out[r] = nan ? 0xFFFFFFFFu : a.i;
+}
+
 // ================================================================ launchers and catalog entries
 
 static float f32_of(uint32_t b) {
@@ -971,17 +1050,21 @@ static void l_gemm_qkv(const PreparedDispatch& pd, void* const* p, hipStream_t s
     a.pos0 = int(w[14]);
     a.max_pos = int(w[15]);
     a.eps = f32_of(w[16]);
-    hipLaunchKernelGGL(k_gemm<EPI_QKV>, dim3(uint32_t(qh + 2 * kvh), (w[10] + GBM - 1) / GBM), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((k_gemm<EPI_QKV, 128>), dim3(uint32_t(qh + 2 * kvh), (w[10] + GBM - 1) / GBM), dim3(256), 0, s, a);
 }
 
 // 16 attention_prefill_f16: q, k_cache, v_cache, y, rows, past, q_heads, kv_heads, max_pos, scale
 static void l_attn_prefill(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     const int T = int(w[5]);
-    hipLaunchKernelGGL(k_attn_prefill, dim3(uint32_t((T + 63) / 64), w[8]), dim3(256), 0, s, (const uint16_t*)p[0],
+    hipLaunchKernelGGL(k_attn_prefill, dim3(uint32_t((T + kAttnRows - 1) / kAttnRows), w[8]), dim3(256), 0, s, (const uint16_t*)p[0],
                        (const uint16_t*)p[1], (const uint16_t*)p[2], (uint16_t*)p[3], T, int(w[6]), int(w[7]),
                        int(w[9]), f32_of(w[10]) * kLog2e);
 }
+
+// Residual GEMMs with few 128 x 128 tiles (o_proj and down_proj have N = hidden) use 64-wide column tiles so the
+// grid covers the CUs.
+static bool resid_narrow(uint32_t m, uint32_t n) { return ((m + 127) / 128) * ((n + 127) / 128) < 512; }
 
 // 17 gemm_residual: a, w, x, m, n, k
 static void l_gemm_resid(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
@@ -989,7 +1072,10 @@ static void l_gemm_resid(const PreparedDispatch& pd, void* const* p, hipStream_t
     GemmArgs a = gemm_base(p, w[4], w[5], w[6]);
     a.y32 = (float*)p[2];
     a.resid = (const float*)p[2];
-    hipLaunchKernelGGL(k_gemm<EPI_RESID>, dim3((w[5] + GBN - 1) / GBN, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
+    if (resid_narrow(w[4], w[5]))
+        hipLaunchKernelGGL((k_gemm<EPI_RESID, 64>), dim3((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemm<EPI_RESID, 128>), dim3((w[5] + GBN - 1) / GBN, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
 }
 
 // 18 gemm_swiglu: a, w (2 inter rows), y, m, inter, k
@@ -998,7 +1084,7 @@ static void l_gemm_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_
     GemmArgs a = gemm_base(p, w[4], 2 * w[5], w[6]);
     a.y16 = (uint16_t*)p[2];
     a.inter = int(w[5]);
-    hipLaunchKernelGGL(k_gemm<EPI_SWIGLU>, dim3((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 128>), dim3((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
 }
 
 // 19 gemm_f32: a, w, y, m, n, k
@@ -1006,7 +1092,7 @@ static void l_gemm_f32(const PreparedDispatch& pd, void* const* p, hipStream_t s
     const uint32_t* w = pd.words.data();
     GemmArgs a = gemm_base(p, w[4], w[5], w[6]);
     a.y32 = (float*)p[2];
-    hipLaunchKernelGGL(k_gemm<EPI_F32>, dim3((w[5] + GBN - 1) / GBN, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((k_gemm<EPI_F32, 128>), dim3((w[5] + GBN - 1) / GBN, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
 }
 
 // The decode GEMVs: one row (or gate/up pair) per wave, 4 waves per block; NCH, the 512-wide k-chunks per lane, is
@@ -1119,13 +1205,25 @@ static void l_convert(const PreparedDispatch& pd, void* const* p, hipStream_t s)
                        (const uint16_t*)p[0], (uint16_t*)p[1], n);
 }
 
+// 30 argmax_rows_partial: x, partials, rows, cols
+static void l_argmax_partial(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax_partial, dim3(kArgmaxParts, pd.words[3]), dim3(256), 0, s, (const float*)p[0],
+                       (float*)p[1], int(pd.words[3]), int(pd.words[4]));
+}
+
+// 31 argmax_rows_final: partials, out, rows
+static void l_argmax_final(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax_final, dim3(pd.words[3]), dim3(64), 0, s, (const float*)p[0], (uint32_t*)p[1],
+                       int(pd.words[3]));
+}
+
 int fast_first_id() { return 14; }
 
 const LaunchFn* fast_launchers() {
     static const LaunchFn t[] = {l_rmsnorm_f16, l_gemm_qkv,  l_attn_prefill, l_gemm_resid,   l_gemm_swiglu,
                                  l_gemm_f32,    l_gemv_norm, l_attn_dec,     l_attn_combine, l_gemv_resid,
                                  l_gemv_swiglu, l_lmhead,    l_argmax_dec,   l_embed_dec,    l_fill_normal,
-                                 l_convert};
+                                 l_convert,     l_argmax_partial, l_argmax_final};
     return t;
 }
 
@@ -1194,7 +1292,7 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 16 attention_prefill_f16: q, k_cache, v_cache, y, rows, past, q_heads, kv_heads, max_pos, scale
     c.push_back({"attention_prefill_f16", "fast", {256, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 63) / 64, w[8], 1}; },
+                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + kAttnRows - 1) / kAttnRows, w[8], 1}; },
                  {TOK_R("q", DT(F16)), TOK_R("k_cache", DT(F16)), TOK_R("v_cache", DT(F16)), TOK_W("y", DT(F16)),
                   U32F("rows"), U32F("past"), U32F("q_heads"), U32F("kv_heads"), U32F("max_pos"), F32F("scale")},
                  [](const uint32_t* w, const uint32_t* c) {
@@ -1209,7 +1307,10 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 17 gemm_residual: a, w, x, m, n, k
     c.push_back({"gemm_residual", "fast", {256, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 127) / 128, (int64_t(w[4]) + 127) / 128, 1}; },
+                 [](const uint32_t* w) {
+                     const int64_t bn = resid_narrow(w[4], w[5]) ? 64 : 128;
+                     return Grid3{(int64_t(w[5]) + bn - 1) / bn, (int64_t(w[4]) + 127) / 128, 1};
+                 },
                  {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_RW("x", DT(F32)), U32F("m"), U32F("n"), U32F("k")},
                  [](const uint32_t* w, const uint32_t* c) {
                      if (w[6] % 64 || w[6] < 64) contract_fail("gemm_residual: k must be a positive multiple of 64");
@@ -1349,6 +1450,22 @@ std::vector<KernelSpec> fast_catalog() {
                  [](const uint32_t* w, const uint32_t* c) {
                      need(c, 0, w[3], "convert_bf16_f16", "x");
                      need(c, 1, w[3], "convert_bf16_f16", "y");
+                 }});
+    // 30 argmax_rows_partial: x, partials, rows, cols
+    c.push_back({"argmax_rows_partial", "fast", {256, 1, 1}, false,
+                 [](const uint32_t* w) { return Grid3{kArgmaxParts, w[3], 1}; },
+                 {TOK_R("x", DT(F32)), TOK_W("partials", DT(F32)), U32F("rows"), U32F("cols")},
+                 [](const uint32_t* w, const uint32_t* c) {
+                     if (w[3] < 1 || w[4] < 1) contract_fail("argmax_rows_partial: rows and cols must be at least 1");
+                     need(c, 0, int64_t(w[3]) * w[4], "argmax_rows_partial", "x");
+                     need(c, 1, int64_t(w[3]) * kArgmaxParts * 2, "argmax_rows_partial", "partials");
+                 }});
+    // 31 argmax_rows_final: partials, out, rows
+    c.push_back({"argmax_rows_final", "fast", {64, 1, 1}, true, [](const uint32_t* w) { return Grid3{w[3], 1, 1}; },
+                 {TOK_R("partials", DT(F32)), TOK_W("out", DT(U32)), U32F("rows")},
+                 [](const uint32_t* w, const uint32_t* c) {
+                     need(c, 0, int64_t(w[3]) * kArgmaxParts * 2, "argmax_rows_final", "partials");
+                     need(c, 1, w[3], "argmax_rows_final", "out");
                  }});
     return c;
 }

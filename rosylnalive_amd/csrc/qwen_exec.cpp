@@ -265,6 +265,7 @@ void QwenExec::plan() {
         add("dec.attn_partials", Scratch, F32, {uint32_t(c.heads) * (MP / 64) * 130});
         add("dec.lm_partials", Scratch, F32, {2 * 1024});
         add("dec.state", Scratch, U32, {4});
+        add("argmax.partials", Scratch, F32, {std::min<uint32_t>(MT, 512) * 64 * 2});
         add("dec.out_ids", Logits, U32, {MP});
     } else {
         for (const char* n : {"h", "oo", "r", "h2", "dd", "f"}) add(n, Activations, F32, {MT, H});
@@ -566,7 +567,8 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
         CommandList* l2 = dev_.begin();
         dispatch(l2, "rmsnorm_rows_f16", {tk("x"), tk("model.norm.weight"), tk("h"), n, H, eps, uint32_t(r0)});
         dispatch(l2, "gemm_f32", {tk("h"), tk("embed.f16"), tk("logits"), n, V, H});
-        dispatch(l2, "argmax_rows", {tk("logits"), tk("argmax"), n, V});
+        dispatch(l2, "argmax_rows_partial", {tk("logits"), tk("argmax.partials"), n, V});
+        dispatch(l2, "argmax_rows_final", {tk("argmax.partials"), tk("argmax"), n});
         uint64_t f2 = dev_.submit(l2);
         dev_.wait(f2);
         dev_.release(l2);

@@ -352,3 +352,27 @@ def test_fill_normal_f16_statistics():
         assert np.array_equal(widen(bf16(y)), y), "every value is a bf16 value"
     finally:
         s.close()
+
+
+def test_argmax_rows_split_matches_cpuref():
+    """argmax_rows_partial + argmax_rows_final == CpuRef.argmaxRows: lowest index of the maximum, 0xFFFFFFFF for a row
+    holding a NaN, ties across the 64 column slices, -0/+0, all -inf."""
+    rows, cols = 9, 151936
+    r = np.random.default_rng(12)
+    x = r.standard_normal((rows, cols)).astype(np.float32)
+    x[1, [5, 100000]] = 50.0          # tie across slices: 5 wins
+    x[2, 7] = np.nan                  # NaN row
+    x[3, :] = -np.inf                 # all -inf: index 0
+    x[4, :] = 0.0
+    x[4, 0] = -0.0                    # -0 then +0: index 0
+    x[5, cols - 1] = 99.0             # last column
+    x[6, [70000, 70001]] = 30.0       # tie inside one slice
+    s = Session({"x": (F32, x.shape, RO, x), "part": (F32, (rows * 64 * 2,), 0, None), "out": (U32, (rows,), 0, None)})
+    try:
+        out = s.run_list([("argmax_rows_partial", dict(x="x", partials="part", rows=rows, cols=cols)),
+                          ("argmax_rows_final", dict(partials="part", out="out", rows=rows))], ["out"])["out"]
+        ref = cpuref.argmax_rows(x)
+        assert out.tolist() == ref.tolist(), (out, ref)
+        assert out[1] == 5 and out[2] == 0xFFFFFFFF and out[3] == 0 and out[4] == 0 and out[5] == cols - 1
+    finally:
+        s.close()
