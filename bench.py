@@ -204,6 +204,33 @@ def main():
                             "bytes_per_token": int(b4 / 64)}
         log("decode 4k:", out["decode_4k"])
 
+        # batched decode: Qwen3-1.7B shape, 16 sequences whose caches hold 8192 positions of bf16-valued N(0, 1)
+        # (stored fp16), 2 warmup + 64 timed steps of all 16 sequences
+        cfg_e = QwenConfig.qwen3_1_7b(max_pos=8192 + 128)
+        w_e = synthetic_weights(cfg_e, seed=args.seed)
+        be_e = HipBackend(0)
+        m_e = QwenModel(be_e, cfg_e, mode="fast", max_tokens=16, batch=16)
+        m_e.load_weights(w_e)
+        del w_e
+        m_e.fill_cache_random(args.seed, 8192)
+        toks = synthetic_ids(args.seed, "bench/batch16", 16, cfg_e.vocab)
+        m_e.decode_batch(toks, [8192] * 16, 2)
+        m_e.decode_batch(toks, [8192] * 16, 64)
+        e_ms = m_e.last_ms()
+        e_w = cfg_e.param_count() * 2
+        e_bytes = sum(e_w + 16 * 2 * cfg_e.layers * cfg_e.kv_heads * (8192 + s + 1) * cfg_e.head_dim * 2
+                      for s in range(64))
+        out["decode_batch16_1.7b_8k"] = {
+            "tok_s": round(16 * 64 / (e_ms / 1e3), 1), "ms_per_step": round(e_ms / 64, 4),
+            "gbs": round(e_bytes / (e_ms / 1e3) / 1e9, 1),
+            "hbm_frac": round(e_bytes / (e_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_step": int(e_bytes / 64),
+            "workload": "Qwen3-1.7B shape, 16 sequences, context 8193..8256, greedy, skinny MFMA GEMMs over fp16 "
+                        "weight copies"}
+        log("decode batch 16 (1.7B, 8K):", out["decode_batch16_1.7b_8k"])
+        m_e.close()
+        be_e.close()
+
     if not args.no_cpu:
         # the oracle (CpuRef F32 restated in C) on the host's cores: prefill of the same 128-token prompt, then 2
         # decode steps; decode tok/s reported from the decode steps.

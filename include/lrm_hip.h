@@ -34,7 +34,7 @@ int lrm_abi_version(void);
  * exact rules the device enforces. */
 
 /* Kernels.all / catalog.json (src/Lrm.Gpu.Core/Kernels.g.fs:27-285): ids 0..13 are the reference catalog, 14.. are
- * this backend's appended bf16 kernels. kind: 1 token, 2 u32, 3 i32, 4 f32; access: 1 read, 2 write, 3 readwrite,
+ * this backend's appended fast-path kernels. kind: 1 token, 2 u32, 3 i32, 4 f32; access: 1 read, 2 write, 3 readwrite,
  * 4 meta; dtype_mask: bit (1 << DType code). */
 int lrm_catalog_count(void);
 int lrm_catalog_find(const char *name); /* id, or -1 */
@@ -128,13 +128,14 @@ int lrm_hip_release(lrm_hip_device *d, lrm_hip_list *l); /* frees a reusable lis
 /* ======================================================================== the Qwen3 executor
  * The counterpart of the planned Lrm.Gpu.Exec GpuForwardOps and Lrm.Models.Qwen Forward/Greedy (docs/dev-plan.md:
  * 166-170,205-209,289-290), whose only existing form is tests/Lrm.Tensor.Tests/TinyModel.fs:144-236. mode 0 runs the
- * reference catalog kernels in fp32 (parity with CpuRef F32); mode 1 runs the bf16 fast path. */
+ * reference catalog kernels in fp32 (parity with CpuRef F32); mode 1 runs the fast path (bf16 weights; fp16 MFMA
+ * operands and an fp16 KV cache in prefill; bf16-weight GEMVs for one sequence in decode). */
 typedef struct lrm_qwen_config {
     int32_t layers, hidden, heads, kv_heads, head_dim, intermediate, vocab, max_pos;
     float eps;
-    int32_t mode;       /* 0 fp32 catalog, 1 bf16 fast */
+    int32_t mode;       /* 0 fp32 catalog, 1 fast */
     int32_t max_tokens; /* rows per forward chunk */
-    int32_t batch;      /* sequences (1) */
+    int32_t batch;      /* sequences with their own KV cache: 1 (mode 0), 1 .. 16 (mode 1) */
     int32_t taps;       /* mode 0: keep every ActivationNames tap (src/Lrm.Tensor/Goldens.fs:288-322) */
 } lrm_qwen_config;
 
@@ -153,11 +154,15 @@ int lrm_qwen_forward(lrm_qwen *q, int seq, int pos0, const int32_t *ids, int t, 
                      uint32_t *argmax);
 /* TinyModel.greedy (TinyModel.fs:219-236): prefill then steps - 1 decode steps; mode 1 decodes on device. */
 int lrm_qwen_greedy(lrm_qwen *q, const int32_t *prompt, int prompt_len, int steps, int32_t *out_ids);
-/* On-device decode (mode 1): state = (token id at position pos), run `steps` recorded decode steps (one HIP graph
- * replay each), read the ids they produced (out_ids[s] = the id chosen by step s). */
+/* On-device decode (mode 1): state = (token ids[b] at positions pos[b], one per sequence), run `steps` recorded decode
+ * steps (one HIP graph replay each), read the ids they produced (out[s * batch + b] = the id sequence b chose at step
+ * s). One sequence decodes with GEMVs over the bf16 weights; 2 .. 16 together with skinny MFMA GEMMs over the fp16
+ * copies (config E of the hot path: the 1.7B shape, 16 sequences at 8K context). */
 int lrm_qwen_decode_set(lrm_qwen *q, const int32_t *ids, const int32_t *pos);
 int lrm_qwen_decode_run(lrm_qwen *q, int steps);
 int lrm_qwen_decode_ids(lrm_qwen *q, int32_t *out, int count);
+/* decode_set + decode_run(steps) + decode_ids(steps * batch): the batched greedy loop on device. */
+int lrm_qwen_decode_batch(lrm_qwen *q, const int32_t *ids, const int32_t *pos, int steps, int32_t *out_ids);
 /* Rows of the logits buffer: after a decode step, row 0 holds that step's logits. */
 int lrm_qwen_read_logits(lrm_qwen *q, float *out, int rows);
 double lrm_qwen_last_ms(lrm_qwen *q); /* device time of the last forward / decode run, ms */

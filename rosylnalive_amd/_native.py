@@ -117,6 +117,7 @@ PROTOTYPES = {
     "lrm_qwen_decode_set": (C.c_int, [P, P, P]),
     "lrm_qwen_decode_run": (C.c_int, [P, C.c_int]),
     "lrm_qwen_decode_ids": (C.c_int, [P, P, C.c_int]),
+    "lrm_qwen_decode_batch": (C.c_int, [P, P, P, C.c_int, P]),
     "lrm_qwen_read_logits": (C.c_int, [P, P, C.c_int]),
     "lrm_qwen_last_ms": (C.c_double, [P]),
     "lrm_qwen_token": (C.c_int, [P, C.c_char_p, U32P]),

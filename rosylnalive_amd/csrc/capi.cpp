@@ -477,6 +477,16 @@ int lrm_qwen_decode_ids(lrm_qwen* q, int32_t* out, int count) {
     });
 }
 
+int lrm_qwen_decode_batch(lrm_qwen* q, const int32_t* ids, const int32_t* pos, int steps, int32_t* out_ids) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(ids, "ids");
+        need_ptr(pos, "pos");
+        need_ptr(out_ids, "out_ids");
+        q->q.decode_batch(ids, pos, steps, out_ids);
+    });
+}
+
 int lrm_qwen_read_logits(lrm_qwen* q, float* out, int rows) {
     return guard([&] {
         need_ptr(q, "model");

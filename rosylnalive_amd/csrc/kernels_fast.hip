@@ -82,7 +82,7 @@ struct GemmArgs {
 };
 
 template <int EPI, int BN>
-__global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
     static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID)), "SwiGLU and QKV pair 128 columns");
     constexpr int WN = BN / 2, JT = WN / 16, BCH = BN / 32;  // columns per wave, MFMA tiles per wave, B chunks/thread
     constexpr int STAGE = (GBM + BN) * GLD;
@@ -91,51 +91,51 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     const int m0 = blockIdx.y * GBM;
     const int n0 = blockIdx.x * BN;
 
-    // the rows this thread loads: chunk c = t + 256 i -> row c / 8, 16-byte column (c % 8); element offsets from the
-    // matrix base (the caller keeps every matrix under 2^31 elements), -1 for a row past the matrix
+    // the rows this thread loads: chunk c = t + 256 i -> row c / 8, 16-byte column (c % 8), as element offsets from
+    // the matrix base (every matrix is under 2^31 elements). A row past the matrix is clamped to its last row: it only
+    // feeds output rows / columns that are never stored, and the loads stay unconditional, so the compiler can keep
+    // several tiles in flight (a guarded load makes it wait for every outstanding load).
     int aoff[4], boff[BCH];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
-        const int m = m0 + r;
-        aoff[i] = m < p.M ? m * p.K + kc : -1;
+        aoff[i] = min(m0 + r, p.M - 1) * p.K + kc;
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
         const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
         int n;
         if (EPI == EPI_SWIGLU) {
-            const int j = blockIdx.x * 64 + (r & 63);
-            n = j < p.inter ? (r < 64 ? j : p.inter + j) : -1;
+            const int j = min(int(blockIdx.x) * 64 + (r & 63), p.inter - 1);
+            n = r < 64 ? j : p.inter + j;
         } else {
-            n = n0 + r < p.N ? n0 + r : -1;
+            n = min(n0 + r, p.N - 1);
         }
-        boff[i] = n >= 0 ? n * p.K + kc : -1;
+        boff[i] = n * p.K + kc;
     }
-    // two register sets: tile j is loaded into set j % 2 two iterations before it is multiplied
-    uint4 ra[2][4], rb[2][BCH];
-    auto gload = [&](auto set, int k0) {
-        constexpr int S = decltype(set)::value;
+    // Tile kt + 1 is loaded into registers at the top of iteration kt, the matrix cores work on tile kt from LDS while
+    // those loads are in flight, and the registers go to the other LDS buffer at the end of the iteration: the
+    // registers never live across the loop's back edge, so the compiler waits for the loads only after the MFMAs of
+    // the iteration have been issued.
+    u32x4 ra[4], rb[BCH];
+    auto gload = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            ra[S][i] = aoff[i] >= 0 ? *reinterpret_cast<const uint4*>(p.a + (aoff[i] + k0)) : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const u32x4*>(p.a + (aoff[i] + k0));
 #pragma unroll
-        for (int i = 0; i < BCH; ++i)
-            rb[S][i] = boff[i] >= 0 ? *reinterpret_cast<const uint4*>(p.w + (boff[i] + k0)) : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < BCH; ++i) rb[i] = *reinterpret_cast<const u32x4*>(p.w + (boff[i] + k0));
     };
-    auto sstore = [&](auto set, int buf) {
-        constexpr int S = decltype(set)::value;
+    auto sstore = [&](int buf) __attribute__((always_inline)) {
         uint16_t* As = lds + buf * STAGE;
         uint16_t* Bs = As + GBM * GLD;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = t + 256 * i;
-            *reinterpret_cast<uint4*>(As + (c >> 3) * GLD + (c & 7) * 8) = ra[S][i];
+            *reinterpret_cast<u32x4*>(As + (c >> 3) * GLD + (c & 7) * 8) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < BCH; ++i) {
             const int c = t + 256 * i;
-            *reinterpret_cast<uint4*>(Bs + (c >> 3) * GLD + (c & 7) * 8) = rb[S][i];
+            *reinterpret_cast<u32x4*>(Bs + (c >> 3) * GLD + (c & 7) * 8) = rb[i];
         }
     };
 
@@ -145,7 +145,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < JT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto mma = [&](int buf) {
+    const int nk = p.K / GBK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        gload(min(kt + 1, nk - 1) * GBK);  // unconditional, so it stays ahead of the MFMAs
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads issued before this tile's LDS reads and MFMAs
         const uint16_t* As = lds + buf * STAGE;
         const uint16_t* Bs = As + GBM * GLD;
 #pragma unroll
@@ -154,41 +161,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             const int kof = ks * 32 + 8 * g;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                af[i] = as_f16x8(*reinterpret_cast<const uint4*>(As + (wm * 64 + i * 16 + c16) * GLD + kof));
+                af[i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + (wm * 64 + i * 16 + c16) * GLD + kof));
 #pragma unroll
             for (int j = 0; j < JT; ++j)
-                bfr[j] = as_f16x8(*reinterpret_cast<const uint4*>(Bs + (wn * WN + j * 16 + c16) * GLD + kof));
+                bfr[j] = as_f16x8(*reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 16 + c16) * GLD + kof));
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < JT; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bfr[j], acc[i][j], 0, 0, 0);
         }
-    };
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    // iteration kt: store tile kt + 1 (set (kt + 1) % 2) into the other LDS buffer, refill that set with tile kt + 3,
-    // multiply tile kt
-    auto step = [&](auto par, int kt, int nk) {
-        constexpr int P = decltype(par)::value;  // kt % 2
-        using Next = std::integral_constant<int, 1 - P>;
-        if (kt + 1 < nk) {
-            sstore(Next{}, 1 - P);
-            if (kt + 3 < nk) gload(Next{}, (kt + 3) * GBK);
-        }
-        mma(P);
+        sstore(buf ^ 1);  // the other buffer was last read in iteration kt - 1, before its barrier (the last copy is unused)
         __syncthreads();
-    };
-
-    const int nk = p.K / GBK;
-    gload(S0{}, 0);
-    sstore(S0{}, 0);
-    if (nk > 1) gload(S1{}, GBK);
-    if (nk > 2) gload(S0{}, 2 * GBK);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt += 2) {
-        step(S0{}, kt, nk);
-        if (kt + 1 < nk) step(S1{}, kt + 1, nk);
     }
 
     if (EPI == EPI_F32 || EPI == EPI_RESID) {
@@ -345,40 +329,43 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
     const uint16_t* kbase = kc + size_t(kvhead) * max_pos * 128;
     const uint16_t* vbase = vc + size_t(kvhead) * 128 * max_pos;
 
-    uint4 rk[4], rv[4];
-    auto fetch = [&](int kb) {
+    // The loads of a 64-key block are unconditional (kb + 63 < max_pos: kb < kend <= max_pos, both multiples of 64);
+    // keys at or past kend may hold anything. Their scores are masked, so K needs nothing; V is zeroed there after
+    // the load, since a zero weight times a NaN is still a NaN.
+    u32x4 rk[4], rv[4];
+    auto fetch = [&](int kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = t + 256 * i, key = c >> 4, dc = (c & 15) * 8;
-            rk[i] = kb + key < kend ? *reinterpret_cast<const uint4*>(kbase + size_t(kb + key) * 128 + dc)
-                                    : make_uint4(0, 0, 0, 0);
+            rk[i] = *reinterpret_cast<const u32x4*>(kbase + size_t(kb + key) * 128 + dc);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = t + 256 * i, d = c >> 3, k8 = (c & 7) * 8;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (kb + k8 < kend) {  // kb + k8 + 7 < max_pos: kb, k8 are multiples of 64 and 8, max_pos of 64
-                v = *reinterpret_cast<const uint4*>(vbase + size_t(d) * max_pos + kb + k8);
-                const int valid = kend - (kb + k8);  // keys at or past kend hold anything: zero them
-                if (valid < 8) {
-                    uint32_t u[4] = {v.x, v.y, v.z, v.w};
+            rv[i] = *reinterpret_cast<const u32x4*>(vbase + size_t(d) * max_pos + kb + k8);
+        }
+    };
+    auto mask_v = [&](int kb) __attribute__((always_inline)) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (e >= valid) u[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-                    v = make_uint4(u[0], u[1], u[2], u[3]);
-                }
+        for (int i = 0; i < 4; ++i) {
+            const int c = t + 256 * i, k8 = (c & 7) * 8;
+            const int valid = kend - (kb + k8);
+            if (valid < 8) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (e >= valid) rv[i][e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
             }
-            rv[i] = v;
         }
     };
     fetch(0);
     for (int kb = 0; kb < kend; kb += 64) {
+        mask_v(kb);
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = t + 256 * i;
-            *reinterpret_cast<uint4*>(Ks + (c >> 4) * 136 + (c & 15) * 8) = rk[i];
-            *reinterpret_cast<uint4*>(Vt + (c >> 3) * 72 + (c & 7) * 8) = rv[i];
+            *reinterpret_cast<u32x4*>(Ks + (c >> 4) * 136 + (c & 15) * 8) = rk[i];
+            *reinterpret_cast<u32x4*>(Vt + (c >> 3) * 72 + (c & 7) * 8) = rv[i];
         }
         __syncthreads();
         if (kb + 64 < kend) fetch(kb + 64);  // in flight during this block's MFMAs
@@ -390,18 +377,20 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
-                const f16x8 a = as_f16x8(*reinterpret_cast<const uint4*>(Ks + (kt * 16 + c16) * 136 + ks * 32 + 8 * g));
+                const f16x8 a = as_f16x8(*reinterpret_cast<const u32x4*>(Ks + (kt * 16 + c16) * 136 + ks * 32 + 8 * g));
                 s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ks], s[kt], 0, 0, 0);
             }
 
+        // causal mask, branch-free, only where the key block crosses the diagonal or the tile runs past T (uniform)
+        const bool need_mask = kb + 63 > past + row0 || row0 + kAttnRows > T;
+        const int lim = row < T ? qpos - kb : -1;  // key offsets in this block above lim are masked
         float mloc = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int key = kb + kt * 16 + 4 * g + r;
                 float v = s[kt][r] * scale_log2;
-                if (row >= T || key > qpos) v = -INFINITY;
+                if (need_mask) v = (kt * 16 + 4 * g + r > lim) ? -INFINITY : v;
                 s[kt][r] = v;
                 mloc = fmaxf(mloc, v);
             }
@@ -409,14 +398,15 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
         const float m_new = fmaxf(m_run, mloc);
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = exp2f(m_run - m_use);
+        // the hardware exp2 (results below 2^-126 flush to 0: weights that small are below fp16 P anyway)
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
         float lsum = 0.f;
         float pv[4][4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                pv[kt][r] = exp2f(s[kt][r] - m_use);
+                pv[kt][r] = __builtin_amdgcn_exp2f(s[kt][r] - m_use);
                 lsum += pv[kt][r];
             }
         lsum += __shfl_xor(lsum, 16, 64);
@@ -456,8 +446,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
 }
 
 // ================================================================ decode kernels (one token per step)
-// The step state is device memory: state[0] = the position being decoded, state[1] = its token id, state[2] = the
-// step index. The argmax kernel writes the next id and advances the state, so a recorded step replays unchanged.
+// The step state is device memory, for B sequences: state[b] = the position sequence b decodes, state[B + b] = its
+// token id, state[2 B] = the step index (B = 1: position, id, step). The argmax kernel writes the next ids and advances
+// the state, so a recorded step replays unchanged.
 //
 // The GEMVs give each wave whole rows and keep every wave independent (no LDS, no barrier): lane l covers the
 // k-chunks 512 c + 8 l .. + 7, c < NCH, and issues the loads of all its weight chunks and of its slice of the input
@@ -559,8 +550,13 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
     __shared__ float stat[2][2];
     __shared__ float redq[4], redk[4];
     const int s = blockIdx.x, S = gridDim.x, kvhead = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int pos = int(state[0]);
+    const int b = blockIdx.z;  // the sequence: its projections, caches and partials follow the previous ones
+    const int pos = int(state[b]);
     if (pos < 0 || pos >= max_pos) return;  // the host keeps decode inside max_pos; never touch memory past the cache
+    qkv += size_t(b) * (qh + 2 * kvh) * 128;
+    kc += size_t(b) * kvh * max_pos * 128;
+    vc += size_t(b) * kvh * 128 * max_pos;
+    part += size_t(b) * qh * S * 130;
     const int key0 = s * 64;
     const int nkeys = min(64, pos + 1 - key0);
     if (nkeys <= 0) return;
@@ -717,16 +713,17 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
 // y[h, d] = sum_s 2^(m_s - M) o_s[d] / sum_s 2^(m_s - M) l_s over the splits that hold keys; one block per head, the
 // splits spread over the threads (every load of a pass is independent of the others).
 constexpr int kMaxSplits = 1024;
-__global__ __launch_bounds__(256) void k_attn_combine(const float* part, float* y, const uint32_t* state, int splits,
+template <typename OUT>
+__global__ __launch_bounds__(256) void k_attn_combine(const float* part, OUT* y, const uint32_t* state, int splits,
                                                       int max_pos) {
     __shared__ float sc[kMaxSplits];
     __shared__ float red[4];
     __shared__ float o_hi[128];
-    const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int pos = int(state[0]);
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int pos = int(state[b]);
     if (pos < 0 || pos >= max_pos) return;
     const int used = min(pos / 64 + 1, splits);
-    const float* hp = part + size_t(h) * splits * 130;
+    const float* hp = part + (size_t(b) * gridDim.x + h) * splits * 130;
     float m = -INFINITY;
     for (int i = t; i < used; i += 256) m = fmaxf(m, hp[size_t(i) * 130]);
     m = wave_max(m);
@@ -750,7 +747,14 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* part, float* 
     for (int i = par; i < used; i += 2) o = fmaf(hp[size_t(i) * 130 + 2 + d], sc[i], o);
     if (par == 1) o_hi[d] = o;
     __syncthreads();
-    if (par == 0) y[h * 128 + d] = (o + o_hi[d]) / L;
+    if (par == 0) {
+        const float v = (o + o_hi[d]) / L;
+        OUT* yo = y + (size_t(b) * gridDim.x + h) * 128 + d;
+        if constexpr (sizeof(OUT) == 4)
+            *yo = v;
+        else
+            *yo = f2h(v);
+    }
 }
 
 // ---------------------------------------------------------------- 23 gemv_residual_dec: x[n] += w[n] . a
@@ -894,12 +898,14 @@ __global__ __launch_bounds__(1024) void k_argmax_dec(const float* part, uint32_t
     }
 }
 
-// ---------------------------------------------------------------- 27 embed_dec: x = widen(E[state[1]])
+// ---------------------------------------------------------------- 27 embed_dec: x[b] = widen(E[state.id[b]])
 __global__ __launch_bounds__(256) void k_embed_dec(const uint16_t* e, const uint32_t* state, float* x, int hidden,
                                                    int vocab) {
-    const uint32_t id = state[1];
+    const int b = blockIdx.x;
+    const uint32_t id = state[gridDim.x + b];
+    float* xb = x + size_t(b) * hidden;
     for (int c = threadIdx.x; c < hidden; c += 256)
-        x[c] = id < uint32_t(vocab) ? bf2f(e[size_t(id) * hidden + c]) : __uint_as_float(0x7FC00000u);
+        xb[c] = id < uint32_t(vocab) ? bf2f(e[size_t(id) * hidden + c]) : __uint_as_float(0x7FC00000u);
 }
 
 // ---------------------------------------------------------------- 28 fill_normal_f16 (synthetic caches)
@@ -1006,6 +1012,97 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* part, uint32_t
     const bool nan = __any(i == 0xFFFFFFFEu);
     ArgBest a = arg_wave(ArgBest{pp[0], i == 0xFFFFFFFEu ? 0xFFFFFFFFu : i});
     if (t == 0) out[r] = nan ? 0xFFFFFFFFu : a.i;
+}
+
+// ================================================================ 32-34 skinny GEMMs (batched decode)
+// Y[r, n] = sum_k A[r, k] W[n, k] for M <= 16 rows (the sequences of a batched decode step), on f16 operands: the
+// weights are read once for all rows. A block owns two 16-column MFMA tiles (32 output columns; for SwiGLU gate
+// columns j0 .. j0 + 15 and the matching up columns) and its 8 waves split K in eight. Each wave streams its slice of
+// the W rows straight into MFMA B operands (lane: row c16, 8 halves at k + 8g, so 64 contiguous bytes per row per
+// 32-k step) with the A rows from L2, 4 steps of loads in flight, then the partial tiles of the 8 waves are summed in
+// LDS in a fixed order (deterministic). Rows of A past M and columns past N are clamped in range and never stored.
+constexpr int kSkWaves = 8;
+enum SkEpi { SK_F32 = 0, SK_RESID = 1, SK_SWIGLU = 2 };
+
+template <int EPI>
+__global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const uint16_t* w, float* y32, uint16_t* y16,
+                                                     int M, int N, int K, int inter) {
+    __shared__ float red[kSkWaves][2][256];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, g = lane >> 4, c16 = lane & 15;
+    int n0, n1;
+    if (EPI == SK_SWIGLU) {
+        const int j = min(int(blockIdx.x) * 16 + c16, inter - 1);
+        n0 = j;
+        n1 = inter + j;
+    } else {
+        n0 = min(int(blockIdx.x) * 32 + c16, N - 1);
+        n1 = min(int(blockIdx.x) * 32 + 16 + c16, N - 1);
+    }
+    const int kper = K / kSkWaves;  // a multiple of 128
+    const int kb = wv * kper + 8 * g;
+    const uint16_t* ap = a + size_t(min(c16, M - 1)) * K + kb;
+    const uint16_t* w0 = w + size_t(n0) * K + kb;
+    const uint16_t* w1 = w + size_t(n1) * K + kb;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < kper; k += 128) {
+        u32x4 av[4], b0[4], b1[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            b0[s] = *reinterpret_cast<const u32x4*>(w0 + k + 32 * s);
+            b1[s] = *reinterpret_cast<const u32x4*>(w1 + k + 32 * s);
+            av[s] = *reinterpret_cast<const u32x4*>(ap + k + 32 * s);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av[s]), as_f16x8(b0[s]), acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av[s]), as_f16x8(b1[s]), acc1, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        red[wv][0][lane * 4 + i] = acc0[i];
+        red[wv][1][lane * 4 + i] = acc1[i];
+    }
+    __syncthreads();
+    // element e of a tile: lane e / 4, register e % 4 -> row 4 (lane / 16) + e % 4, column lane % 16
+    if (EPI == SK_SWIGLU) {
+        if (t >= 256) return;
+        float gv = 0.f, uv = 0.f;
+#pragma unroll
+        for (int i = 0; i < kSkWaves; ++i) {
+            gv += red[i][0][t];
+            uv += red[i][1][t];
+        }
+        const int l = t >> 2, row = 4 * (l >> 4) + (t & 3), j = int(blockIdx.x) * 16 + (l & 15);
+        if (row < M && j < inter) y16[size_t(row) * inter + j] = f2h(gv / (1.0f + __expf(-gv)) * uv);
+        return;
+    }
+    const int tile = t >> 8, e = t & 255;
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < kSkWaves; ++i) v += red[i][tile][e];
+    const int l = e >> 2, row = 4 * (l >> 4) + (e & 3), n = int(blockIdx.x) * 32 + tile * 16 + (l & 15);
+    if (row >= M || n >= N) return;
+    if (EPI == SK_RESID)
+        y32[size_t(row) * N + n] += v;
+    else
+        y32[size_t(row) * N + n] = v;
+}
+
+// ---------------------------------------------------------------- 36 decode_advance
+// After the batched argmax: out_ids[step * B + b] = id[b] (while step < max_steps), then every sequence moves one
+// position and takes its argmax as the next token; step += 1.
+__global__ __launch_bounds__(256) void k_decode_advance(const uint32_t* am, uint32_t* state, uint32_t* out_ids, int B,
+                                                        int max_steps) {
+    const uint32_t step = state[2 * B];
+    for (int b = threadIdx.x; b < B; b += 256) {
+        const uint32_t id = am[b];
+        if (step < uint32_t(max_steps)) out_ids[size_t(step) * B + b] = id;
+        state[B + b] = id;
+        state[b] = state[b] + 1u;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) state[2 * B] = step + 1u;
 }
 
 // ================================================================ launchers and catalog entries
@@ -1132,18 +1229,25 @@ static void l_gemv_norm(const PreparedDispatch& pd, void* const* p, hipStream_t 
 static void l_attn_dec(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     const int max_pos = int(w[12]);
-    hipLaunchKernelGGL(k_attn_dec, dim3(uint32_t(max_pos / 64), w[11]), dim3(256), 0, s, (const float*)p[0],
+    hipLaunchKernelGGL(k_attn_dec, dim3(uint32_t(max_pos / 64), w[11], w[15]), dim3(256), 0, s, (const float*)p[0],
                        (const uint16_t*)p[1], (const uint16_t*)p[2], (const float*)p[3], (const float*)p[4],
                        (uint16_t*)p[5], (uint16_t*)p[6], (float*)p[7], (const uint32_t*)p[8], int(w[10]), int(w[11]),
                        max_pos, f32_of(w[13]), f32_of(w[14]) * kLog2e);
 }
 
-// 22 attention_combine: partials, y, state, q_heads, max_pos
-static void l_attn_combine(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+// 22 attention_combine, 35 attention_combine_f16: partials, y, state, q_heads, max_pos, batch
+template <typename OUT>
+static void l_attn_combine_t(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     const int max_pos = int(w[5]);
-    hipLaunchKernelGGL(k_attn_combine, dim3(w[4]), dim3(256), 0, s, (const float*)p[0], (float*)p[1],
+    hipLaunchKernelGGL((k_attn_combine<OUT>), dim3(w[4], w[6]), dim3(256), 0, s, (const float*)p[0], (OUT*)p[1],
                        (const uint32_t*)p[2], max_pos / 64, max_pos);
+}
+static void l_attn_combine(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    l_attn_combine_t<float>(pd, p, s);
+}
+static void l_attn_combine_f16(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    l_attn_combine_t<uint16_t>(pd, p, s);
 }
 
 // 23 gemv_residual_dec: a, w, x, n, k
@@ -1185,7 +1289,7 @@ static void l_argmax_dec(const PreparedDispatch& pd, void* const* p, hipStream_t
 
 // 27 embed_dec: embed, state, x, hidden, vocab
 static void l_embed_dec(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed_dec, dim3(1), dim3(256), 0, s, (const uint16_t*)p[0], (const uint32_t*)p[1],
+    hipLaunchKernelGGL(k_embed_dec, dim3(pd.words[6]), dim3(256), 0, s, (const uint16_t*)p[0], (const uint32_t*)p[1],
                        (float*)p[2], int(pd.words[4]), int(pd.words[5]));
 }
 
@@ -1217,13 +1321,37 @@ static void l_argmax_final(const PreparedDispatch& pd, void* const* p, hipStream
                        int(pd.words[3]));
 }
 
+// 32 gemm_skinny_f32, 33 gemm_skinny_residual: a, w, y, m, n, k; 34 gemm_skinny_swiglu: a, w, y, m, inter, k
+static void l_gemm_skinny_f32(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    const uint32_t* w = pd.words.data();
+    hipLaunchKernelGGL((k_gemm_skinny<SK_F32>), dim3((w[5] + 31) / 32), dim3(512), 0, s, (const uint16_t*)p[0],
+                       (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
+}
+static void l_gemm_skinny_resid(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    const uint32_t* w = pd.words.data();
+    hipLaunchKernelGGL((k_gemm_skinny<SK_RESID>), dim3((w[5] + 31) / 32), dim3(512), 0, s, (const uint16_t*)p[0],
+                       (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
+}
+static void l_gemm_skinny_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    const uint32_t* w = pd.words.data();
+    hipLaunchKernelGGL((k_gemm_skinny<SK_SWIGLU>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
+                       (const uint16_t*)p[1], (float*)nullptr, (uint16_t*)p[2], int(w[4]), 0, int(w[6]), int(w[5]));
+}
+
+// 36 decode_advance: argmax, state, out_ids, batch, max_steps
+static void l_decode_advance(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    hipLaunchKernelGGL(k_decode_advance, dim3(1), dim3(256), 0, s, (const uint32_t*)p[0], (uint32_t*)p[1],
+                       (uint32_t*)p[2], int(pd.words[4]), int(pd.words[5]));
+}
+
 int fast_first_id() { return 14; }
 
 const LaunchFn* fast_launchers() {
     static const LaunchFn t[] = {l_rmsnorm_f16, l_gemm_qkv,  l_attn_prefill, l_gemm_resid,   l_gemm_swiglu,
                                  l_gemm_f32,    l_gemv_norm, l_attn_dec,     l_attn_combine, l_gemv_resid,
                                  l_gemv_swiglu, l_lmhead,    l_argmax_dec,   l_embed_dec,    l_fill_normal,
-                                 l_convert,     l_argmax_partial, l_argmax_final};
+                                 l_convert,     l_argmax_partial, l_argmax_final, l_gemm_skinny_f32,
+                                 l_gemm_skinny_resid, l_gemm_skinny_swiglu, l_attn_combine_f16, l_decode_advance};
     return t;
 }
 
@@ -1249,6 +1377,29 @@ static void need_group2(const char* k, uint32_t qh, uint32_t kvh) {
 static void need_k(const char* k, uint32_t n) {
     if (n < 8 || n % 8 || n > uint32_t(kMaxHidden))
         contract_fail("%s: the reduced dimension must be a multiple of 8 in 8 .. %d", k, kMaxHidden);
+}
+
+static void need_batch(const char* k, uint32_t b) {
+    if (b < 1 || b > 1024) contract_fail("%s: batch must be in 1 .. 1024", k);
+}
+
+static void check_combine(const char* k, const uint32_t* w, const uint32_t* c) {
+    const int64_t qh = w[4], mp = w[5], B = w[6];
+    need_batch(k, w[6]);
+    if (mp < 64 || mp % 64 || mp > 64 * kMaxSplits) contract_fail("%s: max_pos must be a multiple of 64 in 64 .. %d", k, 64 * kMaxSplits);
+    need(c, 0, B * qh * (mp / 64) * 130, k, "partials");
+    need(c, 1, B * qh * 128, k, "y");
+    need(c, 2, 2 * B + 1, k, "state");
+}
+
+static void check_skinny(const char* k, const uint32_t* w, const uint32_t* c, int64_t wrows, int64_t ycols) {
+    const int64_t m = w[4], K = w[6];
+    if (m < 1 || m > 16) contract_fail("%s: m must be in 1 .. 16", k);
+    if (K < 1024 || K % 1024) contract_fail("%s: k must be a positive multiple of 1024", k);
+    if (wrows < 1) contract_fail("%s: n must be at least 1", k);
+    need(c, 0, m * K, k, "a");
+    need(c, 1, wrows * K, k, "w");
+    need(c, 2, m * ycols, k, "y");
 }
 
 static void need_max_pos(const char* k, uint32_t mp) {
@@ -1353,36 +1504,31 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 21 attention_decode_f16
     c.push_back({"attention_decode_f16", "fast", {256, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{int64_t(w[12]) / 64, w[11], 1}; },
+                 [](const uint32_t* w) { return Grid3{int64_t(w[12]) / 64, w[11], w[15]}; },
                  {TOK_R("qkv", DT(F32)), TOK_R("q_norm", DT(BF16)), TOK_R("k_norm", DT(BF16)),
                   TOK_R("cos_table", DT(F32)), TOK_R("sin_table", DT(F32)), TOK_RW("k_cache", DT(F16)),
                   TOK_RW("v_cache", DT(F16)), TOK_W("partials", DT(F32)), TOK_R("state", DT(U32)), U32F("q_heads"),
-                  U32F("kv_heads"), U32F("max_pos"), F32F("eps"), F32F("scale")},
+                  U32F("kv_heads"), U32F("max_pos"), F32F("eps"), F32F("scale"), U32F("batch")},
                  [](const uint32_t* w, const uint32_t* c) {
-                     const int64_t qh = w[10], kvh = w[11], mp = w[12];
+                     const int64_t qh = w[10], kvh = w[11], mp = w[12], B = w[15];
                      need_group2("attention_decode_f16", w[10], w[11]);
                      need_max_pos("attention_decode_f16", w[12]);
-                     need(c, 0, (qh + 2 * kvh) * 128, "attention_decode_f16", "qkv");
+                     need_batch("attention_decode_f16", w[15]);
+                     need(c, 0, B * (qh + 2 * kvh) * 128, "attention_decode_f16", "qkv");
                      need(c, 1, 128, "attention_decode_f16", "q_norm");
                      need(c, 2, 128, "attention_decode_f16", "k_norm");
                      need(c, 3, mp * 64, "attention_decode_f16", "cos_table");
                      need(c, 4, mp * 64, "attention_decode_f16", "sin_table");
-                     need(c, 5, kvh * mp * 128, "attention_decode_f16", "k_cache");
-                     need(c, 6, kvh * mp * 128, "attention_decode_f16", "v_cache");
-                     need(c, 7, qh * (mp / 64) * 130, "attention_decode_f16", "partials");
-                     need(c, 8, 3, "attention_decode_f16", "state");
+                     need(c, 5, B * kvh * mp * 128, "attention_decode_f16", "k_cache");
+                     need(c, 6, B * kvh * mp * 128, "attention_decode_f16", "v_cache");
+                     need(c, 7, B * qh * (mp / 64) * 130, "attention_decode_f16", "partials");
+                     need(c, 8, 2 * B + 1, "attention_decode_f16", "state");
                  }});
     // 22 attention_combine: partials, y, state, q_heads, max_pos
-    c.push_back({"attention_combine", "fast", {256, 1, 1}, true, [](const uint32_t* w) { return Grid3{w[4], 1, 1}; },
+    c.push_back({"attention_combine", "fast", {256, 1, 1}, false, [](const uint32_t* w) { return Grid3{w[4], w[6], 1}; },
                  {TOK_R("partials", DT(F32)), TOK_W("y", DT(F32)), TOK_R("state", DT(U32)), U32F("q_heads"),
-                  U32F("max_pos")},
-                 [](const uint32_t* w, const uint32_t* c) {
-                     const int64_t qh = w[4], mp = w[5];
-                     need_max_pos("attention_combine", w[5]);
-                     need(c, 0, qh * (mp / 64) * 130, "attention_combine", "partials");
-                     need(c, 1, qh * 128, "attention_combine", "y");
-                     need(c, 2, 3, "attention_combine", "state");
-                 }});
+                  U32F("max_pos"), U32F("batch")},
+                 [](const uint32_t* w, const uint32_t* c) { check_combine("attention_combine", w, c); }});
     // 23 gemv_residual_dec: a, w, x, n, k
     c.push_back({"gemv_residual_dec", "fast", {256, 1, 1}, true,
                  [](const uint32_t* w) { return Grid3{gemv_blocks(w[4]), 1, 1}; },
@@ -1420,7 +1566,7 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 3, w[9] ? int64_t(w[6]) : 0, "lmhead_dec", "logits");
                      need(c, 4, 2 * int64_t(kLmheadBlocks), "lmhead_dec", "partials");
                  }});
-    // 26 argmax_dec: partials, state, out_ids, max_steps
+    // 26 argmax_dec (one sequence): partials, state, out_ids, max_steps
     c.push_back({"argmax_dec", "fast", {1024, 1, 1}, true, [](const uint32_t*) { return Grid3{1, 1, 1}; },
                  {TOK_R("partials", DT(F32)), TOK_RW("state", DT(U32)), TOK_W("out_ids", DT(U32)), U32F("max_steps")},
                  [](const uint32_t* w, const uint32_t* c) {
@@ -1429,13 +1575,14 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 2, w[4], "argmax_dec", "out_ids");
                  }});
     // 27 embed_dec: embed, state, x, hidden, vocab
-    c.push_back({"embed_dec", "fast", {256, 1, 1}, true, [](const uint32_t*) { return Grid3{1, 1, 1}; },
+    c.push_back({"embed_dec", "fast", {256, 1, 1}, true, [](const uint32_t* w) { return Grid3{w[6], 1, 1}; },
                  {TOK_R("embed", DT(BF16)), TOK_R("state", DT(U32)), TOK_W("x", DT(F32)), U32F("hidden"),
-                  U32F("vocab")},
+                  U32F("vocab"), U32F("batch")},
                  [](const uint32_t* w, const uint32_t* c) {
+                     need_batch("embed_dec", w[6]);
                      need(c, 0, int64_t(w[4]) * w[5], "embed_dec", "embed");
-                     need(c, 1, 3, "embed_dec", "state");
-                     need(c, 2, w[4], "embed_dec", "x");
+                     need(c, 1, 2 * int64_t(w[6]) + 1, "embed_dec", "state");
+                     need(c, 2, int64_t(w[6]) * w[4], "embed_dec", "x");
                  }});
     // 28 fill_normal_f16: y, n, seed_lo, seed_hi, stream_lo, stream_hi, std
     c.push_back({"fill_normal_f16", "fast", {256, 1, 1}, true,
@@ -1466,6 +1613,39 @@ std::vector<KernelSpec> fast_catalog() {
                  [](const uint32_t* w, const uint32_t* c) {
                      need(c, 0, int64_t(w[3]) * kArgmaxParts * 2, "argmax_rows_final", "partials");
                      need(c, 1, w[3], "argmax_rows_final", "out");
+                 }});
+    // 32 gemm_skinny_f32: a, w, y, m, n, k
+    c.push_back({"gemm_skinny_f32", "fast", {512, 1, 1}, false,
+                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 31) / 32, 1, 1}; },
+                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F32)), U32F("m"), U32F("n"), U32F("k")},
+                 [](const uint32_t* w, const uint32_t* c) { check_skinny("gemm_skinny_f32", w, c, w[5], w[5]); }});
+    // 33 gemm_skinny_residual: a, w, x, m, n, k
+    c.push_back({"gemm_skinny_residual", "fast", {512, 1, 1}, false,
+                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 31) / 32, 1, 1}; },
+                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_RW("x", DT(F32)), U32F("m"), U32F("n"), U32F("k")},
+                 [](const uint32_t* w, const uint32_t* c) { check_skinny("gemm_skinny_residual", w, c, w[5], w[5]); }});
+    // 34 gemm_skinny_swiglu: a, w (2 inter rows), y, m, inter, k
+    c.push_back({"gemm_skinny_swiglu", "fast", {512, 1, 1}, false,
+                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 15) / 16, 1, 1}; },
+                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F16)), U32F("m"), U32F("inter"), U32F("k")},
+                 [](const uint32_t* w, const uint32_t* c) {
+                     check_skinny("gemm_skinny_swiglu", w, c, 2 * int64_t(w[5]), w[5]);
+                 }});
+    // 35 attention_combine_f16: partials, y (f16), state, q_heads, max_pos, batch
+    c.push_back({"attention_combine_f16", "fast", {256, 1, 1}, false,
+                 [](const uint32_t* w) { return Grid3{w[4], w[6], 1}; },
+                 {TOK_R("partials", DT(F32)), TOK_W("y", DT(F16)), TOK_R("state", DT(U32)), U32F("q_heads"),
+                  U32F("max_pos"), U32F("batch")},
+                 [](const uint32_t* w, const uint32_t* c) { check_combine("attention_combine_f16", w, c); }});
+    // 36 decode_advance: argmax, state, out_ids, batch, max_steps
+    c.push_back({"decode_advance", "fast", {256, 1, 1}, true, [](const uint32_t*) { return Grid3{1, 1, 1}; },
+                 {TOK_R("argmax", DT(U32)), TOK_RW("state", DT(U32)), TOK_W("out_ids", DT(U32)), U32F("batch"),
+                  U32F("max_steps")},
+                 [](const uint32_t* w, const uint32_t* c) {
+                     need_batch("decode_advance", w[4]);
+                     need(c, 0, w[4], "decode_advance", "argmax");
+                     need(c, 1, 2 * int64_t(w[4]) + 1, "decode_advance", "state");
+                     need(c, 2, int64_t(w[4]) * w[5], "decode_advance", "out_ids");
                  }});
     return c;
 }

@@ -183,7 +183,11 @@ QwenExec::QwenExec(Device& dev, const QwenConfig& cfg, const uint32_t* inv_freq_
         if (c.hidden % 64 || c.intermediate % 64 || c.hidden > 8192 || c.intermediate > 8192 || c.heads * 128 > 8192)
             arg_fail("the fast path takes hidden and intermediate multiples of 64 up to 8192, and heads * 128 <= 8192");
         if (c.max_pos % 64 || c.max_pos > 65536) arg_fail("the fast path takes max_pos a multiple of 64 up to 65536");
-        if (c.batch != 1) arg_fail("batched decode is not built yet: batch must be 1");
+        if (c.batch < 1 || c.batch > 16) arg_fail("the fast path decodes 1 .. 16 sequences together");
+        if (c.batch > 1 && (c.hidden % 1024 || c.intermediate % 1024 || (c.heads * 128) % 1024 || c.max_tokens < c.batch))
+            arg_fail("batched decode takes hidden, intermediate and heads * 128 multiples of 1024, and max_tokens >= batch");
+    } else if (c.batch != 1) {
+        arg_fail("the fp32 mode holds one sequence");
     }
     if (!dev_.kernels_loaded()) dev_.load_kernels();
     plan();
@@ -242,9 +246,9 @@ void QwenExec::plan() {
     add("rope.sin", Rope, F32, {MP, HD / 2}, ReadOnly);
     for (int i = 0; i < c.layers; ++i) {
         std::string p = "L" + std::to_string(i);
-        if (fast) {
-            add(p + ".k_cache", KvCache, F16, {uint32_t(c.kv_heads), MP, HD});
-            add(p + ".v_cache", KvCache, F16, {uint32_t(c.kv_heads), HD, MP});
+        if (fast) {  // sequence b's heads follow sequence b - 1's
+            add(p + ".k_cache", KvCache, F16, {uint32_t(c.batch * c.kv_heads), MP, HD});
+            add(p + ".v_cache", KvCache, F16, {uint32_t(c.batch * c.kv_heads), HD, MP});
         } else {
             add(p + ".k_cache", KvCache, F32, {MP, KC});
             add(p + ".v_cache", KvCache, F32, {MP, KC});
@@ -258,15 +262,22 @@ void QwenExec::plan() {
         add("q", Activations, F16, {MT, QC});
         add("o", Activations, F16, {MT, QC});
         add("a", Activations, F16, {MT, I});
-        add("dec.x", Activations, F32, {H});
-        add("dec.o", Activations, F32, {QC});
-        add("dec.a", Activations, F32, {I});
-        add("dec.qkv", Scratch, F32, {QC + 2 * KC});
-        add("dec.attn_partials", Scratch, F32, {uint32_t(c.heads) * (MP / 64) * 130});
-        add("dec.lm_partials", Scratch, F32, {2 * 1024});
-        add("dec.state", Scratch, U32, {4});
+        const uint32_t B = uint32_t(c.batch);
+        add("dec.x", Activations, F32, {B, H});
+        add("dec.qkv", Scratch, F32, {B, QC + 2 * KC});
+        add("dec.attn_partials", Scratch, F32, {B * uint32_t(c.heads) * (MP / 64) * 130});
+        add("dec.state", Scratch, U32, {2 * B + 2});  // pos[B], id[B], step
         add("argmax.partials", Scratch, F32, {std::min<uint32_t>(MT, 512) * 64 * 2});
-        add("dec.out_ids", Logits, U32, {MP});
+        add("dec.out_ids", Logits, U32, {MP * B});
+        if (B == 1) {  // GEMVs on the bf16 weights, f32 vectors
+            add("dec.o", Activations, F32, {QC});
+            add("dec.a", Activations, F32, {I});
+            add("dec.lm_partials", Scratch, F32, {2 * 1024});
+        } else {  // skinny MFMA GEMMs on the fp16 copies
+            add("dec.h16", Activations, F16, {B, H});
+            add("dec.o16", Activations, F16, {B, QC});
+            add("dec.a16", Activations, F16, {B, I});
+        }
     } else {
         for (const char* n : {"h", "oo", "r", "h2", "dd", "f"}) add(n, Activations, F32, {MT, H});
         for (const char* n : {"q", "qn", "qr", "o"}) add(n, Activations, F32, {MT, QC});
@@ -297,6 +308,11 @@ void QwenExec::plan() {
             add_view(lname(i, kLayerWeights[1]), p + ".qkv_proj", {QC, H}, 0);
             add_view(lname(i, kLayerWeights[2]), p + ".qkv_proj", {KC, H}, uint64_t(QC) * H);
             add_view(lname(i, kLayerWeights[3]), p + ".qkv_proj", {KC, H}, uint64_t(QC + KC) * H);
+            for (int b = 0; b < c.batch; ++b) {
+                const uint64_t off = uint64_t(b) * c.kv_heads * MP * HD;
+                add_view(p + ".k_cache.s" + std::to_string(b), p + ".k_cache", {uint32_t(c.kv_heads), MP, HD}, off);
+                add_view(p + ".v_cache.s" + std::to_string(b), p + ".v_cache", {uint32_t(c.kv_heads), HD, MP}, off);
+            }
             add_view(lname(i, kLayerWeights[8]), p + ".gate_up_proj", {I, H}, 0);
             add_view(lname(i, kLayerWeights[9]), p + ".gate_up_proj", {I, H}, uint64_t(I) * H);
         }
@@ -401,7 +417,7 @@ void QwenExec::tap_copy(CommandList* l, const std::string& name, uint32_t src, i
 
 uint32_t QwenExec::forward(int seq, int pos0, const int32_t* ids, int t_, float* logits, int logits_rows) {
     const QwenConfig& c = cfg_;
-    if (seq != 0) arg_fail("sequence %d: one sequence is planned", seq);
+    if (seq < 0 || seq >= c.batch) arg_fail("sequence %d: %d planned", seq, c.batch);
     if (t_ < 1 || pos0 < 0 || pos0 + t_ > c.max_pos)
         arg_fail("positions %d .. %d outside max_pos %d", pos0, pos0 + t_ - 1, c.max_pos);
     if (logits_rows < 0 || logits_rows > t_) arg_fail("logits_rows %d outside 0 .. %d", logits_rows, t_);
@@ -528,7 +544,7 @@ uint32_t QwenExec::forward_fp32(int pos0, int T, float* logits, int lr) {
 }
 
 uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr) {
-    (void)seq;
+    const std::string sq = ".s" + std::to_string(seq);
     const QwenConfig& c = cfg_;
     const uint32_t H = c.hidden, QC = c.heads * c.head_dim, I = c.intermediate, V = c.vocab, HD = c.head_dim,
                    MP = c.max_pos, U = uint32_t(T);
@@ -544,9 +560,9 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
         auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
         dispatch(l, "rmsnorm_rows_f16", {tk("x"), w(0), tk("h"), U, H, eps, 0});
         dispatch(l, "gemm_qkv_rope", {tk("h"), tk(p + "qkv_proj.f16"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
-                                      tk("q"), tk(p + "k_cache"), tk(p + "v_cache"), U, H, uint32_t(c.heads),
-                                      uint32_t(c.kv_heads), uint32_t(pos0), MP, eps});
-        dispatch(l, "attention_prefill_f16", {tk("q"), tk(p + "k_cache"), tk(p + "v_cache"), tk("o"), U,
+                                      tk("q"), tk(p + "k_cache" + sq), tk(p + "v_cache" + sq), U, H,
+                                      uint32_t(c.heads), uint32_t(c.kv_heads), uint32_t(pos0), MP, eps});
+        dispatch(l, "attention_prefill_f16", {tk("q"), tk(p + "k_cache" + sq), tk(p + "v_cache" + sq), tk("o"), U,
                                               uint32_t(pos0), uint32_t(c.heads), uint32_t(c.kv_heads), MP, scale});
         dispatch(l, "gemm_residual", {tk("o"), tk(p + "o_proj.f16"), tk("x"), U, H, QC});
         dispatch(l, "rmsnorm_rows_f16", {tk("x"), w(7), tk("h"), U, H, eps, 0});
@@ -600,15 +616,23 @@ void QwenExec::record_decode_fast() {
     const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
     auto tk = [&](const std::string& n) { return token(n); };
     CommandList* l = dev_.begin(true);
-    dispatch(l, "embed_dec", {tk("model.embed_tokens.weight"), tk("dec.state"), tk("dec.x"), H, V});
+    const uint32_t B = uint32_t(c.batch);
+    if (B > 1) {
+        record_decode_batch(l);
+        decode_list_ = l;
+        return;
+    }
+    dispatch(l, "embed_dec", {tk("model.embed_tokens.weight"), tk("dec.state"), tk("dec.x"), H, V, 1});
     for (int i = 0; i < c.layers; ++i) {
         const std::string p = "L" + std::to_string(i) + ".";
         auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
         dispatch(l, "gemv_norm_dec", {tk("dec.x"), w(0), tk(p + "qkv_proj"), tk("dec.qkv"), QC + 2 * KC, H, eps});
         dispatch(l, "attention_decode_f16", {tk("dec.qkv"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
                                              tk(p + "k_cache"), tk(p + "v_cache"), tk("dec.attn_partials"),
-                                             tk("dec.state"), uint32_t(c.heads), uint32_t(c.kv_heads), MP, eps, scale});
-        dispatch(l, "attention_combine", {tk("dec.attn_partials"), tk("dec.o"), tk("dec.state"), uint32_t(c.heads), MP});
+                                             tk("dec.state"), uint32_t(c.heads), uint32_t(c.kv_heads), MP, eps, scale,
+                                             1});
+        dispatch(l, "attention_combine", {tk("dec.attn_partials"), tk("dec.o"), tk("dec.state"), uint32_t(c.heads), MP,
+                                          1});
         dispatch(l, "gemv_residual_dec", {tk("dec.o"), w(4), tk("dec.x"), H, QC});
         dispatch(l, "gemv_swiglu_dec", {tk("dec.x"), w(7), tk(p + "gate_up_proj"), tk("dec.a"), I, H, eps});
         dispatch(l, "gemv_residual_dec", {tk("dec.a"), w(10), tk("dec.x"), H, I});
@@ -619,19 +643,62 @@ void QwenExec::record_decode_fast() {
     decode_list_ = l;
 }
 
+// One batched step (B > 1): embed; per layer RMSNorm -> fp16 rows, the q|k|v skinny GEMM, split-KV attention per
+// sequence (norm, RoPE and the cache append inside), the combine (fp16 out), o_proj + residual, RMSNorm, the gate/up
+// SwiGLU GEMM, down + residual; then the final norm, the lm_head GEMM over the B rows, the split argmax and the state
+// advance.
+void QwenExec::record_decode_batch(CommandList* l) {
+    const QwenConfig& c = cfg_;
+    const uint32_t H = c.hidden, QC = c.heads * c.head_dim, KC = c.kv_heads * c.head_dim, I = c.intermediate,
+                   V = c.vocab, HD = c.head_dim, MP = c.max_pos, B = uint32_t(c.batch);
+    const uint32_t eps = fbits(c.eps);
+    const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
+    auto tk = [&](const std::string& n) { return token(n); };
+    dispatch(l, "embed_dec", {tk("model.embed_tokens.weight"), tk("dec.state"), tk("dec.x"), H, V, B});
+    for (int i = 0; i < c.layers; ++i) {
+        const std::string p = "L" + std::to_string(i) + ".";
+        auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
+        dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), w(0), tk("dec.h16"), B, H, eps, 0});
+        dispatch(l, "gemm_skinny_f32", {tk("dec.h16"), tk(p + "qkv_proj.f16"), tk("dec.qkv"), B, QC + 2 * KC, H});
+        dispatch(l, "attention_decode_f16", {tk("dec.qkv"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
+                                             tk(p + "k_cache"), tk(p + "v_cache"), tk("dec.attn_partials"),
+                                             tk("dec.state"), uint32_t(c.heads), uint32_t(c.kv_heads), MP, eps, scale,
+                                             B});
+        dispatch(l, "attention_combine_f16", {tk("dec.attn_partials"), tk("dec.o16"), tk("dec.state"),
+                                              uint32_t(c.heads), MP, B});
+        dispatch(l, "gemm_skinny_residual", {tk("dec.o16"), tk(p + "o_proj.f16"), tk("dec.x"), B, H, QC});
+        dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), w(7), tk("dec.h16"), B, H, eps, 0});
+        dispatch(l, "gemm_skinny_swiglu", {tk("dec.h16"), tk(p + "gate_up_proj.f16"), tk("dec.a16"), B, I, H});
+        dispatch(l, "gemm_skinny_residual", {tk("dec.a16"), tk(p + "down_proj.f16"), tk("dec.x"), B, H, I});
+    }
+    dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), tk("model.norm.weight"), tk("dec.h16"), B, H, eps, 0});
+    dispatch(l, "gemm_skinny_f32", {tk("dec.h16"), tk("embed.f16"), tk("logits"), B, V, H});
+    dispatch(l, "argmax_rows_partial", {tk("logits"), tk("argmax.partials"), B, V});
+    dispatch(l, "argmax_rows_final", {tk("argmax.partials"), tk("argmax"), B});
+    dispatch(l, "decode_advance", {tk("argmax"), tk("dec.state"), tk("dec.out_ids"), B, MP});
+}
+
 void QwenExec::set_decode_state(const int32_t* ids, const int32_t* pos) {
     if (cfg_.mode != 1) arg_fail("on-device decode needs the fast mode");
-    uint32_t st[4] = {uint32_t(pos[0]), uint32_t(ids[0]), 0, 0};
-    if (pos[0] < 0 || pos[0] >= cfg_.max_pos) arg_fail("decode position %d outside max_pos %d", pos[0], cfg_.max_pos);
-    upload_tensor("dec.state", st, 16);
+    const int B = cfg_.batch;
+    std::vector<uint32_t> st(size_t(2 * B + 2), 0u);
+    for (int b = 0; b < B; ++b) {
+        if (pos[b] < 0 || pos[b] >= cfg_.max_pos) arg_fail("decode position %d outside max_pos %d", pos[b], cfg_.max_pos);
+        st[size_t(b)] = uint32_t(pos[b]);
+        st[size_t(B + b)] = uint32_t(ids[b]);
+    }
+    upload_tensor("dec.state", st.data(), st.size() * 4);
 }
 
 void QwenExec::run_decode_steps(int steps) {
     if (cfg_.mode != 1) arg_fail("on-device decode needs the fast mode");
     if (steps < 1) return;
-    uint32_t st[4];
-    download_tensor("dec.state", st, 16);
-    if (int64_t(st[0]) + steps > cfg_.max_pos) arg_fail("%d decode steps from position %u pass max_pos %d", steps, st[0], cfg_.max_pos);
+    const int B = cfg_.batch;
+    std::vector<uint32_t> st(size_t(2 * B + 2));
+    download_tensor("dec.state", st.data(), st.size() * 4);
+    for (int b = 0; b < B; ++b)
+        if (int64_t(st[size_t(b)]) + steps > cfg_.max_pos)
+            arg_fail("%d decode steps from position %u pass max_pos %d", steps, st[size_t(b)], cfg_.max_pos);
     if (!decode_list_) record_decode_fast();
     hipEvent_t e0, e1;
     hip_check(hipEventCreate(&e0), "event");
@@ -649,13 +716,14 @@ void QwenExec::run_decode_steps(int steps) {
 }
 
 void QwenExec::read_decode_ids(int32_t* out, int count) {
-    if (count < 0 || count > cfg_.max_pos) arg_fail("count %d", count);
+    if (count < 0 || int64_t(count) > int64_t(cfg_.max_pos) * cfg_.batch) arg_fail("count %d", count);
     download_tensor("dec.out_ids", out, uint64_t(count) * 4);
 }
 
 void QwenExec::greedy(const int32_t* prompt, int plen, int steps, int32_t* out) {
     const QwenConfig& c = cfg_;
     if (plen < 1 || steps < 1) arg_fail("greedy: empty prompt or no steps");
+    if (c.batch != 1) arg_fail("greedy decodes one sequence: use decode_batch for %d", c.batch);
     if (plen + steps - 1 > c.max_pos) arg_fail("greedy: %d positions exceed max_pos %d", plen + steps - 1, c.max_pos);
     uint32_t id = forward(0, 0, prompt, plen, nullptr, 1);
     if (id == 0xFFFFFFFFu) throw std::runtime_error("greedy: argmax of a row that holds a NaN");
@@ -684,8 +752,11 @@ void QwenExec::greedy(const int32_t* prompt, int plen, int steps, int32_t* out) 
     }
 }
 
-void QwenExec::decode_batch(const int32_t*, const int32_t*, int, int32_t*) {
-    arg_fail("batched decode is not built yet");
+void QwenExec::decode_batch(const int32_t* ids, const int32_t* pos, int steps, int32_t* out_ids) {
+    if (steps < 1) arg_fail("decode_batch: no steps");
+    set_decode_state(ids, pos);
+    run_decode_steps(steps);
+    read_decode_ids(out_ids, steps * cfg_.batch);
 }
 
 // ---------------------------------------------------------------- taps and caches
@@ -740,7 +811,7 @@ static uint16_t float_to_half(float f) {
 
 void QwenExec::read_cache(int seq, int layer, int which, int row0, int rows, float* out) {
     const QwenConfig& c = cfg_;
-    if (seq != 0 || layer < 0 || layer >= c.layers || row0 < 0 || rows < 0 || row0 + rows > c.max_pos)
+    if (seq < 0 || seq >= c.batch || layer < 0 || layer >= c.layers || row0 < 0 || rows < 0 || row0 + rows > c.max_pos)
         arg_fail("cache rows out of range");
     const int KC = c.kv_heads * c.head_dim, HD = c.head_dim, MP = c.max_pos;
     std::string n = "L" + std::to_string(layer) + (which ? ".v_cache" : ".k_cache");
@@ -748,6 +819,7 @@ void QwenExec::read_cache(int seq, int layer, int which, int row0, int rows, flo
         download_tensor(n, out, uint64_t(rows) * KC * 4, uint64_t(row0) * KC * 4);
         return;
     }
+    n += ".s" + std::to_string(seq);  // this sequence's heads
     std::vector<uint16_t> all(size_t(c.kv_heads) * MP * HD);
     download_tensor(n, all.data(), all.size() * 2);
     for (int r = 0; r < rows; ++r)
@@ -760,7 +832,7 @@ void QwenExec::read_cache(int seq, int layer, int which, int row0, int rows, flo
 
 void QwenExec::write_cache(int seq, int layer, int which, int row0, int rows, const float* in) {
     const QwenConfig& c = cfg_;
-    if (seq != 0 || layer < 0 || layer >= c.layers || row0 < 0 || rows < 0 || row0 + rows > c.max_pos)
+    if (seq < 0 || seq >= c.batch || layer < 0 || layer >= c.layers || row0 < 0 || rows < 0 || row0 + rows > c.max_pos)
         arg_fail("cache rows out of range");
     const int KC = c.kv_heads * c.head_dim, HD = c.head_dim, MP = c.max_pos;
     std::string n = "L" + std::to_string(layer) + (which ? ".v_cache" : ".k_cache");
@@ -768,6 +840,7 @@ void QwenExec::write_cache(int seq, int layer, int which, int row0, int rows, co
         upload_tensor(n, in, uint64_t(rows) * KC * 4, uint64_t(row0) * KC * 4);
         return;
     }
+    n += ".s" + std::to_string(seq);  // this sequence's heads
     std::vector<uint16_t> all(size_t(c.kv_heads) * MP * HD);
     download_tensor(n, all.data(), all.size() * 2);
     for (int r = 0; r < rows; ++r)

@@ -81,6 +81,7 @@ class QwenExec {
     uint32_t forward_fp32(int pos0, int t, float* logits, int logits_rows);
     uint32_t forward_fast(int seq, int pos0, int t, float* logits, int logits_rows);
     void record_decode_fast();
+    void record_decode_batch(CommandList* l);
     void sync_f16();  // refreshes the fp16 copies of the matrices written since the last forward
     void tap_copy(CommandList* l, const std::string& name, uint32_t src, int t, int width);
     uint32_t dispatch(CommandList* l, const char* kernel, std::vector<uint32_t> fields);

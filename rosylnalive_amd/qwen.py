@@ -148,12 +148,15 @@ class QwenModel:
     MODES = {"fp32": 0, "fast": 1, "bf16": 1}
 
     def __init__(self, backend: Optional[HipBackend], cfg: QwenConfig, mode: str = "fast", max_tokens: int = 512,
-                 taps: bool = False, inv_freq: Optional[Sequence[int]] = None):
+                 taps: bool = False, inv_freq: Optional[Sequence[int]] = None, batch: int = 1):
+        """batch: sequences held together (fast mode, 1..16): one KV cache each, prefilled one at a time with
+        forward(seq=b) and decoded together by decode_batch."""
         self.backend = backend or HipBackend(0)
         self.cfg = cfg
         self.mode = mode
+        self.batch = batch
         c = N.QwenConfigC(cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.intermediate, cfg.vocab,
-                          cfg.max_pos, cfg.eps, self.MODES[mode], max_tokens, 1, 1 if taps else 0)
+                          cfg.max_pos, cfg.eps, self.MODES[mode], max_tokens, batch, 1 if taps else 0)
         inv = np.asarray(inv_freq if inv_freq is not None else inv_freq_bits(cfg.head_dim), np.uint32)
         self._h = C.c_void_p()
         check(lib().lrm_qwen_create(self.backend.handle, C.byref(c), u32s(inv), len(inv), C.byref(self._h)))
@@ -202,10 +205,21 @@ class QwenModel:
         check(lib().lrm_qwen_greedy(self._h, prompt.ctypes.data, prompt.size, steps, out.ctypes.data))
         return out
 
-    def decode_set(self, token: int, pos: int) -> None:
-        a = np.array([token], np.int32)
-        p = np.array([pos], np.int32)
+    def decode_set(self, token, pos) -> None:
+        """The next token and its position, for every sequence (scalars when batch is 1)."""
+        a = np.ascontiguousarray(np.broadcast_to(np.asarray(token, np.int32), (self.batch,)))
+        p = np.ascontiguousarray(np.broadcast_to(np.asarray(pos, np.int32), (self.batch,)))
         check(lib().lrm_qwen_decode_set(self._h, a.ctypes.data, p.ctypes.data))
+
+    def decode_batch(self, tokens, pos, steps: int) -> np.ndarray:
+        """steps greedy decode steps of every sequence on device; returns ids [steps, batch]."""
+        a = np.ascontiguousarray(tokens, np.int32)
+        p = np.ascontiguousarray(pos, np.int32)
+        if a.shape != (self.batch,) or p.shape != (self.batch,):
+            raise ValueError(f"tokens and pos must hold {self.batch} entries")
+        out = np.empty((steps, self.batch), np.int32)
+        check(lib().lrm_qwen_decode_batch(self._h, a.ctypes.data, p.ctypes.data, steps, out.ctypes.data))
+        return out
 
     def decode_run(self, steps: int) -> None:
         check(lib().lrm_qwen_decode_run(self._h, steps))
@@ -240,14 +254,15 @@ class QwenModel:
             out[name.value.decode()] = a
         return out
 
-    def read_cache(self, layer: int, which: str, row0: int, rows: int) -> np.ndarray:
+    def read_cache(self, layer: int, which: str, row0: int, rows: int, seq: int = 0) -> np.ndarray:
         out = np.empty((rows, self.cfg.kv_heads * self.cfg.head_dim), np.float32)
-        check(lib().lrm_qwen_read_cache(self._h, 0, layer, 0 if which == "k" else 1, row0, rows, out.ctypes.data))
+        check(lib().lrm_qwen_read_cache(self._h, seq, layer, 0 if which == "k" else 1, row0, rows, out.ctypes.data))
         return out
 
-    def write_cache(self, layer: int, which: str, row0: int, data: np.ndarray) -> None:
+    def write_cache(self, layer: int, which: str, row0: int, data: np.ndarray, seq: int = 0) -> None:
         a = np.ascontiguousarray(data, np.float32)
-        check(lib().lrm_qwen_write_cache(self._h, 0, layer, 0 if which == "k" else 1, row0, a.shape[0], a.ctypes.data))
+        check(lib().lrm_qwen_write_cache(self._h, seq, layer, 0 if which == "k" else 1, row0, a.shape[0],
+                                         a.ctypes.data))
 
     def fill_cache_random(self, seed: int, rows: int) -> None:
         check(lib().lrm_qwen_fill_cache_random(self._h, seed, rows))

@@ -285,10 +285,10 @@ def test_embed_dec():
     s = Session({"e": (BF16, e.shape, RO, e), "state": (U32, (4,), 0, np.array([9, 123, 0, 0], np.uint32)),
                  "x": (F32, (hidden,), 0, None)})
     try:
-        x = s.run("embed_dec", ["x"], embed="e", state="state", x="x", hidden=hidden, vocab=vocab)["x"]
+        x = s.run("embed_dec", ["x"], embed="e", state="state", x="x", hidden=hidden, vocab=vocab, batch=1)["x"]
         assert x.tobytes() == widen(e[123]).tobytes()
         s.write("state", np.array([9, vocab, 0, 0], np.uint32))
-        x = s.run("embed_dec", ["x"], embed="e", state="state", x="x", hidden=hidden, vocab=vocab)["x"]
+        x = s.run("embed_dec", ["x"], embed="e", state="state", x="x", hidden=hidden, vocab=vocab, batch=1)["x"]
         assert np.isnan(x).all()
     finally:
         s.close()
@@ -318,9 +318,9 @@ def test_attention_decode_f16(pos):
         y = s.run_list([("attention_decode_f16", dict(qkv="qkv", q_norm="qn", k_norm="kn", cos_table="cos",
                                                       sin_table="sin", k_cache="kc", v_cache="vc", partials="part",
                                                       state="state", q_heads=16, kv_heads=8, max_pos=max_pos,
-                                                      eps=1e-6, scale=scale)),
+                                                      eps=1e-6, scale=scale, batch=1)),
                         ("attention_combine", dict(partials="part", y="y", state="state", q_heads=16,
-                                                   max_pos=max_pos))], ["y"])["y"]
+                                                   max_pos=max_pos, batch=1))], ["y"])["y"]
         q64 = qkv[None].astype(np.float64)
         qr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, :2048].copy(), qn, 1e-6), 16, pos)
         kr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, 2048:3072].copy(), kn, 1e-6), 8, pos)
@@ -374,5 +374,102 @@ def test_argmax_rows_split_matches_cpuref():
         ref = cpuref.argmax_rows(x)
         assert out.tolist() == ref.tolist(), (out, ref)
         assert out[1] == 5 and out[2] == 0xFFFFFFFF and out[3] == 0 and out[4] == 0 and out[5] == cols - 1
+    finally:
+        s.close()
+
+
+# ---------------------------------------------------------------- batched decode kernels
+
+@pytest.mark.parametrize("m,n,k", [(1, 96, 1024), (5, 4096, 1024), (16, 2048, 2048), (16, 1000, 3072)])
+def test_gemm_skinny(m, n, k):
+    r = np.random.default_rng(m * 31 + n + k)
+    a = f16(r.standard_normal((m, k)))
+    w = f16(r.standard_normal((n, k)) * 0.05)
+    x0 = r.standard_normal((m, n)).astype(np.float32)
+    s = Session({"a": (F16, (m, k), RO, a), "w": (F16, (n, k), RO, w), "y": (F32, (m, n), 0, None),
+                 "x": (F32, (m, n), 0, x0)})
+    try:
+        ref = hwiden(a).astype(np.float64) @ hwiden(w).astype(np.float64).T
+        y = s.run("gemm_skinny_f32", ["y"], a="a", w="w", y="y", m=m, n=n, k=k)["y"]
+        assert written_everywhere(y) and metrics.rel_l2(y, ref) < 1e-6
+        s.run_list([("gemm_skinny_residual", dict(a="a", w="w", x="x", m=m, n=n, k=k))], [], reset={"x": x0})
+        assert metrics.rel_l2(s.read("x"), x0 + ref) < 1e-6
+    finally:
+        s.close()
+
+
+def test_gemm_skinny_swiglu():
+    m, inter, k = 11, 3072, 1024
+    r = np.random.default_rng(21)
+    a = f16(r.standard_normal((m, k)))
+    w = f16(r.standard_normal((2 * inter, k)) * 0.05)
+    s = Session({"a": (F16, (m, k), RO, a), "w": (F16, w.shape, RO, w), "y": (F16, (m, inter), 0, None)})
+    try:
+        y = hwiden(s.run("gemm_skinny_swiglu", ["y"], a="a", w="w", y="y", m=m, inter=inter, k=k)["y"])
+        h = hwiden(a).astype(np.float64) @ hwiden(w).astype(np.float64).T
+        g, u = h[:, :inter], h[:, inter:]
+        assert metrics.rel_l2(y, g / (1 + np.exp(-g)) * u) < 2e-3
+    finally:
+        s.close()
+
+
+def test_attention_decode_batched_f16_combine():
+    """Three sequences at positions 5, 64 and 700 in one dispatch (batch on the grid), then the fp16 combine; each
+    sequence against CpuRef F64 on its own cache."""
+    max_pos, S = 1024, 16
+    positions = [5, 64, 700]
+    B = len(positions)
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), max_pos)
+    r = np.random.default_rng(33)
+    qkv = (r.standard_normal((B, 4096)) * 1.5).astype(np.float32)
+    qn = bf16(1 + 0.1 * r.standard_normal(128))
+    kn = bf16(1 + 0.1 * r.standard_normal(128))
+    kcs, vcs, rows = [], [], []
+    for b, pos in enumerate(positions):
+        _, kb, vb = _qkv_inputs(1, pos, max_pos, seed=100 + b)
+        kc, vc = _caches(kb[:pos], vb[:pos], max_pos, fill=0x7E00)
+        kcs.append(kc); vcs.append(vc); rows.append((kb[:pos], vb[:pos]))
+    state = np.array(positions + [0] * B + [0, 0], np.uint32)
+    s = Session({"qkv": (F32, qkv.shape, RO, qkv), "qn": (BF16, (128,), RO, qn), "kn": (BF16, (128,), RO, kn),
+                 "cos": (F32, cos.shape, RO, cos), "sin": (F32, sin.shape, RO, sin),
+                 "kc": (F16, (B * 8, max_pos, 128), 0, np.concatenate(kcs)),
+                 "vc": (F16, (B * 8, 128, max_pos), 0, np.concatenate(vcs)),
+                 "part": (F32, (B * 16 * S * 130,), 0, None), "y": (F16, (B, 2048), 0, None),
+                 "state": (U32, state.shape, RO, state)})
+    try:
+        scale = float(cpuref.attention_scale(128, np.float32))
+        y = hwiden(s.run_list([("attention_decode_f16", dict(qkv="qkv", q_norm="qn", k_norm="kn", cos_table="cos",
+                                                             sin_table="sin", k_cache="kc", v_cache="vc",
+                                                             partials="part", state="state", q_heads=16, kv_heads=8,
+                                                             max_pos=max_pos, eps=1e-6, scale=scale, batch=B)),
+                               ("attention_combine_f16", dict(partials="part", y="y", state="state", q_heads=16,
+                                                              max_pos=max_pos, batch=B))], ["y"])["y"])
+        kc2 = s.read("kc").reshape(B, 8, max_pos, 128)
+        vc2 = s.read("vc").reshape(B, 8, 128, max_pos)
+        for b, pos in enumerate(positions):
+            q64 = qkv[b][None].astype(np.float64)
+            qr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, :2048].copy(), qn, 1e-6), 16, pos)
+            k_new = hwiden(kc2[b, :, pos, :]).reshape(1, 1024)
+            v_new = hwiden(vc2[b, :, :, pos]).reshape(1, 1024)
+            kf = np.concatenate([hwiden(rows[b][0]), k_new]).astype(np.float64)
+            vf = np.concatenate([hwiden(rows[b][1]), v_new]).astype(np.float64)
+            ref = cpuref.attention(qr, kf, vf, 16, 8, 128, pos, scale)
+            err = metrics.max_abs(y[b], ref[0])
+            print(f"batched decode attention seq {b} pos {pos}: max-abs {err:.3g}", flush=True)
+            assert err <= 2e-3, (b, err)  # fp16 output rounding included
+    finally:
+        s.close()
+
+
+def test_decode_advance():
+    B = 5
+    state = np.array([10, 11, 12, 13, 14, 1, 2, 3, 4, 5, 7, 0], np.uint32)
+    am = np.array([100, 200, 300, 400, 500], np.uint32)
+    s = Session({"am": (U32, (B,), RO, am), "state": (U32, state.shape, 0, state), "out": (U32, (16 * B,), 0, None)})
+    try:
+        out = s.run_list([("decode_advance", dict(argmax="am", state="state", out_ids="out", batch=B, max_steps=16))],
+                         ["out"], reset={"state": state})["out"]
+        assert s.read("state")[:2 * B + 1].tolist() == [11, 12, 13, 14, 15, 100, 200, 300, 400, 500, 8]
+        assert out[7 * B:8 * B].tolist() == am.tolist()
     finally:
         s.close()
