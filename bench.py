@@ -5,10 +5,12 @@ head_dim 128, SwiGLU 3072, vocab 151936, tied embeddings, random N(0, 0.02) bf16
 prompt, then W warmup steps and exactly K timed decode steps (one step = one token: the recorded decode step replayed
 as a HIP graph, position and token in device memory). Defaults K = 256, W = 8: context 136 .. 392.
 
-Also measured in the same run (extra keys): 512-token prefill with all 512 x 151936 logits, 2048-token prefill with
-last-row logits, decode at 4096 context, the isolated GQA prefill attention at T = 2048, the roofline of the dominant
-decode kernel (the fused gate/up SwiGLU GEMV, timed with HIP events on the device stream), and the oracle timed on the
-host cores on a bounded sample.
+Also measured in the same run (extra keys, skipped by --no-extras): 512-token prefill with all 512 x 151936 logits,
+2048-token prefill with last-row logits, decode at 4096 context, the isolated GQA prefill attention at T = 2048, and the
+batched decode of 16 sequences of a Qwen3-1.7B-shaped model at 8K context. The roofline is that of the dominant decode
+kernel (the fused gate/up SwiGLU GEMV, timed with HIP events on the device stream). cpu_baseline is the oracle on the
+host cores on a bounded sample of the decode workload (--no-cpu skips it); cpu_configs times the oracle on the other
+workloads (tiny model, attention, 512-token prefill, a sample of the batched decode).
 """
 import argparse
 import json
@@ -25,10 +27,86 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 FP32_PEAK_TFLOPS = 157.3
 GEMV_SWIGLU_TRAFFIC_BYTES = 12675736  # measured HBM bytes per gemv_swiglu_dec launch at the 0.6B shape
+CPU_DECODE_STEPS = 128                # the bounded CPU decode sample (about 10 s on 16 host cores)
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_configs(seed, cfg06, w06, threads):
+    """The oracle timed on the other workloads of the hot path (wall clock, one run each): the tiny model's whole
+    run, the isolated attention at T = 2048, the 0.6B prefill of 512 tokens with every logit, and a stated sample of
+    the batched 1.7B decode (its 15 GB cache does not fit a CPU run: one sequence at context 8192, 2 steps)."""
+    from oracle import cpuref
+    from rosylnalive_amd.qwen import QwenConfig, inv_freq_bits, synthetic_ids, synthetic_normal_f32, synthetic_weights
+    res = {"cores": threads, "kind": "port"}
+    # A: tiny plumbing model, prompt 16, 8 greedy tokens
+    ca = QwenConfig.tiny_plumbing(max_pos=64)
+    wa = synthetic_weights(ca, seed=seed)
+    cos, sin = cpuref.rope_table(inv_freq_bits(ca.head_dim), 64)
+    oa = cpuref.QwenOracle(ca.oracle_dict(), wa, cos, sin)
+    ids = synthetic_ids(seed, "bench/tiny", 16, ca.vocab)
+    t0 = time.perf_counter()
+    oa.greedy(ids, 8)
+    res["A_tiny_run_s"] = round(time.perf_counter() - t0, 4)
+    # B: attention only, T = 2048, 16/8 heads, head_dim 128, fp32
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), 2048)
+    q = synthetic_normal_f32(seed, "bench/attn/q", (2048, 16 * 128))
+    k = synthetic_normal_f32(seed, "bench/attn/k", (2048, 8 * 128))
+    v = synthetic_normal_f32(seed, "bench/attn/v", (2048, 8 * 128))
+    ones = np.full(128, 0x3F80, np.uint16)
+    qn = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q, ones, 1e-6), 16, 0)
+    kn = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(k, ones, 1e-6), 8, 0)
+    scale = float(cpuref.attention_scale(128, np.float32))
+    t0 = time.perf_counter()
+    cpuref.attention(qn, kn, v, 16, 8, 128, 0, scale)
+    tb = time.perf_counter() - t0
+    res["B_attention_2048_s"] = round(tb, 4)
+    res["B_attention_2048_gflops"] = round(17288970240 / tb / 1e9, 1)
+    # C: 0.6B prefill of 512 tokens, all logits
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), 512)
+    d = cfg06.oracle_dict()
+    d["max_pos"] = 512
+    oc = cpuref.QwenOracle(d, w06, cos, sin)
+    ids = synthetic_ids(seed, "bench/prefill512", 512, cfg06.vocab)
+    t0 = time.perf_counter()
+    oc.forward(oc.new_cache(), 0, ids)
+    tc = time.perf_counter() - t0
+    res["C_prefill_512_s"] = round(tc, 3)
+    res["C_prefill_512_tok_s"] = round(512 / tc, 1)
+    res["C_prefill_512_gflops"] = round(640588005376 / tc / 1e9, 1)
+    del oc
+    # E (sample): the 1.7B shape, one sequence whose cache holds 8192 positions of bf16-valued N(0, 1), 2 steps
+    ce = QwenConfig.qwen3_1_7b(max_pos=8192 + 64)
+    we = synthetic_weights(ce, seed=seed)
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), ce.max_pos)
+    oe = cpuref.QwenOracle(ce.oracle_dict(), we, cos, sin)
+    kc, vc = oe.new_cache()
+    for name, arr in (("k", kc), ("v", vc)):
+        vals = synthetic_normal_f32(seed, f"bench/cpu_cache/{name}", (ce.layers, 8192, ce.kv_heads * ce.head_dim))
+        arr[:, :8192] = cpuref.bf16_widen(cpuref.bf16_narrow(vals))
+    tok = np.array([int(synthetic_ids(seed, "bench/batch16", 1, ce.vocab)[0])], np.int32)
+    t0 = time.perf_counter()
+    for s_ in range(2):
+        lg = oe.forward((kc, vc), 8192 + s_, tok)
+        tok = np.array([int(np.argmax(lg[-1]))], np.int32)
+    te = time.perf_counter() - t0
+    res["E_sample"] = "1 sequence x 2 steps at context 8193..8194 (of the 16-sequence, 64-step workload)"
+    res["E_sample_s"] = round(te, 3)
+    res["E_tok_s_per_sequence"] = round(2 / te, 3)
+    return res
 
 
 def main():
@@ -232,13 +310,15 @@ def main():
         be_e.close()
 
     if not args.no_cpu:
-        # the oracle (CpuRef F32 restated in C) on the host's cores: prefill of the same 128-token prompt, then 2
-        # decode steps; decode tok/s reported from the decode steps.
+        # The oracle (CpuRef F32 restated in C, parallel over independent outputs) on the host's cores.
+        # Headline baseline: the decode workload itself, bounded: the same 128-token prompt, then CPU_DECODE_STEPS greedy
+        # steps of the same model; value = decode tok/s over those steps.
         threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
         cpuref.set_threads(threads)
-        cos, sin = cpuref.rope_table(inv_freq_bits(HD), 256)
+        cpu_model = _cpu_model()
+        cos, sin = cpuref.rope_table(inv_freq_bits(HD), 512)
         ocfg = cfg.oracle_dict()
-        ocfg["max_pos"] = 256
+        ocfg["max_pos"] = 512
         orc = cpuref.QwenOracle(ocfg, weights, cos, sin)
         cache = orc.new_cache()
         t2 = time.perf_counter()
@@ -246,17 +326,20 @@ def main():
         t_pre = time.perf_counter() - t2
         nxt = int(np.argmax(lg[-1]))
         t3 = time.perf_counter()
-        steps = 2
-        for s in range(steps):
-            lg = orc.forward(cache, 128 + s, np.array([nxt], np.int32))
+        steps = CPU_DECODE_STEPS
+        for s_ in range(steps):
+            lg = orc.forward(cache, 128 + s_, np.array([nxt], np.int32))
             nxt = int(np.argmax(lg[-1]))
         t_dec = time.perf_counter() - t3
         out["cpu_baseline"] = {"value": round(steps / t_dec, 4), "unit": "tok/s (batch-1 decode)", "cores": threads,
-                               "kind": "port",
+                               "kind": "port", "cpu": cpu_model,
                                "sample": f"oracle (CpuRef F32 in C) on the same weights: 128-token prefill "
-                                         f"({t_pre:.2f} s, {128 / t_pre:.1f} tok/s) then {steps} decode steps "
-                                         f"({t_dec:.2f} s)"}
+                                         f"({t_pre:.2f} s, {128 / t_pre:.1f} tok/s) then {steps} greedy decode steps, "
+                                         f"context 129..{128 + steps} ({t_dec:.2f} s)"}
         log("cpu baseline:", out["cpu_baseline"])
+        if not args.no_extras:
+            out["cpu_configs"] = cpu_configs(args.seed, cfg, weights, threads)
+            log("cpu configs:", out["cpu_configs"])
 
     model.close()
     backend.close()
