@@ -59,6 +59,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm_f16(const float* x, const uint1
 // LDS and tile kt + 2 is in flight from HBM into registers.
 constexpr int GBM = 128, GBN = 128, GBK = 64, GLD = GBK + 8;  // LDS row stride (halves), padded against bank conflicts
 
+// A raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3: 32-bit data format, no swizzle): loads
+// through it take a per-lane byte offset and a scalar one, so a loop's changing k offset costs no vector registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
 enum Epi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
 
 struct GemmArgs {
@@ -82,7 +88,7 @@ struct GemmArgs {
 };
 
 template <int EPI, int BN>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
+__global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID)), "SwiGLU and QKV pair 128 columns");
     constexpr int WN = BN / 2, JT = WN / 16, BCH = BN / 32;  // columns per wave, MFMA tiles per wave, B chunks/thread
     constexpr int STAGE = (GBM + BN) * GLD;
@@ -95,11 +101,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
     // the matrix base (every matrix is under 2^31 elements). A row past the matrix is clamped to its last row: it only
     // feeds output rows / columns that are never stored, and the loads stay unconditional, so the compiler can keep
     // several tiles in flight (a guarded load makes it wait for every outstanding load).
-    int aoff[4], boff[BCH];
+    int aoff[4], boff[BCH];  // byte offsets: the loads are buffer loads with the k offset in a scalar register
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
-        aoff[i] = min(m0 + r, p.M - 1) * p.K + kc;
+        aoff[i] = (min(m0 + r, p.M - 1) * p.K + kc) * 2;
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
@@ -111,31 +117,34 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
         } else {
             n = min(n0 + r, p.N - 1);
         }
-        boff[i] = n * p.K + kc;
+        boff[i] = (n * p.K + kc) * 2;
     }
-    // Tile kt + 1 is loaded into registers at the top of iteration kt, the matrix cores work on tile kt from LDS while
-    // those loads are in flight, and the registers go to the other LDS buffer at the end of the iteration: the
-    // registers never live across the loop's back edge, so the compiler waits for the loads only after the MFMAs of
-    // the iteration have been issued.
-    u32x4 ra[4], rb[BCH];
-    auto gload = [&](int k0) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.M * p.K * 2);
+    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(p.w, (EPI == EPI_SWIGLU ? 2 * p.inter : p.N) * p.K * 2);
+    // Two register sets, two LDS buffers: tile j is loaded into set j % 2 at the top of iteration j - 2 and stored to
+    // LDS buffer j % 2 at the end of iteration j - 1, so each load has two iterations of MFMAs to land. The loop is
+    // unrolled by two so every register set is named at compile time.
+    u32x4 ra[2][4], rb[2][BCH];
+    auto gload = [&](auto set, int k0) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const u32x4*>(p.a + (aoff[i] + k0));
+        for (int i = 0; i < 4; ++i) ra[S][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, aoff[i], k0 * 2, 0);
 #pragma unroll
-        for (int i = 0; i < BCH; ++i) rb[i] = *reinterpret_cast<const u32x4*>(p.w + (boff[i] + k0));
+        for (int i = 0; i < BCH; ++i) rb[S][i] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, boff[i], k0 * 2, 0);
     };
-    auto sstore = [&](int buf) __attribute__((always_inline)) {
+    auto sstore = [&](auto set, int buf) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
         uint16_t* As = lds + buf * STAGE;
         uint16_t* Bs = As + GBM * GLD;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = t + 256 * i;
-            *reinterpret_cast<u32x4*>(As + (c >> 3) * GLD + (c & 7) * 8) = ra[i];
+            *reinterpret_cast<u32x4*>(As + (c >> 3) * GLD + (c & 7) * 8) = ra[S][i];
         }
 #pragma unroll
         for (int i = 0; i < BCH; ++i) {
             const int c = t + 256 * i;
-            *reinterpret_cast<u32x4*>(Bs + (c >> 3) * GLD + (c & 7) * 8) = rb[i];
+            *reinterpret_cast<u32x4*>(Bs + (c >> 3) * GLD + (c & 7) * 8) = rb[S][i];
         }
     };
 
@@ -145,14 +154,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < JT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nk = p.K / GBK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        gload(min(kt + 1, nk - 1) * GBK);  // unconditional, so it stays ahead of the MFMAs
-        __builtin_amdgcn_sched_barrier(0);  // keep the loads issued before this tile's LDS reads and MFMAs
+    auto mma = [&](int buf) __attribute__((always_inline)) {
         const uint16_t* As = lds + buf * STAGE;
         const uint16_t* Bs = As + GBM * GLD;
 #pragma unroll
@@ -171,8 +173,27 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs p) {
                 for (int j = 0; j < JT; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bfr[j], acc[i][j], 0, 0, 0);
         }
-        sstore(buf ^ 1);  // the other buffer was last read in iteration kt - 1, before its barrier (the last copy is unused)
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    const int nk = p.K / GBK;
+    // iteration kt (parity P): load tile kt + 2 into set P, multiply LDS buffer P, store set 1 - P (tile kt + 1) into
+    // buffer 1 - P. Loads past the last tile re-read it (clamped) and are never stored.
+    auto step = [&](auto par, int kt) __attribute__((always_inline)) {
+        constexpr int P = decltype(par)::value;
+        gload(std::integral_constant<int, P>{}, min(kt + 2, nk - 1) * GBK);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(P);
+        sstore(std::integral_constant<int, 1 - P>{}, 1 - P);
         __syncthreads();
+    };
+    gload(S0{}, 0);
+    gload(S1{}, min(1, nk - 1) * GBK);
+    sstore(S0{}, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(S0{}, kt);
+        if (kt + 1 < nk) step(S1{}, kt + 1);
     }
 
     if (EPI == EPI_F32 || EPI == EPI_RESID) {
