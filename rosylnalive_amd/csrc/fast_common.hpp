@@ -33,7 +33,12 @@ __device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f
 // IEEE half: round to nearest even (hardware conversion), and exact widening.
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
 __device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
-__device__ __forceinline__ uint32_t pack2h(float a, float b) { return uint32_t(f2h(a)) | (uint32_t(f2h(b)) << 16); }
+// Two floats to an fp16 pair, round to nearest even (one v_cvt_pk_f16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack2h(float a, float b) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, h2));
+}
 
 // The 8 halves of a uint4 widened to float.
 __device__ __forceinline__ void unpack8h(uint4 v, float* f) {
@@ -55,6 +60,17 @@ __device__ __forceinline__ void unpack8(uint4 v, float* f) {
     f[5] = __uint_as_float(v.z & 0xFFFF0000u);
     f[6] = __uint_as_float(v.w << 16);
     f[7] = __uint_as_float(v.w & 0xFFFF0000u);
+}
+
+// A workgroup barrier for LDS traffic only: this wave's LDS operations complete (lgkmcnt(0)), then s_barrier. Unlike
+// __syncthreads() it does not wait for outstanding global loads (gfx9 counts loads and stores in one counter, so the
+// release fence would drain prefetches still in flight). The empty asm statements keep the compiler from moving
+// memory operations across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt and expcnt at their maxima (no wait), lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

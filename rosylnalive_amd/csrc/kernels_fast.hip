@@ -319,7 +319,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 // k-step are ordered {4g .. 4g + 3, 16 + 4g .. 16 + 4g + 3}; V^T is read in the same order, so the sum runs over the
 // same keys.
 constexpr int kAttnRows = 32;
-__global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+__global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                                       uint16_t* y, int T, int past, int qh, int max_pos,
                                                       float scale_log2) {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[64 * 136];
@@ -347,49 +347,54 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
     const int last_row = min(row0 + kAttnRows - 1, T - 1);
     const int kend = past + last_row + 1;  // keys [0, kend) are visible to some row of the tile; kend <= max_pos
     const int qpos = past + row;
-    const uint16_t* kbase = kc + size_t(kvhead) * max_pos * 128;
-    const uint16_t* vbase = vc + size_t(kvhead) * 128 * max_pos;
+    // this KV head's K rows and V^T rows as buffer resources: per-thread byte offsets stay fixed, the key block's
+    // offset is scalar
+    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kc + size_t(kvhead) * max_pos * 128, max_pos * 256);
+    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc + size_t(kvhead) * 128 * max_pos, max_pos * 256);
+    int koff[4], voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = t + 256 * i;
+        koff[i] = ((c >> 4) * 128 + (c & 15) * 8) * 2;
+        voff[i] = ((c >> 3) * max_pos + (c & 7) * 8) * 2;
+    }
 
     // The loads of a 64-key block are unconditional (kb + 63 < max_pos: kb < kend <= max_pos, both multiples of 64);
     // keys at or past kend may hold anything. Their scores are masked, so K needs nothing; V is zeroed there after
-    // the load, since a zero weight times a NaN is still a NaN.
-    u32x4 rk[4], rv[4];
-    auto fetch = [&](int kb) __attribute__((always_inline)) {
+    // the load, since a zero weight times a NaN is still a NaN. Two register sets: key block j is loaded into set
+    // j % 2 two iterations before it is multiplied (the loop is unrolled by two so the sets are named statically).
+    u32x4 rk[2][4], rv[2][4];
+    auto fetch = [&](auto set, int kb) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
+        const int kbl = min(kb, kend - 1) & ~63;  // past the end: re-read the last block (never stored)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = t + 256 * i, key = c >> 4, dc = (c & 15) * 8;
-            rk[i] = *reinterpret_cast<const u32x4*>(kbase + size_t(kb + key) * 128 + dc);
-        }
+        for (int i = 0; i < 4; ++i) rk[S][i] = __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, koff[i], kbl * 256, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = t + 256 * i, d = c >> 3, k8 = (c & 7) * 8;
-            rv[i] = *reinterpret_cast<const u32x4*>(vbase + size_t(d) * max_pos + kb + k8);
-        }
+        for (int i = 0; i < 4; ++i) rv[S][i] = __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, voff[i], kbl * 2, 0);
     };
-    auto mask_v = [&](int kb) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = t + 256 * i, k8 = (c & 7) * 8;
-            const int valid = kend - (kb + k8);
-            if (valid < 8) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (e >= valid) rv[i][e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-            }
-        }
-    };
-    fetch(0);
-    for (int kb = 0; kb < kend; kb += 64) {
-        mask_v(kb);
-        __syncthreads();
+    auto block = [&](auto set, int kb) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
+        // store the block (V^T zeroed past kend in LDS, last block only), then queue the block two ahead into the same
+        // set; the masking is not done on the registers, so no branch depends on data still in flight
+        lds_barrier();  // every wave is done with the previous block's K and V^T
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = t + 256 * i;
-            *reinterpret_cast<u32x4*>(Ks + (c >> 4) * 136 + (c & 15) * 8) = rk[i];
-            *reinterpret_cast<u32x4*>(Vt + (c >> 3) * 72 + (c & 7) * 8) = rv[i];
+            *reinterpret_cast<u32x4*>(Ks + (c >> 4) * 136 + (c & 15) * 8) = rk[S][i];
+            *reinterpret_cast<u32x4*>(Vt + (c >> 3) * 72 + (c & 7) * 8) = rv[S][i];
         }
-        __syncthreads();
-        if (kb + 64 < kend) fetch(kb + 64);  // in flight during this block's MFMAs
+        if (kb + 64 > kend) {  // uniform
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = t + 256 * i, k8 = (c & 7) * 8;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (kb + k8 + e >= kend) Vt[(c >> 3) * 72 + k8 + e] = 0;
+            }
+        }
+        lds_barrier();
+        fetch(set, kb + 128);
+        __builtin_amdgcn_sched_barrier(0);
 
         f32x4 s[4];
 #pragma unroll
@@ -405,39 +410,41 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
         // causal mask, branch-free, only where the key block crosses the diagonal or the tile runs past T (uniform)
         const bool need_mask = kb + 63 > past + row0 || row0 + kAttnRows > T;
         const int lim = row < T ? qpos - kb : -1;  // key offsets in this block above lim are masked
+        // raw scores; the scale is folded into the exponent: p = 2^(s c - m c) with one FMA per score (c > 0, so
+        // the maximum of s c is c times the maximum of s)
         float mloc = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float v = s[kt][r] * scale_log2;
-                if (need_mask) v = (kt * 16 + 4 * g + r > lim) ? -INFINITY : v;
-                s[kt][r] = v;
-                mloc = fmaxf(mloc, v);
+                if (need_mask) s[kt][r] = (kt * 16 + 4 * g + r > lim) ? -INFINITY : s[kt][r];
+                mloc = fmaxf(mloc, s[kt][r]);
             }
         mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run, mloc);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float m_new = fmaxf(m_run, mloc);  // running max of the raw scores
+        const float mc = m_new == -INFINITY ? 0.f : m_new * scale_log2;
         // the hardware exp2 (results below 2^-126 flush to 0: weights that small are below fp16 P anyway)
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - mc);
         float lsum = 0.f;
         float pv[4][4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                pv[kt][r] = __builtin_amdgcn_exp2f(s[kt][r] - m_use);
+                pv[kt][r] = __builtin_amdgcn_exp2f(fmaf(s[kt][r], scale_log2, -mc));
                 lsum += pv[kt][r];
             }
         lsum += __shfl_xor(lsum, 16, 64);
         lsum += __shfl_xor(lsum, 32, 64);
         l_run = l_run * alpha + lsum;
         m_run = m_new;
+        if (__any(alpha != 1.0f)) {  // rescale only when some row's maximum moved (wave-uniform branch)
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
+            for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[dt][r] *= alpha;
+                for (int r = 0; r < 4; ++r) o[dt][r] *= alpha;
+        }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
             const f16x8 bq = as_f16x8(make_uint4(pack2h(pv[2 * kk][0], pv[2 * kk][1]), pack2h(pv[2 * kk][2], pv[2 * kk][3]),
@@ -452,6 +459,17 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const uint16_t* q, const u
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, o[dt], 0, 0, 0);
             }
         }
+    };
+    using A0 = std::integral_constant<int, 0>;
+    using A1 = std::integral_constant<int, 1>;
+    fetch(A0{}, 0);
+    __builtin_amdgcn_sched_barrier(0);  // set 0 issues before set 1, as in the loop, so the first wait can be partial
+    fetch(A1{}, 64);
+    // key blocks in pairs; a block past kend (odd count) is fully masked: P = 0 and V^T zeroed in LDS, so it leaves
+    // the running maximum, sum and output unchanged
+    for (int kb = 0; kb < kend; kb += 128) {
+        block(A0{}, kb);
+        block(A1{}, kb + 64);
     }
     if (row < T) {
         const float inv = 1.0f / l_run;
