@@ -316,9 +316,30 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 // as many blocks as CUs at T = 2048, so the causal triangle packs onto the CUs.
 // S^T = K Q^T (A = K rows from LDS, B = Q^T from registers) puts one query per lane column, so the online-softmax
 // statistics stay per lane; P^T is then already in the B-operand layout of O^T = V^T P^T once the key slots of the
-// k-step are ordered {4g .. 4g + 3, 16 + 4g .. 16 + 4g + 3}; V^T is read in the same order, so the sum runs over the
-// same keys.
+// k-step are ordered {4g .. 4g + 3, 16 + 4g .. 16 + 4g + 3}. V^T is kept in LDS in that order (vt_slot), so each lane
+// reads its A operand as one 16-byte load (two 8-byte loads at a 144-byte row stride run at a third of the rate).
 constexpr int kAttnRows = 32;
+
+// The LDS column of key k (0..63) in a V^T row: 32-key chunks, inside a chunk keys 4g + j -> 8g + j and
+// 16 + 4g + j -> 8g + 4 + j (g, j < 4).
+__device__ __forceinline__ int vt_slot(int k) {
+    return (k & 32) + 8 * ((k & 15) >> 2) + 4 * ((k >> 4) & 1) + (k & 3);
+}
+
+// Sum and maximum over the four lanes of a wave that share lane % 16 (lanes l, l ^ 16, l ^ 32, l ^ 48), with the
+// cross-row lane swaps: no LDS round trip. Every lane of the group gets the same bits.
+__device__ __forceinline__ float quad_max(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                                       uint16_t* y, int T, int past, int qh, int max_pos,
                                                       float scale_log2) {
@@ -381,7 +402,10 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
         for (int i = 0; i < 4; ++i) {
             const int c = t + 256 * i;
             *reinterpret_cast<u32x4*>(Ks + (c >> 4) * 136 + (c & 15) * 8) = rk[S][i];
-            *reinterpret_cast<u32x4*>(Vt + (c >> 3) * 72 + (c & 7) * 8) = rv[S][i];
+            // keys k8 .. k8 + 3 and k8 + 4 .. k8 + 7 land 8 slots apart
+            uint16_t* vd = Vt + (c >> 3) * 72 + vt_slot((c & 7) * 8);
+            *reinterpret_cast<uint2*>(vd) = make_uint2(rv[S][i].x, rv[S][i].y);
+            *reinterpret_cast<uint2*>(vd + 8) = make_uint2(rv[S][i].z, rv[S][i].w);
         }
         if (kb + 64 > kend) {  // uniform
 #pragma unroll
@@ -389,7 +413,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
                 const int c = t + 256 * i, k8 = (c & 7) * 8;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    if (kb + k8 + e >= kend) Vt[(c >> 3) * 72 + k8 + e] = 0;
+                    if (kb + k8 + e >= kend) Vt[(c >> 3) * 72 + vt_slot(k8 + e)] = 0;
             }
         }
         lds_barrier();
@@ -420,8 +444,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
                 if (need_mask) s[kt][r] = (kt * 16 + 4 * g + r > lim) ? -INFINITY : s[kt][r];
                 mloc = fmaxf(mloc, s[kt][r]);
             }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        mloc = quad_max(mloc);
         const float m_new = fmaxf(m_run, mloc);  // running max of the raw scores
         const float mc = m_new == -INFINITY ? 0.f : m_new * scale_log2;
         // the hardware exp2 (results below 2^-126 flush to 0: weights that small are below fp16 P anyway)
@@ -435,8 +458,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
                 pv[kt][r] = __builtin_amdgcn_exp2f(fmaf(s[kt][r], scale_log2, -mc));
                 lsum += pv[kt][r];
             }
-        lsum += __shfl_xor(lsum, 16, 64);
-        lsum += __shfl_xor(lsum, 32, 64);
+        lsum = quad_sum(lsum);
         l_run = l_run * alpha + lsum;
         m_run = m_new;
         if (__any(alpha != 1.0f)) {  // rescale only when some row's maximum moved (wave-uniform branch)
@@ -452,10 +474,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
                                                  pack2h(pv[2 * kk + 1][2], pv[2 * kk + 1][3])));
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
-                const uint16_t* vr = Vt + (dt * 16 + c16) * 72 + kk * 32 + 4 * g;
-                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-                const f16x8 a = as_f16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+                const f16x8 a = as_f16x8(*reinterpret_cast<const u32x4*>(Vt + (dt * 16 + c16) * 72 + kk * 32 + 8 * g));
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, o[dt], 0, 0, 0);
             }
         }
