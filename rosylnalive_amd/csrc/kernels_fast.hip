@@ -154,47 +154,77 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < JT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto mma = [&](int buf) __attribute__((always_inline)) {
+    // MFMA operands of one 32-wide k half (ks) of an LDS buffer: two named register sets, F0 for ks 0 and F1 for
+    // ks 1, so the reads of one half run under the MFMAs of the other
+    f16x8 fa[2][4], fb[2][JT];
+    auto read_frags = [&](auto ksc, int buf) __attribute__((always_inline)) {
+        constexpr int KS = decltype(ksc)::value;
         const uint16_t* As = lds + buf * STAGE;
         const uint16_t* Bs = As + GBM * GLD;
+        const int kof = KS * 32 + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            f16x8 af[4], bfr[JT];
-            const int kof = ks * 32 + 8 * g;
+        for (int i = 0; i < 4; ++i)
+            fa[KS][i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + (wm * 64 + i * 16 + c16) * GLD + kof));
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                af[i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + (wm * 64 + i * 16 + c16) * GLD + kof));
+        for (int j = 0; j < JT; ++j)
+            fb[KS][j] = as_f16x8(*reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 16 + c16) * GLD + kof));
+    };
+    auto mfma_half = [&](auto ksc) __attribute__((always_inline)) {
+        constexpr int KS = decltype(ksc)::value;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < JT; ++j)
-                bfr[j] = as_f16x8(*reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 16 + c16) * GLD + kof));
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[KS][i], fb[KS][j], acc[i][j], 0, 0, 0);
+    };
+    // the MFMAs of one half interleaved with the LDS reads of the other: MPR MFMAs, then one read
+    constexpr int NRD = 4 + JT, NMF = 4 * JT, MPR = NMF / NRD;
+    auto interleave = [&]() __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < JT; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < NRD; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, MPR, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
+        if constexpr (NMF > MPR * NRD) __builtin_amdgcn_sched_group_barrier(0x008, NMF - MPR * NRD, 0);
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
+    using K0 = std::integral_constant<int, 0>;
+    using K1 = std::integral_constant<int, 1>;
     const int nk = p.K / GBK;
-    // iteration kt (parity P): load tile kt + 2 into set P, multiply LDS buffer P, store set 1 - P (tile kt + 1) into
-    // buffer 1 - P. Loads past the last tile re-read it (clamped) and are never stored.
+    // Tile t is loaded into register set t % 2 and stored to LDS buffer t % 2. Step t (parity P), with tile t in
+    // buffer P and its ks-0 operands in F0, tile t + 1 loaded (or landing) in set 1 - P:
+    //   load tile t + 2 into set P (stored in step t - 1, so free); store set 1 - P into buffer 1 - P (read up to
+    //   the previous step, whose barrier every wave has passed); ks-0 MFMAs with the ks-1 reads of buffer P; barrier
+    //   (this wave's stores and reads complete, so buffer 1 - P is whole); ks-1 MFMAs with the ks-0 reads of buffer
+    //   1 - P. Loads past the last tile re-read it (clamped); the last step's store and reads are never used.
     auto step = [&](auto par, int kt) __attribute__((always_inline)) {
         constexpr int P = decltype(par)::value;
         gload(std::integral_constant<int, P>{}, min(kt + 2, nk - 1) * GBK);
-        __builtin_amdgcn_sched_barrier(0);
-        mma(P);
         sstore(std::integral_constant<int, 1 - P>{}, 1 - P);
-        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(K1{}, P);
+        mfma_half(K0{});
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();
+        read_frags(K0{}, 1 - P);
+        mfma_half(K1{});
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
     };
     gload(S0{}, 0);
+    __builtin_amdgcn_sched_barrier(0);  // set 0 issues before set 1, as in the loop, so the first waits can be partial
     gload(S1{}, min(1, nk - 1) * GBK);
     sstore(S0{}, 0);
-    __syncthreads();
+    lds_barrier();
+    read_frags(K0{}, 0);
+    __builtin_amdgcn_sched_barrier(0);
     for (int kt = 0; kt < nk; kt += 2) {
         step(S0{}, kt);
         if (kt + 1 < nk) step(S1{}, kt + 1);
     }
+    __syncthreads();  // the epilogues below reuse the LDS
 
     if (EPI == EPI_F32 || EPI == EPI_RESID) {
 #pragma unroll
