@@ -376,9 +376,13 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
     __shared__ __attribute__((aligned(16))) uint16_t Ks[64 * 136];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[128 * 72];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, g = lane >> 4, c16 = lane & 15;
-    const int ntile = (T + kAttnRows - 1) / kAttnRows;
-    const int row0 = (ntile - 1 - int(blockIdx.x)) * kAttnRows;  // the longest tiles start first
-    const int kvhead = blockIdx.y;
+    // Causal balance: the first half of the workgroups (in dispatch order, KV heads fastest) takes the long tiles,
+    // longest first, and the second half the short ones, shortest first, so workgroups L and L + half, which the
+    // dispatcher places in the two slots of one CU when the grid fills the chip once, carry about equal work together.
+    const int ntile = (T + kAttnRows - 1) / kAttnRows, kvh = int(gridDim.y);
+    const int L = int(blockIdx.y) * ntile + int(blockIdx.x), j = L / kvh, half = (ntile + 1) / 2;
+    const int row0 = (j < half ? ntile - 1 - j : j - half) * kAttnRows;
+    const int kvhead = L % kvh;
     const int head = kvhead * 2 + (w >> 1);
     const int row = row0 + (w & 1) * 16 + c16;  // this lane's query row
     const int QC = qh * 128;
