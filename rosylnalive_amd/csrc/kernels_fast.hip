@@ -256,7 +256,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                 for (int r = 0; r < 4; ++r) x32[((wm * 16 + i * 4 + j) * 4 + r) * 64 + lane] = acc[i][j][r];
     }
     __syncthreads();
-    if (wn == 1) return;
+    // QKV: head = blockIdx.x (q heads, then k heads, then v heads), head_dim 128 = this tile's columns.
+    const int head = blockIdx.x;
+    const bool is_q = head < p.qh, is_k = !is_q && head < p.qh + p.kvh;
+    if (wn == 1 && (EPI == EPI_SWIGLU || is_q || is_k)) return;  // V tiles: all four waves store the transpose
     // the partner half of row tile i, read back from LDS
     auto load_hi = [&](int i, float (&hi)[4][4]) {
 #pragma unroll
@@ -288,9 +291,45 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         return;
     }
 
-    // QKV: head = blockIdx.x (q heads, then k heads, then v heads), head_dim 128 = this tile's columns.
-    const int head = blockIdx.x;
-    const bool is_q = head < p.qh, is_k = !is_q && head < p.qh + p.kvh;
+    if (!is_q && !is_k) {
+        // V: the cache is V^T ([dim][position]), so the tile is transposed through LDS (after the 32 KiB of x32, rows
+        // of 128 positions padded to 136) and written as whole 256-byte rows of 16-byte stores, not 2-byte ones
+        uint16_t* Vs = lds + 16384;
+        if (wn == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float hi[4][4];
+                load_hi(i, hi);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint16_t* vr = Vs + (j * 16 + c16) * 136 + wm * 64 + i * 16 + 4 * g;
+                    *reinterpret_cast<uint2*>(vr) =
+                        make_uint2(pack2h(acc[i][j][0], acc[i][j][1]), pack2h(acc[i][j][2], acc[i][j][3]));
+                    *reinterpret_cast<uint2*>(vr + 64 * 136) =
+                        make_uint2(pack2h(hi[j][0], hi[j][1]), pack2h(hi[j][2], hi[j][3]));
+                }
+            }
+        }
+        __syncthreads();
+        const int p0 = p.pos0 + m0;
+        const bool whole = (p0 & 7) == 0 && m0 + GBM <= p.M;  // 16-byte aligned, every row of the tile present
+        const int ch = t & 15;
+        uint16_t* vbase = p.vc + size_t(head - p.qh - p.kvh) * 128 * p.max_pos + p0 + ch * 8;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int d = (t >> 4) + 16 * k;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(Vs + d * 136 + ch * 8);
+            uint16_t* dst = vbase + size_t(d) * p.max_pos;
+            if (whole) {
+                *reinterpret_cast<u32x4*>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (m0 + ch * 8 + e < p.M) dst[e] = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+            }
+        }
+        return;
+    }
     const uint16_t* nw = is_q ? p.qn : p.kn;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -312,27 +351,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int c = j * 16 + c16;  // 0..63
-                float lo = acc[i][j][r], h2 = hi[j][r];
-                if (is_q || is_k) {
-                    const float a = bf2f(nw[c]) * (lo * rr);
-                    const float b = bf2f(nw[c + 64]) * (h2 * rr);
-                    const float cs = p.cos_t[size_t(pos) * 64 + c], sn = p.sin_t[size_t(pos) * 64 + c];
-                    lo = a * cs - b * sn;
-                    h2 = b * cs + a * sn;
-                }
-                if (is_q) {
-                    uint16_t* qo = p.q_out + size_t(m) * (p.qh * 128) + head * 128;
-                    qo[c] = f2h(lo);
-                    qo[c + 64] = f2h(h2);
-                } else if (is_k) {
-                    uint16_t* ko = p.kc + (size_t(head - p.qh) * p.max_pos + pos) * 128;
-                    ko[c] = f2h(lo);
-                    ko[c + 64] = f2h(h2);
-                } else {
-                    uint16_t* vo = p.vc + size_t(head - p.qh - p.kvh) * 128 * p.max_pos + pos;
-                    vo[size_t(c) * p.max_pos] = f2h(lo);
-                    vo[size_t(c + 64) * p.max_pos] = f2h(h2);
-                }
+                const float a = bf2f(nw[c]) * (acc[i][j][r] * rr);
+                const float b = bf2f(nw[c + 64]) * (hi[j][r] * rr);
+                const float cs = p.cos_t[size_t(pos) * 64 + c], sn = p.sin_t[size_t(pos) * 64 + c];
+                const float lo = a * cs - b * sn, h2 = b * cs + a * sn;
+                uint16_t* out = is_q ? p.q_out + size_t(m) * (p.qh * 128) + head * 128
+                                     : p.kc + (size_t(head - p.qh) * p.max_pos + pos) * 128;
+                out[c] = f2h(lo);
+                out[c + 64] = f2h(h2);
             }
         }
     }

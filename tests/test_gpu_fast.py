@@ -6,7 +6,7 @@ each against the oracle or an float64 restatement on the same rounded inputs.
 import numpy as np
 import pytest
 
-from gpu_session import Session, written_everywhere
+from gpu_session import POISON_16, Session, written_everywhere
 from oracle import cpuref, metrics
 from rosylnalive_amd.gpu_core import DType, TensorFlags
 from rosylnalive_amd.qwen import inv_freq_bits, synthetic_normal_f32
@@ -74,10 +74,12 @@ def test_gemm_swiglu():
         s.close()
 
 
-def test_gemm_qkv_rope_epilogue():
+@pytest.mark.parametrize("T,pos0,max_pos", [(100, 37, 256), (300, 64, 512)])
+def test_gemm_qkv_rope_epilogue(T, pos0, max_pos):
     """q|k|v projection with the per-head RMSNorm + RoPE epilogue and the K / V^T cache writes, against CpuRef F64
-    on the same fp16 operands."""
-    T, pos0, H, max_pos = 100, 37, 256, 256
+    on the same fp16 operands: an unaligned position (element-wise V^T stores) and an aligned one (16-byte rows for the
+    two whole row tiles, element-wise for the partial third)."""
+    H = 256
     r = np.random.default_rng(11)
     h = f16(r.standard_normal((T, H)))
     w = f16(r.standard_normal((32 * 128, H)) * 0.06)
@@ -101,7 +103,8 @@ def test_gemm_qkv_rope_epilogue():
         for got, ref in [(hwiden(out["q"]), qr), (kc, kr), (vc, v)]:
             assert metrics.max_abs(got, ref) <= 2e-3 * max(1.0, np.abs(ref).max()), metrics.max_abs(got, ref)
         # rows outside [pos0, pos0 + T) are untouched
-        assert not written_everywhere(out["kc"][:, :pos0, :]) and not written_everywhere(out["vc"][:, :, :pos0])
+        for c in (out["kc"][:, :pos0, :], out["kc"][:, pos0 + T:, :], out["vc"][:, :, :pos0], out["vc"][:, :, pos0 + T:]):
+            assert np.all(c == POISON_16)
     finally:
         s.close()
 
