@@ -193,15 +193,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     using K1 = std::integral_constant<int, 1>;
     const int nk = p.K / GBK;
     // Tile t is loaded into register set t % 2 and stored to LDS buffer t % 2. Step t (parity P), with tile t in
-    // buffer P and its ks-0 operands in F0, tile t + 1 loaded (or landing) in set 1 - P:
-    //   load tile t + 2 into set P (stored in step t - 1, so free); store set 1 - P into buffer 1 - P (read up to
-    //   the previous step, whose barrier every wave has passed); ks-0 MFMAs with the ks-1 reads of buffer P; barrier
-    //   (this wave's stores and reads complete, so buffer 1 - P is whole); ks-1 MFMAs with the ks-0 reads of buffer
-    //   1 - P. Loads past the last tile re-read it (clamped); the last step's store and reads are never used.
+    // buffer P and its ks-0 operands in F0, tiles t + 1 and t + 2 loaded (or landing) in sets 1 - P and P:
+    //   store set 1 - P (tile t + 1) into buffer 1 - P (read up to the previous step, whose barrier every wave has
+    //   passed) and load tile t + 3 into it, so every load has two steps to land; ks-0 MFMAs with the ks-1 reads of
+    //   buffer P; barrier (this wave's stores and reads complete, so buffer 1 - P is whole); ks-1 MFMAs with the ks-0
+    //   reads of buffer 1 - P. Loads past the last tile re-read it (clamped); the last steps' stores and reads of
+    //   such tiles are never used.
     auto step = [&](auto par, int kt) __attribute__((always_inline)) {
         constexpr int P = decltype(par)::value;
-        gload(std::integral_constant<int, P>{}, min(kt + 2, nk - 1) * GBK);
         sstore(std::integral_constant<int, 1 - P>{}, 1 - P);
+        gload(std::integral_constant<int, 1 - P>{}, min(kt + 3, nk - 1) * GBK);
         __builtin_amdgcn_sched_barrier(0);
         read_frags(K1{}, P);
         mfma_half(K0{});
@@ -213,17 +214,24 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         interleave();
         __builtin_amdgcn_sched_barrier(0);
     };
+    // loads issue in tile order, so each wait leaves the younger tiles in flight
     gload(S0{}, 0);
-    __builtin_amdgcn_sched_barrier(0);  // set 0 issues before set 1, as in the loop, so the first waits can be partial
+    __builtin_amdgcn_sched_barrier(0);
     gload(S1{}, min(1, nk - 1) * GBK);
+    __builtin_amdgcn_sched_barrier(0);
     sstore(S0{}, 0);
+    gload(S0{}, min(2, nk - 1) * GBK);
     lds_barrier();
     read_frags(K0{}, 0);
     __builtin_amdgcn_sched_barrier(0);
-    for (int kt = 0; kt < nk; kt += 2) {
+    // whole pairs in the loop (a conditional second step would leave the loop head with set 1 possibly the younger,
+    // and the waits there would drain every load); an odd last step after it
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
         step(S0{}, kt);
-        if (kt + 1 < nk) step(S1{}, kt + 1);
+        step(S1{}, kt + 1);
     }
+    if (kt < nk) step(S0{}, kt);
     __syncthreads();  // the epilogues below reuse the LDS
 
     if (EPI == EPI_F32 || EPI == EPI_RESID) {
