@@ -1142,77 +1142,116 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* part, uint32_t
 
 // ================================================================ 32-34 skinny GEMMs (batched decode)
 // Y[r, n] = sum_k A[r, k] W[n, k] for M <= 16 rows (the sequences of a batched decode step), on f16 operands: the
-// weights are read once for all rows. A block owns two 16-column MFMA tiles (32 output columns; for SwiGLU gate
-// columns j0 .. j0 + 15 and the matching up columns) and its 8 waves split K in eight. Each wave streams its slice of
-// the W rows straight into MFMA B operands (lane: row c16, 8 halves at k + 8g, so 64 contiguous bytes per row per
-// 32-k step) with the A rows from L2, 4 steps of loads in flight, then the partial tiles of the 8 waves are summed in
-// LDS in a fixed order (deterministic). Rows of A past M and columns past N are clamped in range and never stored.
+// weights are read once for all rows. A block owns NT 16-column MFMA tiles (SwiGLU: gate columns j0 .. j0 + 15 and
+// the matching up columns; two tiles also for the plain GEMM, whose wide N (the lm_head) would otherwise read the A
+// rows from L2 once per 16 columns; one for the residual GEMMs, whose N = hidden needs the blocks) and its 8 waves
+// split K in eight. Each wave streams its slice of the W rows straight into MFMA B operands (lane: row c16, 8 halves at
+// k + 8g, so 64 contiguous bytes per row per 32-k step) with the A rows from L2, 128 k per iteration, and the next
+// iteration's loads in flight while the current one multiplies (two named register sets). The partial tiles of the 8
+// waves are summed in LDS in a fixed order (deterministic). Rows of A past M and columns past N are clamped in range
+// and never stored.
 constexpr int kSkWaves = 8;
 enum SkEpi { SK_F32 = 0, SK_RESID = 1, SK_SWIGLU = 2 };
 
 template <int EPI>
 __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const uint16_t* w, float* y32, uint16_t* y16,
                                                      int M, int N, int K, int inter) {
-    __shared__ float red[kSkWaves][2][256];
+    constexpr int NT = EPI == SK_RESID ? 1 : 2;  // MFMA column tiles per block
+    __shared__ float red[kSkWaves][NT][256];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6, g = lane >> 4, c16 = lane & 15;
-    int n0, n1;
+    int n0, n1 = 0;
     if (EPI == SK_SWIGLU) {
         const int j = min(int(blockIdx.x) * 16 + c16, inter - 1);
         n0 = j;
         n1 = inter + j;
     } else {
-        n0 = min(int(blockIdx.x) * 32 + c16, N - 1);
-        n1 = min(int(blockIdx.x) * 32 + 16 + c16, N - 1);
+        n0 = min(int(blockIdx.x) * (16 * NT) + c16, N - 1);
+        n1 = min(int(blockIdx.x) * (16 * NT) + 16 + c16, N - 1);
     }
-    const int kper = K / kSkWaves;  // a multiple of 128
+    const int kper = K / kSkWaves, niter = kper / 128;  // kper a multiple of 128
     const int kb = wv * kper + 8 * g;
     const uint16_t* ap = a + size_t(min(c16, M - 1)) * K + kb;
     const uint16_t* w0 = w + size_t(n0) * K + kb;
     const uint16_t* w1 = w + size_t(n1) * K + kb;
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < kper; k += 128) {
-        u32x4 av[4], b0[4], b1[4];
+    u32x4 av[2][4], bw[2][NT][4];
+    auto load = [&](auto set, int it) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
+        const int k = it * 128;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            b0[s] = *reinterpret_cast<const u32x4*>(w0 + k + 32 * s);
-            b1[s] = *reinterpret_cast<const u32x4*>(w1 + k + 32 * s);
-            av[s] = *reinterpret_cast<const u32x4*>(ap + k + 32 * s);
+            bw[S][0][s] = *reinterpret_cast<const u32x4*>(w0 + k + 32 * s);
+            if constexpr (NT == 2) bw[S][NT - 1][s] = *reinterpret_cast<const u32x4*>(w1 + k + 32 * s);
+            av[S][s] = *reinterpret_cast<const u32x4*>(ap + k + 32 * s);
         }
+    };
+    auto mma = [&](auto set) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av[s]), as_f16x8(b0[s]), acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av[s]), as_f16x8(b1[s]), acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av[S][s]), as_f16x8(bw[S][0][s]), acc0, 0, 0, 0);
+            if constexpr (NT == 2)
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av[S][s]), as_f16x8(bw[S][NT - 1][s]), acc1, 0, 0,
+                                                              0);
         }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    // The scheduling barriers keep each set's loads ahead of the other set's MFMAs (left alone, the compiler sinks
+    // them between the MFMAs and drains every load at the end of each iteration). The loop runs while two more
+    // iterations exist, so no load is issued past the end and the loop head always has set 0 as the younger load.
+    load(S0{}, 0);
+    int it = 0;
+    for (; it + 2 < niter; it += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        load(S1{}, it + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(S0{});
+        __builtin_amdgcn_sched_barrier(0);
+        load(S0{}, it + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(S1{});
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < niter) {
+        load(S1{}, it + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(S0{});
+        __builtin_amdgcn_sched_barrier(0);
+        mma(S1{});
+    } else {
+        mma(S0{});
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         red[wv][0][lane * 4 + i] = acc0[i];
-        red[wv][1][lane * 4 + i] = acc1[i];
+        if constexpr (NT == 2) red[wv][NT - 1][lane * 4 + i] = acc1[i];
     }
     __syncthreads();
     // element e of a tile: lane e / 4, register e % 4 -> row 4 (lane / 16) + e % 4, column lane % 16
     if (EPI == SK_SWIGLU) {
         if (t >= 256) return;
+        const int l = t >> 2, row = 4 * (l >> 4) + (t & 3), col = int(blockIdx.x) * 16 + (l & 15);
         float gv = 0.f, uv = 0.f;
 #pragma unroll
         for (int i = 0; i < kSkWaves; ++i) {
             gv += red[i][0][t];
-            uv += red[i][1][t];
+            uv += red[i][NT - 1][t];
         }
-        const int l = t >> 2, row = 4 * (l >> 4) + (t & 3), j = int(blockIdx.x) * 16 + (l & 15);
-        if (row < M && j < inter) y16[size_t(row) * inter + j] = f2h(gv / (1.0f + __expf(-gv)) * uv);
+        if (row < M && col < inter) y16[size_t(row) * inter + col] = f2h(gv / (1.0f + __expf(-gv)) * uv);
         return;
     }
+    if (t >= 256 * NT) return;
     const int tile = t >> 8, e = t & 255;
+    const int l = e >> 2, row = 4 * (l >> 4) + (e & 3), col = int(blockIdx.x) * (16 * NT) + tile * 16 + (l & 15);
     float v = 0.f;
 #pragma unroll
     for (int i = 0; i < kSkWaves; ++i) v += red[i][tile][e];
-    const int l = e >> 2, row = 4 * (l >> 4) + (e & 3), n = int(blockIdx.x) * 32 + tile * 16 + (l & 15);
-    if (row >= M || n >= N) return;
+    if (row >= M || col >= N) return;
     if (EPI == SK_RESID)
-        y32[size_t(row) * N + n] += v;
+        y32[size_t(row) * N + col] += v;
     else
-        y32[size_t(row) * N + n] = v;
+        y32[size_t(row) * N + col] = v;
 }
 
 // ---------------------------------------------------------------- 36 decode_advance
@@ -1455,7 +1494,7 @@ static void l_gemm_skinny_f32(const PreparedDispatch& pd, void* const* p, hipStr
 }
 static void l_gemm_skinny_resid(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    hipLaunchKernelGGL((k_gemm_skinny<SK_RESID>), dim3((w[5] + 31) / 32), dim3(512), 0, s, (const uint16_t*)p[0],
+    hipLaunchKernelGGL((k_gemm_skinny<SK_RESID>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
                        (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
 }
 static void l_gemm_skinny_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
@@ -1747,7 +1786,7 @@ std::vector<KernelSpec> fast_catalog() {
                  [](const uint32_t* w, const uint32_t* c) { check_skinny("gemm_skinny_f32", w, c, w[5], w[5]); }});
     // 33 gemm_skinny_residual: a, w, x, m, n, k
     c.push_back({"gemm_skinny_residual", "fast", {512, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 31) / 32, 1, 1}; },
+                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 15) / 16, 1, 1}; },
                  {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_RW("x", DT(F32)), U32F("m"), U32F("n"), U32F("k")},
                  [](const uint32_t* w, const uint32_t* c) { check_skinny("gemm_skinny_residual", w, c, w[5], w[5]); }});
     // 34 gemm_skinny_swiglu: a, w (2 inter rows), y, m, inter, k
