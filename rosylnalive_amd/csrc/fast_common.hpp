@@ -40,13 +40,20 @@ __device__ __forceinline__ uint32_t pack2h(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, h2));
 }
 
-// The 8 halves of a uint4 widened to float.
+// The 8 halves of a uint4 (or u32x4) widened to float.
 __device__ __forceinline__ void unpack8h(uint4 v, float* f) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         f[2 * i] = h2f(uint16_t(w[i] & 0xFFFFu));
         f[2 * i + 1] = h2f(uint16_t(w[i] >> 16));
+    }
+}
+__device__ __forceinline__ void unpack8h(u32x4 v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = h2f(uint16_t(v[i] & 0xFFFFu));
+        f[2 * i + 1] = h2f(uint16_t(v[i] >> 16));
     }
 }
 

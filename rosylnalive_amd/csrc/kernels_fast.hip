@@ -659,21 +659,28 @@ __global__ __launch_bounds__(256) void k_gemv_norm_dec(const float* x, const uin
 }
 
 // ---------------------------------------------------------------- 21 attention_decode_f16
-// Split-KV decode attention over positions 0 .. pos = state[0]. Block (s, kv head) takes keys [64 s, 64 s + 64) for
-// the two query heads of the group. It issues the loads of its cached keys and values first, then applies the q
-// RMSNorm and RoPE to the raw projection; the block whose split holds pos also computes the new key (k RMSNorm +
-// RoPE) and value, appends them (fp16) to the caches and uses the same rounded values in place of the stale slot it
-// loaded. Each block writes, per head, (max, sum, unnormalised output[128]) of its keys in the log2 domain; splits
-// past pos do nothing.
+// Split-KV decode attention over positions 0 .. pos = state[b]. Block (s, kv head, b) takes keys [64 C s, 64 C s +
+// 64 C) (C = chunks per split, chosen by the caller so the grid still fills the chip: 1 for one sequence, more for a
+// batch at long context) for the two query heads of the group, 64 keys at a time. It issues the loads of its first two
+// chunks, then applies the q RMSNorm and RoPE to the raw projection; the block whose split holds pos also computes the
+// new key (k RMSNorm + RoPE) and value, appends them (fp16) to the caches and uses the same rounded values in place of
+// the stale slot it loaded. Per chunk: scores (each key's dot over 16 lanes), an online softmax per head in the log2
+// domain, and P V accumulated per thread (its 4 dims x 8 keys, rescaled when the maximum moves), with the chunk two
+// ahead loading meanwhile; the 8 key groups are reduced once at the end. Each block writes, per head, (max, sum,
+// unnormalised output[128]); splits past pos do nothing. Positions past pos are loaded (they lie inside max_pos) but
+// masked by selects: the scores to -inf, the values to 0 (unwritten positions may hold anything).
+// MULTI = false is the one-chunk form (chunks == 1): no second register set and no loop, so the registers stay low
+// enough for many blocks per CU, which the one-sequence decode needs (its splits are its only parallelism).
+template <bool MULTI>
 __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16_t* qn, const uint16_t* kn,
                                                   const float* cos_t, const float* sin_t, uint16_t* kc, uint16_t* vc,
                                                   float* part, const uint32_t* state, int qh, int kvh, int max_pos,
-                                                  float eps, float scale_log2) {
+                                                  float eps, float scale_log2, int chunks) {
     __shared__ float qs[2][128];
     __shared__ float knew[128];
     __shared__ float vnew[128];
     __shared__ float ps[2][64];
-    __shared__ float stat[2][2];
+    __shared__ float alpha_s[2];
     __shared__ float redq[4], redk[4];
     const int s = blockIdx.x, S = gridDim.x, kvhead = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int b = blockIdx.z;  // the sequence: its projections, caches and partials follow the previous ones
@@ -683,35 +690,46 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
     kc += size_t(b) * kvh * max_pos * 128;
     vc += size_t(b) * kvh * 128 * max_pos;
     part += size_t(b) * qh * S * 130;
-    const int key0 = s * 64;
-    const int nkeys = min(64, pos + 1 - key0);
+    const int key0 = s * 64 * chunks;
+    const int nkeys = min(64 * chunks, pos + 1 - key0);  // keys of this split at or before pos
     if (nkeys <= 0) return;
-    const bool last = s == (pos >> 6);  // uniform over the block
-    const int jnew = pos - key0;        // the new key's slot when `last`
+    const int nch = (nkeys + 63) / 64;  // chunks to run; the last one ends inside max_pos (a multiple of 64)
+    const bool has_pos = pos < key0 + 64 * chunks;  // uniform over the block
+    const int jnew = pos - key0;                     // the new key's offset in the split when has_pos
 
-    // 1) all loads together: this split's keys (thread: 4 keys x 8 dims) and values (4 dims x 8 keys), the raw
-    // projections, the norm weights and the rotation of pos
-    const uint16_t* kb = kc + (size_t(kvhead) * max_pos + key0) * 128;
-    const int d0 = 8 * (lane & 15);
-    uint4 kv4[4];
+    // thread mapping: K as 4 keys (wv * 16 + it * 4 + lane / 16) x 8 dims (d0); V^T as 4 dims (rg + 32 dd) x 8 keys
+    const int d0 = 8 * (lane & 15), sub = t & 7, rg = t >> 3;
+    const uint16_t* kb = kc + (size_t(kvhead) * max_pos + key0) * 128 + d0;
+    const uint16_t* vb = vc + size_t(kvhead) * 128 * max_pos + key0 + sub * 8;
+    u32x4 kv4[2][4], vv[2][4];
+    auto fetch = [&](auto set, int c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set)::value;
+        c = min(c, nch - 1) * 64;  // past the last chunk: re-read it (an L2 hit, never used)
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int key = wv * 16 + it * 4 + (lane >> 4);
-        kv4[it] = key < nkeys ? *reinterpret_cast<const uint4*>(kb + size_t(key) * 128 + d0) : make_uint4(0, 0, 0, 0);
+        for (int it = 0; it < 4; ++it)
+            kv4[SET][it] = *reinterpret_cast<const u32x4*>(kb + size_t(c + wv * 16 + it * 4 + (lane >> 4)) * 128);
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd)
+            vv[SET][dd] = *reinterpret_cast<const u32x4*>(vb + size_t(rg + 32 * dd) * max_pos + c);
+    };
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    fetch(C0{}, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (MULTI) {
+        fetch(C1{}, 1);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    const int sub = t & 7, rg = t >> 3;
-    const uint16_t* vb = vc + size_t(kvhead) * 128 * max_pos + key0 + sub * 8;  // key0 + 63 < max_pos
-    uint4 vv[4];
-#pragma unroll
-    for (int dd = 0; dd < 4; ++dd) vv[dd] = *reinterpret_cast<const uint4*>(vb + size_t(rg + 32 * dd) * max_pos);
+
+    // the raw projections, the norm weights and the rotation of pos
     const int hh = t >> 7, d = t & 127;  // thread t: q head 2 kvhead + hh; new key (hh = 0) or value (hh = 1); dim d
     const int QC = qh * 128, KC = kvh * 128;
     const float qv = qkv[(kvhead * 2 + hh) * 128 + d];
-    const float kvv = last ? qkv[QC + hh * KC + kvhead * 128 + d] : 0.f;
+    const float kvv = has_pos ? qkv[QC + hh * KC + kvhead * 128 + d] : 0.f;
     const float cs = cos_t[size_t(pos) * 64 + (d & 63)], sn = sin_t[size_t(pos) * 64 + (d & 63)];
     const float qw = bf2f(qn[d]), kw = bf2f(kn[d]);
 
-    // 2) per-head RMSNorm (head hh = waves 2 hh, 2 hh + 1; the new key = waves 0, 1), then the rotation of (d, d + 64)
+    // per-head RMSNorm (head hh = waves 2 hh, 2 hh + 1; the new key = waves 0, 1), then the rotation of (d, d + 64)
     const float sq = wave_sum(qv * qv), sk = wave_sum(kvv * kvv);
     if (lane == 0) {
         redq[wv] = sq;
@@ -727,7 +745,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
     const float krot = d < 64 ? kr * cs - knew[d + 64] * sn : kr * cs + knew[d - 64] * sn;
     __syncthreads();
     qs[hh][d] = qrot;
-    if (last) {
+    if (has_pos) {
         if (hh == 0) {
             const uint16_t kh = f2h(krot);
             knew[d] = h2f(kh);
@@ -739,99 +757,136 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
         }
     }
     __syncthreads();
-
-    // 3) scores of the split's keys for both heads
-    float q0[8], q1[8];
+    // this thread's query dims and, for the split holding pos, its slices of the new key and value (read
+    // unconditionally, used only through selects: a conditional LDS read would become a branch per element)
+    float q0[8], q1[8], kn8[8], vn4[4];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         q0[e] = qs[0][d0 + e];
         q1[e] = qs[1][d0 + e];
+        kn8[e] = knew[d0 + e];
     }
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int key = wv * 16 + it * 4 + (lane >> 4);
-        float kf[8];
-        unpack8h(kv4[it], kf);
-        if (last && key == jnew) {
+    for (int dd = 0; dd < 4; ++dd) vn4[dd] = vnew[rg + 32 * dd];
+
+    float m_run = -INFINITY, l_run = 0.f;  // waves 0 and 1: the running statistics of head wv
+    float o0[4] = {0.f, 0.f, 0.f, 0.f}, o1[4] = {0.f, 0.f, 0.f, 0.f};
+    // masked keys (past pos) and the new key (= pos, when this split holds it) lie in the split's last chunk only:
+    // TAIL instantiates the selects for it, the other chunks run without them
+    auto chunk = [&](auto set, auto tailc, int c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set)::value;
+        constexpr bool tail = decltype(tailc)::value;
+        const int cb = c * 64;  // the chunk's first key, as an offset in the split
+        // scores of the chunk's keys for both heads
 #pragma unroll
-            for (int e = 0; e < 8; ++e) kf[e] = knew[d0 + e];
+        for (int it = 0; it < 4; ++it) {
+            const int key = wv * 16 + it * 4 + (lane >> 4);
+            float kf[8];
+            unpack8h(kv4[SET][it], kf);
+            if constexpr (tail) {
+                const bool is_new = has_pos && cb + key == jnew;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) kf[e] = is_new ? kn8[e] : kf[e];
+            }
+            float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                a0 = fmaf(q0[e], kf[e], a0);
+                a1 = fmaf(q1[e], kf[e], a1);
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                a0 += __shfl_xor(a0, o, 64);
+                a1 += __shfl_xor(a1, o, 64);
+            }
+            if ((lane & 15) == 0) {
+                const bool ok = !tail || cb + key < nkeys;
+                ps[0][key] = ok ? a0 * scale_log2 : -INFINITY;
+                ps[1][key] = ok ? a1 * scale_log2 : -INFINITY;
+            }
         }
-        float a0 = 0.f, a1 = 0.f;
+        __syncthreads();
+        if (wv < 2) {  // online softmax of head wv over this chunk (key 0 of a chunk is always valid)
+            const float v = ps[wv][lane];
+            const float m_new = fmaxf(m_run, wave_max(v));
+            const float e = exp2f(v - m_new);
+            const float al = exp2f(m_run - m_new);  // 0 on the first chunk
+            l_run = l_run * al + wave_sum(e);
+            m_run = m_new;
+            ps[wv][lane] = e;
+            if (lane == 0) alpha_s[wv] = al;
+        }
+        __syncthreads();
+        // P V: thread t covers V^T rows rg + 32 dd and keys 8 sub .. + 7 of the chunk
+        float e0[8], e1[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            a0 = fmaf(q0[e], kf[e], a0);
-            a1 = fmaf(q1[e], kf[e], a1);
+            e0[e] = ps[0][sub * 8 + e];
+            e1[e] = ps[1][sub * 8 + e];
         }
+        const float al0 = alpha_s[0], al1 = alpha_s[1];
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            a0 += __shfl_xor(a0, o, 64);
-            a1 += __shfl_xor(a1, o, 64);
+        for (int dd = 0; dd < 4; ++dd) {
+            float vf[8];
+            unpack8h(vv[SET][dd], vf);
+            if constexpr (tail) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int key = cb + sub * 8 + e;
+                    vf[e] = key >= nkeys ? 0.f : (has_pos && key == jnew ? vn4[dd] : vf[e]);
+                }
+            }
+            float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                a0 = fmaf(e0[e], vf[e], a0);
+                a1 = fmaf(e1[e], vf[e], a1);
+            }
+            o0[dd] = fmaf(o0[dd], al0, a0);
+            o1[dd] = fmaf(o1[dd], al1, a1);
         }
-        if ((lane & 15) == 0) {
-            ps[0][key] = key < nkeys ? a0 * scale_log2 : -INFINITY;
-            ps[1][key] = key < nkeys ? a1 * scale_log2 : -INFINITY;
+        __syncthreads();  // ps and alpha_s are rewritten by the next chunk
+    };
+    using Body = std::false_type;
+    using Tail = std::true_type;
+    if constexpr (!MULTI) {
+        chunk(C0{}, Tail{}, 0);
+    } else {
+        int c = 0;
+        for (; c + 2 < nch; c += 2) {  // whole pairs before the last chunk: the loop head has set 0 as the older load
+            chunk(C0{}, Body{}, c);
+            fetch(C0{}, c + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            chunk(C1{}, Body{}, c + 1);
+            fetch(C1{}, c + 3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (c + 1 < nch) {  // two chunks left (set 0, set 1), the second the last
+            chunk(C0{}, Body{}, c);
+            chunk(C1{}, Tail{}, c + 1);
+        } else {
+            chunk(C0{}, Tail{}, c);
         }
     }
-    __syncthreads();
-    if (wv < 2) {
-        const float v = ps[wv][lane];
-        const float m = wave_max(v);  // key 0 of the split is always valid: m is finite
-        const float e = exp2f(v - m);
-        const float l = wave_sum(e);
-        ps[wv][lane] = e;
-        if (lane == 0) {
-            stat[wv][0] = m;
-            stat[wv][1] = l;
-        }
-    }
-    __syncthreads();
 
-    // 4) P V: thread t covers V^T rows d = (t >> 3) + 32 dd and keys 8 (t & 7) .. + 7 of the split
-    float e0[8], e1[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        e0[e] = ps[0][sub * 8 + e];
-        e1[e] = ps[1][sub * 8 + e];
-    }
-    const bool full = sub * 8 + 8 <= nkeys;
-    const bool has_new = last && (jnew >> 3) == sub;
+    // reduce the 8 key groups (lanes differing in t & 7) and write the partials
     float* myp = part + (size_t(kvhead * 2) * S + s) * 130;  // head 2 kvhead + hh at + hh * S * 130
 #pragma unroll
     for (int dd = 0; dd < 4; ++dd) {
-        const int dim = rg + 32 * dd;
-        float vf[8];
-        unpack8h(vv[dd], vf);
-        if (!full) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (sub * 8 + e >= nkeys) vf[e] = 0.f;  // unwritten positions may hold anything
-        }
-        if (has_new) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (sub * 8 + e == jnew) vf[e] = vnew[dim];
-        }
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            a0 = fmaf(e0[e], vf[e], a0);
-            a1 = fmaf(e1[e], vf[e], a1);
-        }
+        float a0 = o0[dd], a1 = o1[dd];
 #pragma unroll
         for (int o = 1; o < 8; o <<= 1) {
             a0 += __shfl_xor(a0, o, 64);
             a1 += __shfl_xor(a1, o, 64);
         }
         if (sub == 0) {
-            myp[2 + dim] = a0;
-            myp[size_t(S) * 130 + 2 + dim] = a1;
+            myp[2 + rg + 32 * dd] = a0;
+            myp[size_t(S) * 130 + 2 + rg + 32 * dd] = a1;
         }
     }
-    if (t == 0) {
-        myp[0] = stat[0][0];
-        myp[1] = stat[0][1];
-        myp[size_t(S) * 130] = stat[1][0];
-        myp[size_t(S) * 130 + 1] = stat[1][1];
+    if (wv < 2 && lane == 0) {
+        myp[size_t(wv) * S * 130] = m_run;
+        myp[size_t(wv) * S * 130 + 1] = l_run;
     }
 }
 
@@ -841,14 +896,14 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
 constexpr int kMaxSplits = 1024;
 template <typename OUT>
 __global__ __launch_bounds__(256) void k_attn_combine(const float* part, OUT* y, const uint32_t* state, int splits,
-                                                      int max_pos) {
+                                                      int split_keys, int max_pos) {
     __shared__ float sc[kMaxSplits];
     __shared__ float red[4];
     __shared__ float o_hi[128];
     const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int pos = int(state[b]);
     if (pos < 0 || pos >= max_pos) return;
-    const int used = min(pos / 64 + 1, splits);
+    const int used = min(pos / split_keys + 1, splits);
     const float* hp = part + (size_t(b) * gridDim.x + h) * splits * 130;
     float m = -INFINITY;
     for (int i = t; i < used; i += 256) m = fmaxf(m, hp[size_t(i) * 130]);
@@ -1391,22 +1446,37 @@ static void l_gemv_norm(const PreparedDispatch& pd, void* const* p, hipStream_t 
 
 // 21 attention_decode_f16: qkv, q_norm, k_norm, cos, sin, k_cache, v_cache, partials, state, q_heads, kv_heads,
 // max_pos, eps, scale
+// 64-key chunks per split block: the `chunks` field, 0 meaning 1 (the field is the last one; callers that predate it
+// leave its word 0)
+static int dec_chunks(uint32_t w) { return w == 0 ? 1 : int(w); }
+static uint32_t dec_splits(uint32_t max_pos, uint32_t chunks) {
+    const uint32_t keys = 64u * uint32_t(dec_chunks(chunks));
+    return (max_pos + keys - 1) / keys;
+}
+
 static void l_attn_dec(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     const int max_pos = int(w[12]);
-    hipLaunchKernelGGL(k_attn_dec, dim3(uint32_t(max_pos / 64), w[11], w[15]), dim3(256), 0, s, (const float*)p[0],
-                       (const uint16_t*)p[1], (const uint16_t*)p[2], (const float*)p[3], (const float*)p[4],
-                       (uint16_t*)p[5], (uint16_t*)p[6], (float*)p[7], (const uint32_t*)p[8], int(w[10]), int(w[11]),
-                       max_pos, f32_of(w[13]), f32_of(w[14]) * kLog2e);
+    const dim3 grid(dec_splits(w[12], w[16]), w[11], w[15]);
+#define L_DEC(M)                                                                                                     \
+    hipLaunchKernelGGL(k_attn_dec<M>, grid, dim3(256), 0, s, (const float*)p[0], (const uint16_t*)p[1],             \
+                       (const uint16_t*)p[2], (const float*)p[3], (const float*)p[4], (uint16_t*)p[5],              \
+                       (uint16_t*)p[6], (float*)p[7], (const uint32_t*)p[8], int(w[10]), int(w[11]), max_pos,       \
+                       f32_of(w[13]), f32_of(w[14]) * kLog2e, dec_chunks(w[16]))
+    if (dec_chunks(w[16]) == 1)
+        L_DEC(false);
+    else
+        L_DEC(true);
+#undef L_DEC
 }
 
-// 22 attention_combine, 35 attention_combine_f16: partials, y, state, q_heads, max_pos, batch
+// 22 attention_combine, 35 attention_combine_f16: partials, y, state, q_heads, max_pos, batch, chunks
 template <typename OUT>
 static void l_attn_combine_t(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     const int max_pos = int(w[5]);
     hipLaunchKernelGGL((k_attn_combine<OUT>), dim3(w[4], w[6]), dim3(256), 0, s, (const float*)p[0], (OUT*)p[1],
-                       (const uint32_t*)p[2], max_pos / 64, max_pos);
+                       (const uint32_t*)p[2], int(dec_splits(w[5], w[7])), 64 * dec_chunks(w[7]), max_pos);
 }
 static void l_attn_combine(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     l_attn_combine_t<float>(pd, p, s);
@@ -1548,9 +1618,14 @@ static void need_batch(const char* k, uint32_t b) {
     if (b < 1 || b > 1024) contract_fail("%s: batch must be in 1 .. 1024", k);
 }
 
+static void need_chunks(const char* k, uint32_t chunks) {
+    if (chunks > 64) contract_fail("%s: chunks must be in 0 .. 64 (0 = 1)", k);
+}
+
 static void check_combine(const char* k, const uint32_t* w, const uint32_t* c) {
     const int64_t qh = w[4], mp = w[5], B = w[6];
     need_batch(k, w[6]);
+    need_chunks(k, w[7]);
     if (mp < 64 || mp % 64 || mp > 64 * kMaxSplits) contract_fail("%s: max_pos must be a multiple of 64 in 64 .. %d", k, 64 * kMaxSplits);
     need(c, 0, B * qh * (mp / 64) * 130, k, "partials");
     need(c, 1, B * qh * 128, k, "y");
@@ -1669,16 +1744,17 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 21 attention_decode_f16
     c.push_back({"attention_decode_f16", "fast", {256, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{int64_t(w[12]) / 64, w[11], w[15]}; },
+                 [](const uint32_t* w) { return Grid3{dec_splits(w[12], w[16]), w[11], w[15]}; },
                  {TOK_R("qkv", DT(F32)), TOK_R("q_norm", DT(BF16)), TOK_R("k_norm", DT(BF16)),
                   TOK_R("cos_table", DT(F32)), TOK_R("sin_table", DT(F32)), TOK_RW("k_cache", DT(F16)),
                   TOK_RW("v_cache", DT(F16)), TOK_W("partials", DT(F32)), TOK_R("state", DT(U32)), U32F("q_heads"),
-                  U32F("kv_heads"), U32F("max_pos"), F32F("eps"), F32F("scale"), U32F("batch")},
+                  U32F("kv_heads"), U32F("max_pos"), F32F("eps"), F32F("scale"), U32F("batch"), U32F("chunks")},
                  [](const uint32_t* w, const uint32_t* c) {
                      const int64_t qh = w[10], kvh = w[11], mp = w[12], B = w[15];
                      need_group2("attention_decode_f16", w[10], w[11]);
                      need_max_pos("attention_decode_f16", w[12]);
                      need_batch("attention_decode_f16", w[15]);
+                     need_chunks("attention_decode_f16", w[16]);
                      need(c, 0, B * (qh + 2 * kvh) * 128, "attention_decode_f16", "qkv");
                      need(c, 1, 128, "attention_decode_f16", "q_norm");
                      need(c, 2, 128, "attention_decode_f16", "k_norm");
@@ -1692,7 +1768,7 @@ std::vector<KernelSpec> fast_catalog() {
     // 22 attention_combine: partials, y, state, q_heads, max_pos
     c.push_back({"attention_combine", "fast", {256, 1, 1}, false, [](const uint32_t* w) { return Grid3{w[4], w[6], 1}; },
                  {TOK_R("partials", DT(F32)), TOK_W("y", DT(F32)), TOK_R("state", DT(U32)), U32F("q_heads"),
-                  U32F("max_pos"), U32F("batch")},
+                  U32F("max_pos"), U32F("batch"), U32F("chunks")},
                  [](const uint32_t* w, const uint32_t* c) { check_combine("attention_combine", w, c); }});
     // 23 gemv_residual_dec: a, w, x, n, k
     c.push_back({"gemv_residual_dec", "fast", {256, 1, 1}, true,
@@ -1800,7 +1876,7 @@ std::vector<KernelSpec> fast_catalog() {
     c.push_back({"attention_combine_f16", "fast", {256, 1, 1}, false,
                  [](const uint32_t* w) { return Grid3{w[4], w[6], 1}; },
                  {TOK_R("partials", DT(F32)), TOK_W("y", DT(F16)), TOK_R("state", DT(U32)), U32F("q_heads"),
-                  U32F("max_pos"), U32F("batch")},
+                  U32F("max_pos"), U32F("batch"), U32F("chunks")},
                  [](const uint32_t* w, const uint32_t* c) { check_combine("attention_combine_f16", w, c); }});
     // 36 decode_advance: argmax, state, out_ids, batch, max_steps
     c.push_back({"decode_advance", "fast", {256, 1, 1}, true, [](const uint32_t*) { return Grid3{1, 1, 1}; },

@@ -653,6 +653,10 @@ void QwenExec::record_decode_batch(CommandList* l) {
                    V = c.vocab, HD = c.head_dim, MP = c.max_pos, B = uint32_t(c.batch);
     const uint32_t eps = fbits(c.eps);
     const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
+    // 64-key chunks per decode-attention block: as many as keep about 2048 blocks (8 per CU) at full context, so a
+    // block streams several chunks with its loads ahead instead of paying its set-up latency per 64 keys
+    uint32_t chunks = 1;
+    while (chunks < 16 && B * uint32_t(c.kv_heads) * (MP / 64) / (2 * chunks) >= 2048) chunks *= 2;
     auto tk = [&](const std::string& n) { return token(n); };
     dispatch(l, "embed_dec", {tk("model.embed_tokens.weight"), tk("dec.state"), tk("dec.x"), H, V, B});
     for (int i = 0; i < c.layers; ++i) {
@@ -663,9 +667,9 @@ void QwenExec::record_decode_batch(CommandList* l) {
         dispatch(l, "attention_decode_f16", {tk("dec.qkv"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
                                              tk(p + "k_cache"), tk(p + "v_cache"), tk("dec.attn_partials"),
                                              tk("dec.state"), uint32_t(c.heads), uint32_t(c.kv_heads), MP, eps, scale,
-                                             B});
+                                             B, chunks});
         dispatch(l, "attention_combine_f16", {tk("dec.attn_partials"), tk("dec.o16"), tk("dec.state"),
-                                              uint32_t(c.heads), MP, B});
+                                              uint32_t(c.heads), MP, B, chunks});
         dispatch(l, "gemm_skinny_residual", {tk("dec.o16"), tk(p + "o_proj.f16"), tk("dec.x"), B, H, QC});
         dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), w(7), tk("dec.h16"), B, H, eps, 0});
         dispatch(l, "gemm_skinny_swiglu", {tk("dec.h16"), tk(p + "gate_up_proj.f16"), tk("dec.a16"), B, I, H});

@@ -297,10 +297,12 @@ def test_embed_dec():
         s.close()
 
 
-@pytest.mark.parametrize("pos", [0, 63, 64, 383, 1000, 4095])
-def test_attention_decode_f16(pos):
+@pytest.mark.parametrize("pos,chunks", [(0, 1), (63, 1), (64, 1), (383, 1), (1000, 1), (4095, 1), (0, 4), (383, 4),
+                                        (1000, 8), (4095, 16), (4095, 3), (130, 2)])
+def test_attention_decode_f16(pos, chunks):
     """One decode step's attention: raw q|k|v projection in, q/k RMSNorm + RoPE at `pos`, the new key and value
-    appended to the caches, split-KV attention over positions 0..pos, then the split combine."""
+    appended to the caches, split-KV attention over positions 0..pos (`chunks` 64-key chunks per split block, so
+    blocks of one chunk, of several, and a last split cut short by max_pos), then the split combine."""
     max_pos = 4096
     S = max_pos // 64
     r = np.random.default_rng(pos)
@@ -321,9 +323,9 @@ def test_attention_decode_f16(pos):
         y = s.run_list([("attention_decode_f16", dict(qkv="qkv", q_norm="qn", k_norm="kn", cos_table="cos",
                                                       sin_table="sin", k_cache="kc", v_cache="vc", partials="part",
                                                       state="state", q_heads=16, kv_heads=8, max_pos=max_pos,
-                                                      eps=1e-6, scale=scale, batch=1)),
+                                                      eps=1e-6, scale=scale, batch=1, chunks=chunks)),
                         ("attention_combine", dict(partials="part", y="y", state="state", q_heads=16,
-                                                   max_pos=max_pos, batch=1))], ["y"])["y"]
+                                                   max_pos=max_pos, batch=1, chunks=chunks))], ["y"])["y"]
         q64 = qkv[None].astype(np.float64)
         qr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, :2048].copy(), qn, 1e-6), 16, pos)
         kr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, 2048:3072].copy(), kn, 1e-6), 8, pos)
@@ -339,7 +341,7 @@ def test_attention_decode_f16(pos):
         vf = np.concatenate([hwiden(vb[:pos]), hwiden(v_new)]).astype(np.float64)
         ref = cpuref.attention(qr, kf, vf, 16, 8, 128, pos, scale)
         err, rel = metrics.max_abs(y, ref), metrics.rel_l2(y, ref)
-        print(f"attention decode pos={pos}: max-abs {err:.3g}, relL2 {rel:.3g}", flush=True)
+        print(f"attention decode pos={pos} chunks={chunks}: max-abs {err:.3g}, relL2 {rel:.3g}", flush=True)
         assert err <= 1e-3 and rel <= 1e-4
     finally:
         s.close()
@@ -416,7 +418,8 @@ def test_gemm_skinny_swiglu():
         s.close()
 
 
-def test_attention_decode_batched_f16_combine():
+@pytest.mark.parametrize("chunks", [1, 4])
+def test_attention_decode_batched_f16_combine(chunks):
     """Three sequences at positions 5, 64 and 700 in one dispatch (batch on the grid), then the fp16 combine; each
     sequence against CpuRef F64 on its own cache."""
     max_pos, S = 1024, 16
@@ -444,9 +447,11 @@ def test_attention_decode_batched_f16_combine():
         y = hwiden(s.run_list([("attention_decode_f16", dict(qkv="qkv", q_norm="qn", k_norm="kn", cos_table="cos",
                                                              sin_table="sin", k_cache="kc", v_cache="vc",
                                                              partials="part", state="state", q_heads=16, kv_heads=8,
-                                                             max_pos=max_pos, eps=1e-6, scale=scale, batch=B)),
+                                                             max_pos=max_pos, eps=1e-6, scale=scale, batch=B,
+                                                             chunks=chunks)),
                                ("attention_combine_f16", dict(partials="part", y="y", state="state", q_heads=16,
-                                                              max_pos=max_pos, batch=B))], ["y"])["y"])
+                                                              max_pos=max_pos, batch=B, chunks=chunks))],
+                              ["y"])["y"])
         kc2 = s.read("kc").reshape(B, 8, max_pos, 128)
         vc2 = s.read("vc").reshape(B, 8, 128, max_pos)
         for b, pos in enumerate(positions):
