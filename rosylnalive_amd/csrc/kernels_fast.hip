@@ -94,8 +94,22 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     constexpr int STAGE = (GBM + BN) * GLD;
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1, g = lane >> 4, c16 = lane & 15;
-    const int m0 = blockIdx.y * GBM;
-    const int n0 = blockIdx.x * BN;
+    // XCD-aware tile order. Blocks are dispatched round-robin over the 8 XCDs (block L, x fastest, on XCD L % 8), each
+    // with its own L2. Block L takes tile T = (L % 8) (tiles / 8) + L / 8, so an XCD's blocks are consecutive tiles,
+    // and tiles are numbered in groups of GM row tiles, rows fastest within a group: an XCD then covers about a
+    // GM x (tiles / 8 / GM) rectangle and reads GM row tiles of A and tiles / 8 / GM column tiles of W into its L2,
+    // instead of (with x fastest) every row tile of A. GM balances the two (A rows are 128 wide, W columns BN).
+    constexpr int GM = BN == 64 ? 4 : 8;
+    int tx = blockIdx.x, ty = blockIdx.y;
+    {
+        const int gx = gridDim.x, ntiles = gx * int(gridDim.y), L = int(blockIdx.y) * gx + int(blockIdx.x);
+        const int T = ntiles % 8 == 0 ? (L % 8) * (ntiles / 8) + L / 8 : L;
+        const int sr = T / (GM * gx), within = T - sr * GM * gx, rows = min(GM, int(gridDim.y) - sr * GM);
+        ty = sr * GM + within % rows;
+        tx = within / rows;
+    }
+    const int m0 = ty * GBM;
+    const int n0 = tx * BN;
 
     // the rows this thread loads: chunk c = t + 256 i -> row c / 8, 16-byte column (c % 8), as element offsets from
     // the matrix base (every matrix is under 2^31 elements). A row past the matrix is clamped to its last row: it only
@@ -112,7 +126,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
         int n;
         if (EPI == EPI_SWIGLU) {
-            const int j = min(int(blockIdx.x) * 64 + (r & 63), p.inter - 1);
+            const int j = min(tx * 64 + (r & 63), p.inter - 1);
             n = r < 64 ? j : p.inter + j;
         } else {
             n = min(n0 + r, p.N - 1);
@@ -264,8 +278,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                 for (int r = 0; r < 4; ++r) x32[((wm * 16 + i * 4 + j) * 4 + r) * 64 + lane] = acc[i][j][r];
     }
     __syncthreads();
-    // QKV: head = blockIdx.x (q heads, then k heads, then v heads), head_dim 128 = this tile's columns.
-    const int head = blockIdx.x;
+    // QKV: head = the column tile (q heads, then k heads, then v heads), head_dim 128 = this tile's columns.
+    const int head = tx;
     const bool is_q = head < p.qh, is_k = !is_q && head < p.qh + p.kvh;
     if (wn == 1 && (EPI == EPI_SWIGLU || is_q || is_k)) return;  // V tiles: all four waves store the transpose
     // the partner half of row tile i, read back from LDS
@@ -284,7 +298,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             load_hi(i, hi);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int col = blockIdx.x * 64 + j * 16 + c16;
+                const int col = tx * 64 + j * 16 + c16;
                 if (col >= p.inter) continue;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {

@@ -36,8 +36,11 @@ def hwiden(h):
 
 # ---------------------------------------------------------------- prefill kernels
 
-@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (512, 1024, 1024), (37, 300, 192), (2048, 2048, 1024)])
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (512, 1024, 1024), (37, 300, 192), (2048, 2048, 1024),
+                                   (300, 200, 128), (2048, 1024, 3072)])
 def test_gemm_f32_and_residual(m, n, k):
+    """f32 and residual epilogues over whole and partial tiles; the residual GEMMs with few tiles and an even number
+    of 64-wide k steps (1024, 128, 3072) run with K split between two wave groups of the block."""
     r = np.random.default_rng(m + n + k)
     a = f16(r.standard_normal((m, k)))
     w = f16(r.standard_normal((n, k)) * 0.05)
