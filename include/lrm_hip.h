@@ -115,6 +115,12 @@ int lrm_hip_denormal_probe(lrm_hip_device *d, int *mode, uint32_t results[7]);
 typedef struct lrm_hip_list lrm_hip_list;
 int lrm_hip_begin(lrm_hip_device *d, int reusable, lrm_hip_list **out);
 int lrm_hip_dispatch(lrm_hip_list *l, uint32_t kernel, const uint32_t words[32]);
+/* ICommandList.Dispatch for work that may overlap what follows (an extension; the reference's ordering rule,
+ * docs/contracts/gpu-backend.md:58-64, lets dispatches not separated by Barrier overlap, while lrm_hip_dispatch runs
+ * each dispatch after the previous one): it runs on a second stream after everything recorded before it, and the next
+ * lrm_hip_barrier, or the end of the list, waits for it. For read-only side work such as cache prefetch. */
+int lrm_hip_dispatch_overlapped(lrm_hip_list *l, uint32_t kernel, const uint32_t words[32]);
+/* ICommandList.Barrier: joins the overlapped dispatches (the in-order dispatches need nothing). */
 int lrm_hip_barrier(lrm_hip_list *l);
 int lrm_hip_copy(lrm_hip_list *l, int src_slot, uint64_t src_offset, int dst_slot, uint64_t dst_offset, uint64_t bytes);
 int lrm_hip_begin_timer(lrm_hip_list *l, const char *name, int *timer);

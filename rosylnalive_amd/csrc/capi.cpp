@@ -329,6 +329,14 @@ int lrm_hip_dispatch(lrm_hip_list* l, uint32_t kernel, const uint32_t words[32])
     });
 }
 
+int lrm_hip_dispatch_overlapped(lrm_hip_list* l, uint32_t kernel, const uint32_t words[32]) {
+    return guard([&] {
+        need_ptr(l, "list");
+        need_ptr(words, "words");
+        l->l->dispatch_overlapped(int(kernel), words);
+    });
+}
+
 int lrm_hip_barrier(lrm_hip_list* l) {
     return guard([&] {
         need_ptr(l, "list");

@@ -75,6 +75,9 @@ Device::Device(int index, uint32_t flags) : index_(index), flags_(flags) {
     info_ = all[size_t(index)];
     HIPC(hipSetDevice(index));
     HIPC(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    HIPC(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking));
+    HIPC(hipEventCreateWithFlags(&fork_ev_, hipEventDisableTiming));
+    HIPC(hipEventCreateWithFlags(&join_ev_, hipEventDisableTiming));
     HIPC(hipEventCreate(&epoch_));
     HIPC(hipEventRecord(epoch_, stream_));
 }
@@ -97,6 +100,9 @@ Device::~Device() {
         (void)hipEventDestroy(e.second);
     }
     if (epoch_) (void)hipEventDestroy(epoch_);
+    if (fork_ev_) (void)hipEventDestroy(fork_ev_);
+    if (join_ev_) (void)hipEventDestroy(join_ev_);
+    if (side_) (void)hipStreamDestroy(side_);
     if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -273,9 +279,23 @@ void CommandList::dispatch(int kernel, const uint32_t* words) {
     ++dispatches_;
 }
 
+void CommandList::dispatch_overlapped(int kernel, const uint32_t* words) {
+    dispatch(kernel, words);
+    cmds_.back().kind = Cmd::LaunchSide;
+    side_open_ = true;
+}
+
 void CommandList::barrier() {
     check_open();
-    // One in-order stream: every earlier command has finished its writes before a later one starts.
+    // The main stream is in order: every earlier command on it has finished its writes before a later one starts.
+    // Overlapped dispatches are joined here.
+    if (side_open_) {
+        if (exec_) contract_fail("a reusable list cannot be changed after its first submission");
+        Cmd c{};
+        c.kind = Cmd::Join;
+        cmds_.push_back(std::move(c));
+        side_open_ = false;
+    }
 }
 
 void CommandList::copy(int ss, uint64_t so, int ds, uint64_t dof, uint64_t bytes) {
@@ -336,14 +356,33 @@ bool Device::graphs_enabled() {
     return on;
 }
 
+void Device::launch_side(const CommandList::Cmd& c) {
+    HIPC(hipEventRecord(fork_ev_, stream_));
+    HIPC(hipStreamWaitEvent(side_, fork_ev_, 0));
+    launcher_of(c.pd.kernel)(c.pd, c.ptr.data(), side_);
+}
+
+void Device::join_side() {
+    HIPC(hipEventRecord(join_ev_, side_));
+    HIPC(hipStreamWaitEvent(stream_, join_ev_, 0));
+}
+
 void Device::run(CommandList* l) {
+    bool side = false;
     for (auto& c : l->cmds_) {
         if (c.kind == CommandList::Cmd::Launch) {
             launcher_of(c.pd.kernel)(c.pd, c.ptr.data(), stream_);
+        } else if (c.kind == CommandList::Cmd::LaunchSide) {
+            launch_side(c);
+            side = true;
+        } else if (c.kind == CommandList::Cmd::Join) {
+            join_side();
+            side = false;
         } else if (c.kind == CommandList::Cmd::Copy) {
             HIPC(hipMemcpyAsync(c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice, stream_));
         }
     }
+    if (side) join_side();  // the list ends with every overlapped dispatch joined (and, under capture, in the graph)
 }
 
 uint64_t Device::submit(CommandList* l, uint32_t repeat) {
@@ -362,6 +401,7 @@ uint64_t Device::submit(CommandList* l, uint32_t repeat) {
         // One-shot: launch every command now, with timer events and per-dispatch timing as asked.
         std::vector<std::pair<hipEvent_t, hipEvent_t>> tev(l->timer_names_.size());
         bool time_dispatches = (flags_ & TimeDispatches) != 0;
+        bool side = false;
         for (auto& c : l->cmds_) {
             switch (c.kind) {
                 case CommandList::Cmd::Launch: {
@@ -380,6 +420,14 @@ uint64_t Device::submit(CommandList* l, uint32_t repeat) {
                     }
                     break;
                 }
+                case CommandList::Cmd::LaunchSide:
+                    launch_side(c);
+                    side = true;
+                    break;
+                case CommandList::Cmd::Join:
+                    join_side();
+                    side = false;
+                    break;
                 case CommandList::Cmd::Copy:
                     HIPC(hipMemcpyAsync(c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice, stream_));
                     break;
@@ -393,6 +441,7 @@ uint64_t Device::submit(CommandList* l, uint32_t repeat) {
                     break;
             }
         }
+        if (side) join_side();
         // Timers first, in the order opened, then the dispatch timings (Completion.Timers).
         std::vector<std::pair<hipEvent_t, hipEvent_t>> all(tev.begin(), tev.end());
         std::vector<std::string> names(l->timer_names_.begin(), l->timer_names_.end());

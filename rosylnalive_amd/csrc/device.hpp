@@ -66,6 +66,10 @@ class Device;
 class CommandList {
   public:
     void dispatch(int kernel, const uint32_t* words);
+    // A dispatch that may run concurrently with the dispatches after it, up to the next barrier (the reference's
+    // ordering rule: dispatches not separated by Barrier may overlap). It runs on the device's side stream, after
+    // everything recorded before it; Barrier, and the end of the list, wait for it.
+    void dispatch_overlapped(int kernel, const uint32_t* words);
     void barrier();
     void copy(int src_slot, uint64_t src_off, int dst_slot, uint64_t dst_off, uint64_t bytes);
     int begin_timer(const std::string& name);
@@ -77,7 +81,7 @@ class CommandList {
   private:
     friend class Device;
     struct Cmd {
-        enum Kind { Launch, Copy, TimerBegin, TimerEnd } kind;
+        enum Kind { Launch, LaunchSide, Join, Copy, TimerBegin, TimerEnd } kind;
         PreparedDispatch pd;
         std::vector<void*> ptr;
         void* src = nullptr;
@@ -94,6 +98,7 @@ class CommandList {
     std::vector<std::string> timer_names_;
     std::vector<int> open_timers_;
     int dispatches_ = 0;
+    bool side_open_ = false;  // an overlapped dispatch not yet joined
     hipGraph_t graph_ = nullptr;
     hipGraphExec_t exec_ = nullptr;
 };
@@ -139,12 +144,16 @@ class Device {
   private:
     friend class CommandList;
     void run(CommandList* l);
+    void launch_side(const CommandList::Cmd& c);  // fork from the main stream, launch on the side stream
+    void join_side();                             // the main stream waits for the side stream
     static bool graphs_enabled();
     void run_probe();
     DeviceInfo info_{};
     int index_;
     uint32_t flags_;
     hipStream_t stream_ = nullptr;
+    hipStream_t side_ = nullptr;  // overlapped dispatches (default priority, like stream_)
+    hipEvent_t fork_ev_ = nullptr, join_ev_ = nullptr;
     hipEvent_t epoch_ = nullptr;
     bool heap_created_ = false;
     HeapLayout layout_;

@@ -397,13 +397,16 @@ void QwenExec::read_weight(const std::string& name, uint16_t* out, uint64_t elem
     download_tensor(name, out, elems * 2);
 }
 
-uint32_t QwenExec::dispatch(CommandList* l, const char* kernel, std::vector<uint32_t> fields) {
+uint32_t QwenExec::dispatch(CommandList* l, const char* kernel, std::vector<uint32_t> fields, bool overlapped) {
     int id = catalog_find(kernel);
     if (id < 0) arg_fail("no kernel %s", kernel);
     uint32_t words[32] = {0};
     if (fields.size() > 31) arg_fail("too many fields");
     for (size_t i = 0; i < fields.size(); ++i) words[i + 1] = fields[i];
-    l->dispatch(id, words);
+    if (overlapped)
+        l->dispatch_overlapped(id, words);
+    else
+        l->dispatch(id, words);
     return uint32_t(id);
 }
 

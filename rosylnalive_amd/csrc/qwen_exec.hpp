@@ -84,7 +84,7 @@ class QwenExec {
     void record_decode_batch(CommandList* l);
     void sync_f16();  // refreshes the fp16 copies of the matrices written since the last forward
     void tap_copy(CommandList* l, const std::string& name, uint32_t src, int t, int width);
-    uint32_t dispatch(CommandList* l, const char* kernel, std::vector<uint32_t> fields);
+    uint32_t dispatch(CommandList* l, const char* kernel, std::vector<uint32_t> fields, bool overlapped = false);
 
     Device& dev_;
     QwenConfig cfg_;

@@ -474,6 +474,11 @@ class HipCommandList:
         kid = Catalog.find(kernel).id if isinstance(kernel, str) else int(kernel)
         check(lib().lrm_hip_dispatch(self._h, kid, args.as_c()))
 
+    def dispatch_overlapped(self, kernel, args: ArgBlock) -> None:
+        """A dispatch that may run concurrently with the following ones up to the next barrier (side stream)."""
+        kid = Catalog.find(kernel).id if isinstance(kernel, str) else int(kernel)
+        check(lib().lrm_hip_dispatch_overlapped(self._h, kid, args.as_c()))
+
     def barrier(self) -> None:
         check(lib().lrm_hip_barrier(self._h))
 

@@ -173,6 +173,32 @@ def test_convert_bf16_f16_bit_exact():
         s.close()
 
 
+@pytest.mark.parametrize("reusable", [False, True])
+def test_prefetch_overlapped(reusable):
+    """An overlapped prefetch (side stream, joined by the barrier and by the end of the list) beside ordinary
+    dispatches: the ordinary results are exact, in a one-shot list and in a reusable (graph) list replayed 3 times."""
+    n = 1 << 20
+    r = np.random.default_rng(5)
+    x = bf16(r.standard_normal(n))
+    big = bf16(r.standard_normal(3 * n))
+    s = Session({"x": (BF16, (n,), RO, x), "big": (BF16, (3 * n,), RO, big), "y": (F16, (n,), 0, None),
+                 "z": (F16, (n,), 0, None)})
+    try:
+        cl = s.backend.begin(reusable)
+        cl.dispatch_overlapped("prefetch", s.fields("prefetch", x0="big", x1="x", x2="big", x3="x"))
+        cl.dispatch("convert_bf16_f16", s.fields("convert_bf16_f16", x="x", y="y", n=n))
+        cl.barrier()
+        cl.dispatch_overlapped("prefetch", s.fields("prefetch", x0="x", x1="x", x2="x", x3="big"))
+        cl.dispatch("convert_bf16_f16", s.fields("convert_bf16_f16", x="x", y="z", n=n))
+        c = s.backend.wait(s.backend.submit(cl, repeat=3 if reusable else 1))
+        assert c.dispatches == 4 * (3 if reusable else 1)
+        cl.release()
+        ref = widen(x).astype(np.float16).view(np.uint16)
+        assert np.array_equal(s.read("y"), ref) and np.array_equal(s.read("z"), ref)
+    finally:
+        s.close()
+
+
 def test_rmsnorm_rows_f16():
     rows, cols, row0 = 37, 1024, 5
     r = np.random.default_rng(2)
