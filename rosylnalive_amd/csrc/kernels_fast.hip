@@ -54,15 +54,24 @@ __global__ __launch_bounds__(256) void k_rmsnorm_f16(const float* x, const uint1
 }
 
 // ================================================================ GEMM (ids 15, 17, 18, 19)
-// C[m, n] = sum_k A[m, k] W[n, k] on f16 operands, 128 x 128 tiles, k in steps of 64, 4 waves each owning a 64 x 64
-// quarter as 4 x 4 MFMA tiles. Two LDS buffers: while the matrix cores work on k-tile kt, tile kt + 1 is already in
-// LDS and tile kt + 2 is in flight from HBM into registers.
-constexpr int GBM = 128, GBN = 128, GBK = 64, GLD = GBK + 8;  // LDS row stride (halves), padded against bank conflicts
+// C[m, n] = sum_k A[m, k] W[n, k] on f16 operands, 128 x 128 tiles (128 x 64 for the residual GEMMs of few tiles), k
+// in steps of 64, 4 waves each owning a 64 x 64 quarter as 4 x 4 MFMA tiles. Tiles are loaded from memory straight
+// into two LDS stages (the lds form of the buffer load), the next k tile landing while the current one multiplies.
+constexpr int GBM = 128, GBN = 128, GBK = 64;
 
 // A raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3: 32-bit data format, no swizzle): loads
 // through it take a per-lane byte offset and a scalar one, so a loop's changing k offset costs no vector registers.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// 16 bytes per lane from a buffer resource straight into LDS: lane l writes lds_block + 16 l (lds_block is uniform).
+// The builtin exists only for the device target, so the host pass (which only needs the kernels' launch stubs) sees
+// an empty body.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, uint16_t* lds_block, int voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_block, 16, voff, soff, 0, 0);
+#endif
 }
 
 enum Epi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
@@ -87,12 +96,18 @@ struct GemmArgs {
     float eps;
 };
 
-template <int EPI, int BN>
+// Two main loops, chosen by the launcher: DMA (a grid of at least two blocks per CU) moves tiles from memory
+// straight into two LDS stages, the two blocks on a CU hiding each other's load latency; otherwise (one block per CU)
+// tiles go through two register sets into two padded LDS buffers with every load two k steps ahead.
+template <int EPI, int BN, bool DMA>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID)), "SwiGLU and QKV pair 128 columns");
-    constexpr int WN = BN / 2, JT = WN / 16, BCH = BN / 32;  // columns per wave, MFMA tiles per wave, B chunks/thread
-    constexpr int STAGE = (GBM + BN) * GLD;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+    constexpr int WN = BN / 2, JT = WN / 16;    // columns per wave, MFMA tiles per wave
+    constexpr int GLD = GBK + 8;                // register path: LDS row stride (halves), padded against bank conflicts
+    constexpr int STAGE = DMA ? (GBM + BN) * GBK : (GBM + BN) * GLD;  // halves: the A tile then the W tile
+    // the two stages, or what the QKV epilogue needs after them (x32 32 KiB + the V^T tile 128 x 136 halves)
+    constexpr int LDS_HALVES = EPI == EPI_QKV ? (2 * STAGE > 33792 ? 2 * STAGE : 33792) : 2 * STAGE;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALVES];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1, g = lane >> 4, c16 = lane & 15;
     // XCD-aware tile order. Blocks are dispatched round-robin over the 8 XCDs (block L, x fastest, on XCD L % 8), each
     // with its own L2. Block L takes tile T = (L % 8) (tiles / 8) + L / 8, so an XCD's blocks are consecutive tiles,
@@ -111,141 +126,216 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     const int m0 = ty * GBM;
     const int n0 = tx * BN;
 
-    // the rows this thread loads: chunk c = t + 256 i -> row c / 8, 16-byte column (c % 8), as element offsets from
-    // the matrix base (every matrix is under 2^31 elements). A row past the matrix is clamped to its last row: it only
-    // feeds output rows / columns that are never stored, and the loads stay unconditional, so the compiler can keep
-    // several tiles in flight (a guarded load makes it wait for every outstanding load).
-    int aoff[4], boff[BCH];  // byte offsets: the loads are buffer loads with the k offset in a scalar register
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
-        aoff[i] = (min(m0 + r, p.M - 1) * p.K + kc) * 2;
-    }
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-        const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
-        int n;
-        if (EPI == EPI_SWIGLU) {
-            const int j = min(tx * 64 + (r & 63), p.inter - 1);
-            n = r < 64 ? j : p.inter + j;
-        } else {
-            n = min(n0 + r, p.N - 1);
-        }
-        boff[i] = (n * p.K + kc) * 2;
-    }
-    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.M * p.K * 2);
-    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(p.w, (EPI == EPI_SWIGLU ? 2 * p.inter : p.N) * p.K * 2);
-    // Two register sets, two LDS buffers: tile j is loaded into set j % 2 at the top of iteration j - 2 and stored to
-    // LDS buffer j % 2 at the end of iteration j - 1, so each load has two iterations of MFMAs to land. The loop is
-    // unrolled by two so every register set is named at compile time.
-    u32x4 ra[2][4], rb[2][BCH];
-    auto gload = [&](auto set, int k0) __attribute__((always_inline)) {
-        constexpr int S = decltype(set)::value;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ra[S][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, aoff[i], k0 * 2, 0);
-#pragma unroll
-        for (int i = 0; i < BCH; ++i) rb[S][i] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, boff[i], k0 * 2, 0);
-    };
-    auto sstore = [&](auto set, int buf) __attribute__((always_inline)) {
-        constexpr int S = decltype(set)::value;
-        uint16_t* As = lds + buf * STAGE;
-        uint16_t* Bs = As + GBM * GLD;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = t + 256 * i;
-            *reinterpret_cast<u32x4*>(As + (c >> 3) * GLD + (c & 7) * 8) = ra[S][i];
-        }
-#pragma unroll
-        for (int i = 0; i < BCH; ++i) {
-            const int c = t + 256 * i;
-            *reinterpret_cast<u32x4*>(Bs + (c >> 3) * GLD + (c & 7) * 8) = rb[S][i];
-        }
-    };
-
     f32x4 acc[4][JT];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < JT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // MFMA operands of one 32-wide k half (ks) of an LDS buffer: two named register sets, F0 for ks 0 and F1 for
-    // ks 1, so the reads of one half run under the MFMAs of the other
-    f16x8 fa[2][4], fb[2][JT];
-    auto read_frags = [&](auto ksc, int buf) __attribute__((always_inline)) {
-        constexpr int KS = decltype(ksc)::value;
-        const uint16_t* As = lds + buf * STAGE;
-        const uint16_t* Bs = As + GBM * GLD;
-        const int kof = KS * 32 + 8 * g;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            fa[KS][i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + (wm * 64 + i * 16 + c16) * GLD + kof));
-#pragma unroll
-        for (int j = 0; j < JT; ++j)
-            fb[KS][j] = as_f16x8(*reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 16 + c16) * GLD + kof));
-    };
-    auto mfma_half = [&](auto ksc) __attribute__((always_inline)) {
-        constexpr int KS = decltype(ksc)::value;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < JT; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[KS][i], fb[KS][j], acc[i][j], 0, 0, 0);
-    };
-    // the MFMAs of one half interleaved with the LDS reads of the other: MPR MFMAs, then one read
-    constexpr int NRD = 4 + JT, NMF = 4 * JT, MPR = NMF / NRD;
-    auto interleave = [&]() __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < NRD; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, MPR, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if constexpr (DMA) {
+        // Tiles go from memory straight into LDS (buffer loads with the lds flag: no registers, no LDS store
+        // instructions). One load instruction moves 64 lanes x 16 B = 1 KiB = 8 rows of 128 B; lane l writes LDS bytes
+        // 16 l of it, i.e. row l / 8, chunk position l % 8. Rows are unpadded and the 16-byte chunks XOR-swizzled: LDS row
+        // r, position q holds k chunk q ^ (r % 8), so a fragment read (16 rows, one chunk) spreads over the banks. Each wave
+        // issues instructions i = 0, 1, ... for the 1 KiB blocks 4 i + w. A row past the matrix is clamped to its last row
+        // (it only feeds outputs that are never stored); the k offset is a scalar.
+        constexpr int NA = GBM / 32, NB = BN / 32;  // load instructions per wave per stage
+        int aoff[NA], boff[NB];
+    #pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int r = 8 * (4 * i + w) + (lane >> 3), c = (lane & 7) ^ (r & 7);
+            aoff[i] = (min(m0 + r, p.M - 1) * p.K + c * 8) * 2;
         }
-        if constexpr (NMF > MPR * NRD) __builtin_amdgcn_sched_group_barrier(0x008, NMF - MPR * NRD, 0);
-    };
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using K0 = std::integral_constant<int, 0>;
-    using K1 = std::integral_constant<int, 1>;
-    const int nk = p.K / GBK;
-    // Tile t is loaded into register set t % 2 and stored to LDS buffer t % 2. Step t (parity P), with tile t in
-    // buffer P and its ks-0 operands in F0, tiles t + 1 and t + 2 loaded (or landing) in sets 1 - P and P:
-    //   store set 1 - P (tile t + 1) into buffer 1 - P (read up to the previous step, whose barrier every wave has
-    //   passed) and load tile t + 3 into it, so every load has two steps to land; ks-0 MFMAs with the ks-1 reads of
-    //   buffer P; barrier (this wave's stores and reads complete, so buffer 1 - P is whole); ks-1 MFMAs with the ks-0
-    //   reads of buffer 1 - P. Loads past the last tile re-read it (clamped); the last steps' stores and reads of
-    //   such tiles are never used.
-    auto step = [&](auto par, int kt) __attribute__((always_inline)) {
-        constexpr int P = decltype(par)::value;
-        sstore(std::integral_constant<int, 1 - P>{}, 1 - P);
-        gload(std::integral_constant<int, 1 - P>{}, min(kt + 3, nk - 1) * GBK);
+    #pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int r = 8 * (4 * i + w) + (lane >> 3), c = (lane & 7) ^ (r & 7);
+            int n;
+            if (EPI == EPI_SWIGLU) {
+                const int j = min(tx * 64 + (r & 63), p.inter - 1);
+                n = r < 64 ? j : p.inter + j;
+            } else {
+                n = min(n0 + r, p.N - 1);
+            }
+            boff[i] = (n * p.K + c * 8) * 2;
+        }
+        const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.M * p.K * 2);
+        const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(p.w, (EPI == EPI_SWIGLU ? 2 * p.inter : p.N) * p.K * 2);
+        auto issue = [&](int buf, int k0) __attribute__((always_inline)) {
+            uint16_t* st = lds + buf * STAGE;
+    #pragma unroll
+            for (int i = 0; i < NA; ++i) buffer_load_lds16(a_rsrc, st + (4 * i + w) * 512, aoff[i], k0 * 2);
+    #pragma unroll
+            for (int i = 0; i < NB; ++i) buffer_load_lds16(w_rsrc, st + GBM * GBK + (4 * i + w) * 512, boff[i], k0 * 2);
+        };
+
+        // one k step of a stage: per 32-wide half, the A fragments (rows of this wave's 4 MFMA row tiles) and the W
+        // fragments, read from their swizzled chunk, then the MFMAs
+        auto compute = [&](int buf) __attribute__((always_inline)) {
+            const uint16_t* As = lds + buf * STAGE;
+            const uint16_t* Bs = As + GBM * GBK;
+    #pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                f16x8 af[4], bf[JT];
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = wm * 64 + i * 16 + c16;
+                    af[i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + r * GBK + (((ks * 4 + g) ^ (r & 7)) * 8)));
+                }
+    #pragma unroll
+                for (int j = 0; j < JT; ++j) {
+                    const int r = wn * WN + j * 16 + c16;
+                    bf[j] = as_f16x8(*reinterpret_cast<const u32x4*>(Bs + r * GBK + (((ks * 4 + g) ^ (r & 7)) * 8)));
+                }
+    #pragma unroll
+                for (int i = 0; i < 4; ++i)
+    #pragma unroll
+                    for (int j = 0; j < JT; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+        };
+        // Two stages: step kt waits for its tile (this wave's loads, then the barrier for everyone's, which also means
+        // every wave is done reading the other stage), queues tile kt + 1 into the other stage and multiplies tile kt.
+        // The LDS-only barrier: __syncthreads() would also make every wave wait for the loads just queued.
+        const int nk = p.K / GBK;
+        issue(0, 0);
+        for (int kt = 0; kt < nk; ++kt) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile kt have landed in LDS
+            lds_barrier();
+            if (kt + 1 < nk) issue((kt + 1) & 1, (kt + 1) * GBK);  // uniform
+            compute(kt & 1);
+        }
+    } else {
+        // the rows this thread loads: chunk c = t + 256 i -> row c / 8, 16-byte column (c % 8), as element offsets from
+        // the matrix base (every matrix is under 2^31 elements). A row past the matrix is clamped to its last row: it only
+        // feeds output rows / columns that are never stored, and the loads stay unconditional, so the compiler can keep
+        // several tiles in flight (a guarded load makes it wait for every outstanding load).
+        constexpr int BCH = BN / 32;  // B chunks per thread
+        int aoff[4], boff[BCH];  // byte offsets: the loads are buffer loads with the k offset in a scalar register
+    #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
+            aoff[i] = (min(m0 + r, p.M - 1) * p.K + kc) * 2;
+        }
+    #pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
+            int n;
+            if (EPI == EPI_SWIGLU) {
+                const int j = min(tx * 64 + (r & 63), p.inter - 1);
+                n = r < 64 ? j : p.inter + j;
+            } else {
+                n = min(n0 + r, p.N - 1);
+            }
+            boff[i] = (n * p.K + kc) * 2;
+        }
+        const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.M * p.K * 2);
+        const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(p.w, (EPI == EPI_SWIGLU ? 2 * p.inter : p.N) * p.K * 2);
+        // Two register sets, two LDS buffers: tile j is loaded into set j % 2 at the top of iteration j - 2 and stored to
+        // LDS buffer j % 2 at the end of iteration j - 1, so each load has two iterations of MFMAs to land. The loop is
+        // unrolled by two so every register set is named at compile time.
+        u32x4 ra[2][4], rb[2][BCH];
+        auto gload = [&](auto set, int k0) __attribute__((always_inline)) {
+            constexpr int S = decltype(set)::value;
+    #pragma unroll
+            for (int i = 0; i < 4; ++i) ra[S][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, aoff[i], k0 * 2, 0);
+    #pragma unroll
+            for (int i = 0; i < BCH; ++i) rb[S][i] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, boff[i], k0 * 2, 0);
+        };
+        auto sstore = [&](auto set, int buf) __attribute__((always_inline)) {
+            constexpr int S = decltype(set)::value;
+            uint16_t* As = lds + buf * STAGE;
+            uint16_t* Bs = As + GBM * GLD;
+    #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = t + 256 * i;
+                *reinterpret_cast<u32x4*>(As + (c >> 3) * GLD + (c & 7) * 8) = ra[S][i];
+            }
+    #pragma unroll
+            for (int i = 0; i < BCH; ++i) {
+                const int c = t + 256 * i;
+                *reinterpret_cast<u32x4*>(Bs + (c >> 3) * GLD + (c & 7) * 8) = rb[S][i];
+            }
+        };
+
+
+        // MFMA operands of one 32-wide k half (ks) of an LDS buffer: two named register sets, F0 for ks 0 and F1 for
+        // ks 1, so the reads of one half run under the MFMAs of the other
+        f16x8 fa[2][4], fb[2][JT];
+        auto read_frags = [&](auto ksc, int buf) __attribute__((always_inline)) {
+            constexpr int KS = decltype(ksc)::value;
+            const uint16_t* As = lds + buf * STAGE;
+            const uint16_t* Bs = As + GBM * GLD;
+            const int kof = KS * 32 + 8 * g;
+    #pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fa[KS][i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + (wm * 64 + i * 16 + c16) * GLD + kof));
+    #pragma unroll
+            for (int j = 0; j < JT; ++j)
+                fb[KS][j] = as_f16x8(*reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 16 + c16) * GLD + kof));
+        };
+        auto mfma_half = [&](auto ksc) __attribute__((always_inline)) {
+            constexpr int KS = decltype(ksc)::value;
+    #pragma unroll
+            for (int i = 0; i < 4; ++i)
+    #pragma unroll
+                for (int j = 0; j < JT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[KS][i], fb[KS][j], acc[i][j], 0, 0, 0);
+        };
+        // the MFMAs of one half interleaved with the LDS reads of the other: MPR MFMAs, then one read
+        constexpr int NRD = 4 + JT, NMF = 4 * JT, MPR = NMF / NRD;
+        auto interleave = [&]() __attribute__((always_inline)) {
+    #pragma unroll
+            for (int i = 0; i < NRD; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, MPR, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            if constexpr (NMF > MPR * NRD) __builtin_amdgcn_sched_group_barrier(0x008, NMF - MPR * NRD, 0);
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using K0 = std::integral_constant<int, 0>;
+        using K1 = std::integral_constant<int, 1>;
+        const int nk = p.K / GBK;
+        // Tile t is loaded into register set t % 2 and stored to LDS buffer t % 2. Step t (parity P), with tile t in
+        // buffer P and its ks-0 operands in F0, tiles t + 1 and t + 2 loaded (or landing) in sets 1 - P and P:
+        //   store set 1 - P (tile t + 1) into buffer 1 - P (read up to the previous step, whose barrier every wave has
+        //   passed) and load tile t + 3 into it, so every load has two steps to land; ks-0 MFMAs with the ks-1 reads of
+        //   buffer P; barrier (this wave's stores and reads complete, so buffer 1 - P is whole); ks-1 MFMAs with the ks-0
+        //   reads of buffer 1 - P. Loads past the last tile re-read it (clamped); the last steps' stores and reads of
+        //   such tiles are never used.
+        auto step = [&](auto par, int kt) __attribute__((always_inline)) {
+            constexpr int P = decltype(par)::value;
+            sstore(std::integral_constant<int, 1 - P>{}, 1 - P);
+            gload(std::integral_constant<int, 1 - P>{}, min(kt + 3, nk - 1) * GBK);
+            __builtin_amdgcn_sched_barrier(0);
+            read_frags(K1{}, P);
+            mfma_half(K0{});
+            interleave();
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier();
+            read_frags(K0{}, 1 - P);
+            mfma_half(K1{});
+            interleave();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // loads issue in tile order, so each wait leaves the younger tiles in flight
+        gload(S0{}, 0);
         __builtin_amdgcn_sched_barrier(0);
-        read_frags(K1{}, P);
-        mfma_half(K0{});
-        interleave();
+        gload(S1{}, min(1, nk - 1) * GBK);
         __builtin_amdgcn_sched_barrier(0);
+        sstore(S0{}, 0);
+        gload(S0{}, min(2, nk - 1) * GBK);
         lds_barrier();
-        read_frags(K0{}, 1 - P);
-        mfma_half(K1{});
-        interleave();
+        read_frags(K0{}, 0);
         __builtin_amdgcn_sched_barrier(0);
-    };
-    // loads issue in tile order, so each wait leaves the younger tiles in flight
-    gload(S0{}, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    gload(S1{}, min(1, nk - 1) * GBK);
-    __builtin_amdgcn_sched_barrier(0);
-    sstore(S0{}, 0);
-    gload(S0{}, min(2, nk - 1) * GBK);
-    lds_barrier();
-    read_frags(K0{}, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // whole pairs in the loop (a conditional second step would leave the loop head with set 1 possibly the younger,
-    // and the waits there would drain every load); an odd last step after it
-    int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-        step(S0{}, kt);
-        step(S1{}, kt + 1);
+        // whole pairs in the loop (a conditional second step would leave the loop head with set 1 possibly the younger,
+        // and the waits there would drain every load); an odd last step after it
+        int kt = 0;
+        for (; kt + 1 < nk; kt += 2) {
+            step(S0{}, kt);
+            step(S1{}, kt + 1);
+        }
+        if (kt < nk) step(S0{}, kt);
     }
-    if (kt < nk) step(S0{}, kt);
     __syncthreads();  // the epilogues below reuse the LDS
 
     if (EPI == EPI_F32 || EPI == EPI_RESID) {
@@ -1391,6 +1481,15 @@ static GemmArgs gemm_base(void* const* p, uint32_t m, uint32_t n, uint32_t k) {
 }
 
 // 15 gemm_qkv_rope: h, w, q_norm, k_norm, cos, sin, q, k_cache, v_cache, m, hidden, q_heads, kv_heads, pos0, max_pos,
+// The GEMM's direct-to-LDS loop needs two blocks on every CU (MI355X: 256 CUs, two 64 KiB blocks each) for the whole
+// launch: grids of whole rounds of 512 tiles, or long enough (4 rounds) that a last partial round hardly counts. In a
+// partial round a CU holds one block, which the register-pipelined loop (loads two k steps ahead) serves better
+// (measured: the 768-tile SwiGLU GEMM of a 2048-token prefill, 42 against 44 us).
+static bool two_per_cu(const dim3& g) {
+    const uint64_t tiles = uint64_t(g.x) * g.y;
+    return tiles >= 512 && (tiles % 512 == 0 || tiles >= 4 * 512);
+}
+
 // eps
 static void l_gemm_qkv(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
@@ -1408,7 +1507,11 @@ static void l_gemm_qkv(const PreparedDispatch& pd, void* const* p, hipStream_t s
     a.pos0 = int(w[14]);
     a.max_pos = int(w[15]);
     a.eps = f32_of(w[16]);
-    hipLaunchKernelGGL((k_gemm<EPI_QKV, 128>), dim3(uint32_t(qh + 2 * kvh), (w[10] + GBM - 1) / GBM), dim3(256), 0, s, a);
+    const dim3 grid(uint32_t(qh + 2 * kvh), (w[10] + GBM - 1) / GBM);
+    if (two_per_cu(grid))
+        hipLaunchKernelGGL((k_gemm<EPI_QKV, 128, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemm<EPI_QKV, 128, false>), grid, dim3(256), 0, s, a);
 }
 
 // 16 attention_prefill_f16: q, k_cache, v_cache, y, rows, past, q_heads, kv_heads, max_pos, scale
@@ -1430,10 +1533,12 @@ static void l_gemm_resid(const PreparedDispatch& pd, void* const* p, hipStream_t
     GemmArgs a = gemm_base(p, w[4], w[5], w[6]);
     a.y32 = (float*)p[2];
     a.resid = (const float*)p[2];
-    if (resid_narrow(w[4], w[5]))
-        hipLaunchKernelGGL((k_gemm<EPI_RESID, 64>), dim3((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
+    if (resid_narrow(w[4], w[5]))  // under two blocks per CU by construction
+        hipLaunchKernelGGL((k_gemm<EPI_RESID, 64, false>), dim3((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM), dim3(256), 0, s,
+                           a);
     else
-        hipLaunchKernelGGL((k_gemm<EPI_RESID, 128>), dim3((w[5] + GBN - 1) / GBN, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_gemm<EPI_RESID, 128, true>), dim3((w[5] + GBN - 1) / GBN, (w[4] + GBM - 1) / GBM), dim3(256), 0,
+                           s, a);
 }
 
 // 18 gemm_swiglu: a, w (2 inter rows), y, m, inter, k
@@ -1442,7 +1547,11 @@ static void l_gemm_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_
     GemmArgs a = gemm_base(p, w[4], 2 * w[5], w[6]);
     a.y16 = (uint16_t*)p[2];
     a.inter = int(w[5]);
-    hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 128>), dim3((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
+    const dim3 grid((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM);
+    if (two_per_cu(grid))
+        hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 128, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 128, false>), grid, dim3(256), 0, s, a);
 }
 
 // 19 gemm_f32: a, w, y, m, n, k
@@ -1450,7 +1559,11 @@ static void l_gemm_f32(const PreparedDispatch& pd, void* const* p, hipStream_t s
     const uint32_t* w = pd.words.data();
     GemmArgs a = gemm_base(p, w[4], w[5], w[6]);
     a.y32 = (float*)p[2];
-    hipLaunchKernelGGL((k_gemm<EPI_F32, 128>), dim3((w[5] + GBN - 1) / GBN, (w[4] + GBM - 1) / GBM), dim3(256), 0, s, a);
+    const dim3 grid((w[5] + GBN - 1) / GBN, (w[4] + GBM - 1) / GBM);
+    if (two_per_cu(grid))
+        hipLaunchKernelGGL((k_gemm<EPI_F32, 128, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemm<EPI_F32, 128, false>), grid, dim3(256), 0, s, a);
 }
 
 // The decode GEMVs: one row (or gate/up pair) per wave, 4 waves per block; NCH, the 512-wide k-chunks per lane, is
