@@ -53,6 +53,37 @@ __global__ __launch_bounds__(256) void k_rmsnorm_f16(const float* x, const uint1
     for (uint32_t c = threadIdx.x; c < cols; c += 256u) yr[c] = f2h(bf2f(w[c]) * (xr[c] * rr));
 }
 
+// The same for cols = 256 NC (the model widths): one wave per row, four rows per block. Each lane loads its NC float4
+// of the row (lane l: columns 4 l + 256 j) at once and keeps them, so the row is read once, the sum of squares is a
+// wave reduction with no barrier, and the output goes out as 8-byte packs of four halves.
+template <int NC>
+__global__ __launch_bounds__(256) void k_rmsnorm_f16_wave(const float* x, const uint16_t* w, uint16_t* y,
+                                                          uint32_t rows, uint32_t cols, float eps, uint32_t row0) {
+    const uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float4* xr = reinterpret_cast<const float4*>(x + size_t(row0 + r) * cols) + lane;
+    const uint2* wr = reinterpret_cast<const uint2*>(w) + lane;
+    float4 v[NC];
+    uint2 wv[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        v[j] = xr[64 * j];
+        wv[j] = wr[64 * j];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) ss = fmaf(v[j].x, v[j].x, fmaf(v[j].y, v[j].y, fmaf(v[j].z, v[j].z, fmaf(v[j].w, v[j].w, ss))));
+    ss = wave_sum(ss);
+    const float rr = 1.0f / sqrtf(ss / float(cols) + eps);
+    uint2* yr = reinterpret_cast<uint2*>(y + size_t(r) * cols) + lane;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const float w0 = __uint_as_float(wv[j].x << 16), w1 = __uint_as_float(wv[j].x & 0xFFFF0000u);
+        const float w2 = __uint_as_float(wv[j].y << 16), w3 = __uint_as_float(wv[j].y & 0xFFFF0000u);
+        yr[64 * j] = make_uint2(pack2h(w0 * (v[j].x * rr), w1 * (v[j].y * rr)), pack2h(w2 * (v[j].z * rr), w3 * (v[j].w * rr)));
+    }
+}
+
 // ================================================================ GEMM (ids 15, 17, 18, 19)
 // C[m, n] = sum_k A[m, k] W[n, k] on f16 operands, 128 x 128 tiles (128 x 64 for the residual GEMMs of few tiles), k
 // in steps of 64, 4 waves each owning a 64 x 64 quarter as 4 x 4 MFMA tiles. Tiles are loaded from memory straight
@@ -1466,8 +1497,21 @@ static float f32_of(uint32_t b) {
 
 // 14 rmsnorm_rows_f16: x, w, y, rows, cols, eps, x_row0
 static void l_rmsnorm_f16(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
-    hipLaunchKernelGGL(k_rmsnorm_f16, dim3(pd.words[4]), dim3(256), 0, s, (const float*)p[0], (const uint16_t*)p[1],
-                       (uint16_t*)p[2], pd.words[4], pd.words[5], f32_of(pd.words[6]), pd.words[7]);
+    const uint32_t rows = pd.words[4], cols = pd.words[5];
+#define L_RMS(NC)                                                                                                    \
+    hipLaunchKernelGGL(k_rmsnorm_f16_wave<NC>, dim3((rows + 3) / 4), dim3(256), 0, s, (const float*)p[0],            \
+                       (const uint16_t*)p[1], (uint16_t*)p[2], rows, cols, f32_of(pd.words[6]), pd.words[7])
+    switch (cols % 256 == 0 ? cols / 256 : 0) {
+        case 1: L_RMS(1); break;
+        case 2: L_RMS(2); break;
+        case 4: L_RMS(4); break;
+        case 8: L_RMS(8); break;
+        case 16: L_RMS(16); break;
+        default:
+            hipLaunchKernelGGL(k_rmsnorm_f16, dim3(rows), dim3(256), 0, s, (const float*)p[0], (const uint16_t*)p[1],
+                               (uint16_t*)p[2], rows, cols, f32_of(pd.words[6]), pd.words[7]);
+    }
+#undef L_RMS
 }
 
 static GemmArgs gemm_base(void* const* p, uint32_t m, uint32_t n, uint32_t k) {

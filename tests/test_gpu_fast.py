@@ -199,9 +199,10 @@ def test_prefetch_overlapped(reusable):
         s.close()
 
 
-def test_rmsnorm_rows_f16():
-    rows, cols, row0 = 37, 1024, 5
-    r = np.random.default_rng(2)
+@pytest.mark.parametrize("rows,cols,row0", [(37, 1024, 5), (16, 2048, 0), (9, 256, 1), (5, 300, 2), (3, 64, 0)])
+def test_rmsnorm_rows_f16(rows, cols, row0):
+    """Widths that are multiples of 256 take the wave-per-row form, the others the block-per-row one."""
+    r = np.random.default_rng(2 + cols)
     x = (r.standard_normal((rows + row0, cols)) * 3).astype(np.float32)
     w = bf16(1 + 0.1 * r.standard_normal(cols))
     s = Session({"x": (F32, x.shape, RO, x), "w": (BF16, (cols,), RO, w), "y": (F16, (rows, cols), 0, None)})
