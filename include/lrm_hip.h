@@ -172,6 +172,11 @@ int lrm_qwen_decode_batch(lrm_qwen *q, const int32_t *ids, const int32_t *pos, i
 /* Rows of the logits buffer: after a decode step, row 0 holds that step's logits. */
 int lrm_qwen_read_logits(lrm_qwen *q, float *out, int rows);
 double lrm_qwen_last_ms(lrm_qwen *q); /* device time of the last forward / decode run, ms */
+/* 1 when the one-sequence decode step runs as the single persistent launch (catalog kernel decode_step_persistent:
+ * all layers in one dispatch, stages handed over through tagged exchange entries), 0 when it runs as the recorded list
+ * of per-stage kernels, -1 for a null model. No counterpart in the reference: its decode loop is the planned
+ * Lrm.Gpu.Exec composition of per-op dispatches (docs/dev-plan.md:166-170), which the per-stage list mirrors. */
+int lrm_qwen_persistent_decode(lrm_qwen *q);
 int lrm_qwen_token(lrm_qwen *q, const char *name, uint32_t *token);
 lrm_hip_device *lrm_qwen_device(lrm_qwen *q);
 int lrm_qwen_tap_count(lrm_qwen *q);

@@ -509,6 +509,8 @@ int lrm_qwen_read_logits(lrm_qwen* q, float* out, int rows) {
 
 double lrm_qwen_last_ms(lrm_qwen* q) { return q ? q->q.last_ms() : -1.0; }
 
+int lrm_qwen_persistent_decode(lrm_qwen* q) { return q ? (q->q.persistent_decode() ? 1 : 0) : -1; }
+
 int lrm_qwen_token(lrm_qwen* q, const char* name, uint32_t* token) {
     return guard([&] {
         need_ptr(q, "model");

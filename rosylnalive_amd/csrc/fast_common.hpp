@@ -80,17 +80,52 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// Cross-lane reductions without an LDS round trip: DPP moves inside each 16-lane row (quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror, row_mirror), then the gfx950 row swaps (v_permlane16_swap, v_permlane32_swap) across the
+// four rows. Every step adds a lane's value to its partner's, so partners hold the same bits (a + b == b + a) and the
+// result is identical in every lane of the group.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+// the sum over lanes 4 (l / 4) .. + 3
+__device__ __forceinline__ float quad4_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    return v + dpp_f<0x4E>(v);
 }
+
+// the sum over the 16 lanes of the row of lane l (lanes 16 (l / 16) .. + 15)
+__device__ __forceinline__ float row_sum16(float v) {
+    v = quad4_sum(v);
+    v += dpp_f<0x141>(v);
+    return v + dpp_f<0x140>(v);
+}
+
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    return fmaxf(v, dpp_f<0x140>(v));
+}
+
+// the sum / maximum over the four rows of lanes that share l % 16
+__device__ __forceinline__ float cross_rows_sum(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float cross_rows_max(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return cross_rows_sum(row_sum16(v)); }
+
+__device__ __forceinline__ float wave_max(float v) { return cross_rows_max(row_max16(v)); }
 
 }  // namespace fast
 }  // namespace lrm

@@ -28,6 +28,7 @@
 
 #include "device.hpp"
 #include "fast_common.hpp"
+#include "persist.hpp"
 
 namespace lrm {
 using namespace fast;
@@ -525,20 +526,6 @@ __device__ __forceinline__ int vt_slot(int k) {
     return (k & 32) + 8 * ((k & 15) >> 2) + 4 * ((k >> 4) & 1) + (k & 3);
 }
 
-// Sum and maximum over the four lanes of a wave that share lane % 16 (lanes l, l ^ 16, l ^ 32, l ^ 48), with the
-// cross-row lane swaps: no LDS round trip. Every lane of the group gets the same bits.
-__device__ __forceinline__ float quad_max(float v) {
-    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float quad_sum(float v) {
-    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
 __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                                       uint16_t* y, int T, int past, int qh, int max_pos,
                                                       float scale_log2) {
@@ -647,7 +634,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
                 if (need_mask) s[kt][r] = (kt * 16 + 4 * g + r > lim) ? -INFINITY : s[kt][r];
                 mloc = fmaxf(mloc, s[kt][r]);
             }
-        mloc = quad_max(mloc);
+        mloc = cross_rows_max(mloc);
         const float m_new = fmaxf(m_run, mloc);  // running max of the raw scores
         const float mc = m_new == -INFINITY ? 0.f : m_new * scale_log2;
         // the hardware exp2 (results below 2^-126 flush to 0: weights that small are below fp16 P anyway)
@@ -661,7 +648,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
                 pv[kt][r] = __builtin_amdgcn_exp2f(fmaf(s[kt][r], scale_log2, -mc));
                 lsum += pv[kt][r];
             }
-        lsum = quad_sum(lsum);
+        lsum = cross_rows_sum(lsum);
         l_run = l_run * alpha + lsum;
         m_run = m_new;
         if (__any(alpha != 1.0f)) {  // rescale only when some row's maximum moved (wave-uniform branch)
@@ -929,11 +916,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
                 a0 = fmaf(q0[e], kf[e], a0);
                 a1 = fmaf(q1[e], kf[e], a1);
             }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                a0 += __shfl_xor(a0, o, 64);
-                a1 += __shfl_xor(a1, o, 64);
-            }
+            a0 = row_sum16(a0);
+            a1 = row_sum16(a1);
             if ((lane & 15) == 0) {
                 const bool ok = !tail || cb + key < nkeys;
                 ps[0][key] = ok ? a0 * scale_log2 : -INFINITY;
@@ -1786,6 +1770,9 @@ static void l_prefetch(const PreparedDispatch& pd, void* const* p, hipStream_t s
                        (const u32x4*)p[2], n[2], (const u32x4*)p[3], n[3]);
 }
 
+// 38 decode_step_persistent (kernels_persist.hip)
+void launch_decode_persistent(const PreparedDispatch& pd, void* const* p, hipStream_t s);
+
 int fast_first_id() { return 14; }
 
 const LaunchFn* fast_launchers() {
@@ -1794,11 +1781,11 @@ const LaunchFn* fast_launchers() {
                                  l_gemv_swiglu, l_lmhead,    l_argmax_dec,   l_embed_dec,    l_fill_normal,
                                  l_convert,     l_argmax_partial, l_argmax_final, l_gemm_skinny_f32,
                                  l_gemm_skinny_resid, l_gemm_skinny_swiglu, l_attn_combine_f16, l_decode_advance,
-                                 l_prefetch};
+                                 l_prefetch,    launch_decode_persistent};
     return t;
 }
 
-// ---------------------------------------------------------------- catalog entries (ids 14..29)
+// ---------------------------------------------------------------- catalog entries (ids 14..38)
 
 #define DT(x) (1u << (x))
 #define TOK_R(n, m) FieldSpec{n, FieldKind::Token, Access::Read, m, nullptr}
@@ -2101,6 +2088,45 @@ std::vector<KernelSpec> fast_catalog() {
                  {TOK_R("x0", DT(F32) | DT(BF16) | DT(F16) | DT(U32)), TOK_R("x1", DT(F32) | DT(BF16) | DT(F16) | DT(U32)),
                   TOK_R("x2", DT(F32) | DT(BF16) | DT(F16) | DT(U32)), TOK_R("x3", DT(F32) | DT(BF16) | DT(F16) | DT(U32))},
                  [](const uint32_t*, const uint32_t*) {}});
+    // 38 decode_step_persistent: the whole one-sequence decode step in one launch of `blocks` resident workgroups.
+    // Weights and caches are the layer-stacked tensors ([layers, ...]); the exchange buffer holds the header and the
+    // tagged hand-off entries (persist::exchange_entries 8-byte entries).
+    c.push_back({"decode_step_persistent", "fast", {persist::kThreads, 1, 1}, true,
+                 [](const uint32_t* w) { return Grid3{w[30], 1, 1}; },
+                 {TOK_R("embed", DT(BF16)), TOK_R("final_norm", DT(BF16)), TOK_R("in_norm", DT(BF16)),
+                  TOK_R("qkv", DT(BF16)), TOK_R("q_norm", DT(BF16)), TOK_R("k_norm", DT(BF16)), TOK_R("o_proj", DT(BF16)),
+                  TOK_R("post_norm", DT(BF16)), TOK_R("gate_up", DT(BF16)), TOK_R("down", DT(BF16)),
+                  TOK_RW("k_cache", DT(F16)), TOK_RW("v_cache", DT(F16)), TOK_R("cos", DT(F32)), TOK_R("sin", DT(F32)),
+                  TOK_W("logits", DT(F32)), TOK_RW("state", DT(U32)), TOK_W("out_ids", DT(U32)),
+                  TOK_RW("exchange", DT(U32)), U32F("layers"), U32F("hidden"), U32F("q_heads"), U32F("kv_heads"),
+                  U32F("inter"), U32F("vocab"), U32F("max_pos"), U32F("max_steps"), U32F("write_logits"), F32F("eps"),
+                  F32F("scale"), U32F("blocks")},
+                 [](const uint32_t* w, const uint32_t* c) {
+                     const int64_t L = w[19], H = w[20], QH = w[21], KVH = w[22], I = w[23], V = w[24], MP = w[25];
+                     const persist::Shape sh{int(H), int(QH), int(KVH), 128, int(I), int(MP), int(w[30])};
+                     if (L < 1 || V < 1 || MP < 1) contract_fail("decode_step_persistent: layers, vocab and max_pos >= 1");
+                     if (const char* why = persist::unsupported(sh))
+                         contract_fail("decode_step_persistent: this shape is not covered (%s)", why);
+                     const int64_t N1 = (QH + 2 * KVH) * 128;
+                     need(c, 0, V * H, "decode_step_persistent", "embed");
+                     need(c, 1, H, "decode_step_persistent", "final_norm");
+                     need(c, 2, L * H, "decode_step_persistent", "in_norm");
+                     need(c, 3, L * N1 * H, "decode_step_persistent", "qkv");
+                     need(c, 4, L * 128, "decode_step_persistent", "q_norm");
+                     need(c, 5, L * 128, "decode_step_persistent", "k_norm");
+                     need(c, 6, L * H * QH * 128, "decode_step_persistent", "o_proj");
+                     need(c, 7, L * H, "decode_step_persistent", "post_norm");
+                     need(c, 8, L * 2 * I * H, "decode_step_persistent", "gate_up");
+                     need(c, 9, L * H * I, "decode_step_persistent", "down");
+                     need(c, 10, L * KVH * MP * 128, "decode_step_persistent", "k_cache");
+                     need(c, 11, L * KVH * MP * 128, "decode_step_persistent", "v_cache");
+                     need(c, 12, MP * 64, "decode_step_persistent", "cos");
+                     need(c, 13, MP * 64, "decode_step_persistent", "sin");
+                     need(c, 14, w[27] ? V : 0, "decode_step_persistent", "logits");
+                     need(c, 15, 3, "decode_step_persistent", "state");
+                     need(c, 16, w[26], "decode_step_persistent", "out_ids");
+                     need(c, 17, 2 * int64_t(persist::exchange_entries(int(L), sh)), "decode_step_persistent", "exchange");
+                 }});
     return c;
 }
 

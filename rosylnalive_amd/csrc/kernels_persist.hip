@@ -1,0 +1,751 @@
+// ================================================================ 38 decode_step_persistent
+// The one-sequence decode step (embed, every layer, lm_head, greedy argmax, state advance) as ONE launch: G
+// workgroups of 8 waves (G = 256 on MI355X, one per CU, all resident together) walk the layers stage by stage, each
+// taking a fixed share of every stage, and hand the stage outputs to each other through tagged exchange entries in
+// device memory instead of kernel boundaries. It computes what the multi-kernel step of the executor computes
+// (embed_dec, then per layer gemv_norm_dec, attention_decode_f16, attention_combine, gemv_residual_dec,
+// gemv_swiglu_dec, gemv_residual_dec, then lmhead_dec and argmax_dec) with the same per-lane arithmetic; only the
+// order of a few partial sums differs (the o_proj, SwiGLU and down rows are split over two waves, the split combine
+// runs one split per lane).
+//
+// Why: batch-1 decode of a 0.6B model moves ~1.2 GB per token, ~150 us at HBM speed, but as ~170 dependent kernels
+// it is bound by launch and ramp latency (4-6 us per kernel). Here each hand-off costs one store and one poll (about
+// 1 us between CUs), and every workgroup issues the weight loads of its next stage before it waits, so the weight
+// stream overlaps the hand-off latency.
+//
+// Exchange entries are 8 bytes: (tag << 32) | value bits, written by one agent-scope 64-bit store and read by
+// agent-scope 64-bit loads (both coherent across the XCDs' L2s without cache maintenance), so a consumer polls the
+// data itself: an entry is ready when it carries this launch's tag. The tag is the launch epoch + 1 (header word 0,
+// advanced by workgroup 0 at the end of every step), so entries left by earlier steps never match. Every entry is
+// written once per step; nothing is reset between steps. The vectors every workgroup reads are written in 8 copies,
+// one per XCD, so each copy is polled by 32 workgroups instead of 256 (all of them polling one copy measured 1.7-2.8
+// us per hand-off, the lines of the copy being the bottleneck).
+//
+// Stages of layer l (G = 256, Qwen3-0.6B: hidden 1024, 16/8 heads, intermediate 3072):
+//   A  q|k|v = W_qkv . RMSNorm(x): 2 rows per wave. Waits for x (all of it: the RMSNorm needs the whole row).
+//   B  attention: workgroup b takes KV head b / S (S = G / kv_heads = 32 splits) and the keys [s KPS, (s + 1) KPS)
+//      of split s = b % S (KPS a multiple of 64 chosen so the splits cover pos + 1 keys), both query heads, 64 keys
+//      at a time with an online softmax; the split holding pos also normalises, rotates and appends the new key and
+//      value. Its K/V loads are issued before it waits for q. Writes (max, sum, out[128]) per query head.
+//   B' combine: 8 output dims of one query head per workgroup, one split per lane.
+//   C  x += W_o . o: 4 rows per workgroup, each split over two waves.
+//   D  a = silu(W_g . h) * (W_u . h), h = RMSNorm(x): 12 gate/up pairs per workgroup.
+//   E  x += W_d . a: 4 rows per workgroup, each split over two waves.
+// Then every workgroup takes 1/G of the lm_head rows and writes its (max, lowest index); workgroup 0 merges them,
+// records the id and advances the state (position, id, step) for the next launch.
+//
+// Every wait is bounded: a poll that waits longer than 0.2 s, or sees another workgroup's abort, sets the abort word
+// (header word 1) and the stage (word 2) and the workgroup returns; so every wave ends even if a workgroup were never
+// scheduled. A launch that finds the abort word set returns at once; the host reads the word after the steps and
+// raises. Launches on one device must not overlap (the executor keeps them on one stream).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <type_traits>
+
+#include "device.hpp"
+#include "fast_common.hpp"
+#include "persist.hpp"
+
+namespace lrm {
+using namespace fast;
+using namespace persist;
+
+namespace {
+
+constexpr long long kWaitTicks = 20000000;  // 0.2 s of the 100 MHz constant clock
+
+struct PArgs {
+    const uint16_t* embed;       // [V, H] bf16; also the tied lm_head
+    const uint16_t* final_norm;  // [H]
+    const uint16_t* in_norm;     // [L, H]
+    const uint16_t* qkv;         // [L, QC + 2 KC, H]
+    const uint16_t* q_norm;      // [L, 128]
+    const uint16_t* k_norm;      // [L, 128]
+    const uint16_t* o_proj;      // [L, H, QC]
+    const uint16_t* post_norm;   // [L, H]
+    const uint16_t* gate_up;     // [L, 2 I, H] (gate rows, then up rows)
+    const uint16_t* down;        // [L, H, I]
+    uint16_t* kc;                // [L, KVH, MP, 128] f16
+    uint16_t* vc;                // [L, KVH, 128, MP] f16
+    const float* cos_t;          // [MP, 64]
+    const float* sin_t;          // [MP, 64]
+    float* logits;               // [V]
+    uint32_t* state;             // position, id, step
+    uint32_t* out_ids;           // [max_steps]
+    uint64_t* xch;               // exchange: header, then the entries
+    int layers, hidden, qh, kvh, inter, vocab, max_pos, max_steps, write_logits;
+    float eps, scale_log2;
+};
+
+__device__ __forceinline__ uint64_t xload(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void xstore(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t word_load(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void abort_step(uint32_t* hdr, int stage) {
+    __hip_atomic_store(hdr + 2, uint32_t(stage), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(hdr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void unpack8bf(u32x4 v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(v[i] << 16);
+        f[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
+    }
+}
+
+__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Block-wide: waits until the entries at idx(i), i < n (n <= E * 512), carry `tag` and writes their values to dst[i]
+// in LDS. Thread t polls entries t, t + 512, ..., re-reading only those not yet ready. When the step is aborted (this
+// wait timed out or another workgroup aborted) it sets `fail` (the workgroup's LDS flag), which the caller reads after
+// the barrier that ends the wait. `fail` must stay an LDS access: a generic (flat) read would also wait for every
+// global load in flight, the prefetched weights included.
+template <int E, typename F>
+__device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, uint32_t* hdr, int stage, int& fail) {
+    const int t = threadIdx.x;
+    bool pend[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) pend[e] = t + e * kThreads < n;
+    long long start = 0;
+    for (int it = 0;; ++it) {
+        uint64_t v[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = pend[e] ? xload(idx(t + e * kThreads)) : 0ull;
+        bool any = false;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            if (pend[e] && uint32_t(v[e] >> 32) == tag) {
+                dst[t + e * kThreads] = __uint_as_float(uint32_t(v[e]));
+                pend[e] = false;
+            }
+            any |= pend[e];
+        }
+        if (!any) break;
+        if (it == 0) {
+            start = wall_clock64();
+        } else if ((it & 15) == 0 && (word_load(hdr + 1) != 0u || wall_clock64() - start > kWaitTicks)) {
+            abort_step(hdr, stage);
+            fail = 1;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    lds_barrier();
+    // Nothing is in flight now (every poll waited for all older loads and stores); saying so lets the compiler's
+    // wait counting start from zero after the loop instead of waiting for loads issued later.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+}
+
+// This lane's values k = 512 c + 8 lane + e of RMSNorm(vec) (vec in LDS, 512 NCH wide): every wave reads the whole
+// vector and reduces its own sum of squares, in the order of the multi-kernel GEMVs (rmsnorm_chunks).
+template <int NCH>
+__device__ __forceinline__ void norm_lane(const float* vec, const u32x4 (&nw)[NCH], float eps, float (&xv)[NCH][8]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const float4 lo = *reinterpret_cast<const float4*>(vec + 512 * c + 8 * lane);
+        const float4 hi = *reinterpret_cast<const float4*>(vec + 512 * c + 8 * lane + 4);
+        xv[c][0] = lo.x, xv[c][1] = lo.y, xv[c][2] = lo.z, xv[c][3] = lo.w;
+        xv[c][4] = hi.x, xv[c][5] = hi.y, xv[c][6] = hi.z, xv[c][7] = hi.w;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(xv[c][e], xv[c][e], ss);
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / float(512 * NCH) + eps);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        float g[8];
+        unpack8bf(nw[c], g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[c][e] = g[e] * (xv[c][e] * r);
+    }
+}
+
+// sum over this lane's chunks of w . v (bf16 weights, f32 vector in registers), not yet reduced over the wave
+__device__ __forceinline__ float dot8(u32x4 wv, const float* v, float acc) {
+    float f[8];
+    unpack8bf(wv, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(f[e], v[e], acc);
+    return acc;
+}
+
+// the same with the vector in LDS at vec[k0 .. k0 + 7]
+__device__ __forceinline__ float dot8_lds(u32x4 wv, const float* vec, int k0, float acc) {
+    const float4 lo = *reinterpret_cast<const float4*>(vec + k0);
+    const float4 hi = *reinterpret_cast<const float4*>(vec + k0 + 4);
+    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    return dot8(wv, v, acc);
+}
+
+template <int NCH, int RA, int NCC, int UD, int NCE, int KSX>
+__global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
+    __shared__ __align__(16) float vec[kVecMax];
+    __shared__ float red[64];
+    __shared__ float qs[2][128];
+    __shared__ float knew[128], vnew[128];
+    __shared__ float ps[2][64];
+    __shared__ float alpha_s[2];
+    __shared__ float xown[8];
+    __shared__ float lmv[kWaves];
+    __shared__ uint32_t lmi[kWaves];
+    __shared__ int s_fail;
+
+    const int b = blockIdx.x, G = gridDim.x, t = threadIdx.x, lane = t & 63;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: row offsets stay scalar
+    uint32_t* hdr = reinterpret_cast<uint32_t*>(a.xch);
+    const uint32_t pos = word_load(a.state), id = word_load(a.state + 1), step = word_load(a.state + 2);
+    const uint32_t tag = word_load(hdr) + 1u;
+    if (pos >= uint32_t(a.max_pos) || word_load(hdr + 1) != 0u) return;  // the same words for every workgroup
+    if (t == 0) s_fail = 0;
+
+    const int H = a.hidden, QC = a.qh * 128, KC = a.kvh * 128, N1 = QC + 2 * KC, I = a.inter, MP = a.max_pos;
+    const int S = G / a.kvh, RB = kWaves / KSX, KS = KSX, PB = I / G;
+    const XLayout X(a.qh, a.kvh, H, I, G);
+    const int gw = b * kWaves + w, NWv = G * kWaves;
+    const int rr = b * RB + w / KS, ks = w % KS;  // stages C and E: this wave's row and its part of the row
+    const int rep = b % kReplicas;                // the copy of the shared vectors this workgroup polls
+
+    // attention split of this workgroup (stage B): fixed for the step
+    const int hk = b / S, s = b % S;
+    const int ntot = int(pos) + 1;
+    const int KPS = ((ntot + S - 1) / S + 63) / 64 * 64;
+    const int S_used = (ntot + KPS - 1) / KPS;
+    const bool attn = s < S_used;
+    const bool has_pos = s == S_used - 1;  // the split of the last key, pos
+    const int k0 = s * KPS, nk = attn ? min(KPS, ntot - k0) : 0, nch = (nk + 63) / 64;
+    const int jnew = int(pos) - k0;
+
+    u32x4 wa[RA][NCH], na[NCH];
+    auto issue_a = [&](int l) __attribute__((always_inline)) {
+        const uint16_t* W = a.qkv + size_t(l) * N1 * H;
+#pragma unroll
+        for (int r = 0; r < RA; ++r) {
+            const int row = min(gw + r * NWv, N1 - 1);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) wa[r][c] = ld16(W + size_t(row) * H + 512 * c + 8 * lane);
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) na[c] = ld16(a.in_norm + size_t(l) * H + 512 * c + 8 * lane);
+    };
+
+    // x = widen(E[id]) (NaN for an id outside the vocabulary, as embed_dec); this workgroup keeps rows b RB .. + RB
+    issue_a(0);
+    for (int k = t; k < H; k += kThreads)
+        vec[k] = id < uint32_t(a.vocab) ? bf2f(a.embed[size_t(id) * H + k]) : __uint_as_float(0x7FC00000u);
+    lds_barrier();
+    if (t < RB) xown[t] = vec[b * RB + t];
+
+    for (int l = 0; l < a.layers; ++l) {
+        uint64_t* xl = a.xch + kHdrEntries + size_t(l) * X.per_layer;
+        // ---------------------------------------------------------------- A: q|k|v = W_qkv . RMSNorm(x)
+        if (l > 0) {
+            const uint64_t* src = xl - X.per_layer + X.x2 + rep * H;
+            gather<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, tag, vec, hdr, 1, s_fail);
+            if (s_fail) return;
+        }
+        // this split's first two 64-key chunks of K and V^T: they do not depend on this step, so they load while the
+        // projections are computed and handed over. K: thread t holds key slots t / 16 and t / 16 + 32 of a chunk,
+        // dims 8 (t % 16) .. + 7; V^T: dim t / 4, keys 16 (t % 4) .. + 15. Past the last chunk: re-read it (never used).
+        const uint16_t* kb = a.kc + ((size_t(l) * a.kvh + hk) * MP + k0) * 128 + 8 * (t & 15);
+        const uint16_t* vb = a.vc + ((size_t(l) * a.kvh + hk) * 128 + (t >> 2)) * MP + k0 + 16 * (t & 3);
+        u32x4 kr[2][2], vr[2][2];
+        auto fetch = [&](auto set, int c) __attribute__((always_inline)) {
+            constexpr int SET = decltype(set)::value;
+            const int cc = min(c, nch - 1) * 64;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) kr[SET][i] = ld16(kb + size_t(cc + (t >> 4) + 32 * i) * 128);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) vr[SET][j] = ld16(vb + cc + 8 * j);
+        };
+        using C0 = std::integral_constant<int, 0>;
+        using C1 = std::integral_constant<int, 1>;
+        if (attn) {
+            fetch(C0{}, 0);
+            fetch(C1{}, 1);
+        }
+        {
+            float xv[NCH][8];
+            norm_lane<NCH>(vec, na, a.eps, xv);
+#pragma unroll
+            for (int r = 0; r < RA; ++r) {
+                const int row = gw + r * NWv;
+                float acc = 0.f;
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) acc = dot8(wa[r][c], xv[c], acc);
+                acc = wave_sum(acc);
+                if (lane == 0 && row < N1) xstore(xl + X.qkv + row, acc, tag);
+            }
+        }
+        // stage C's o_proj weights: this wave's part of row rr
+        u32x4 wc[NCC];
+        {
+            const uint16_t* W = a.o_proj + (size_t(l) * H + rr) * QC + ks * (QC / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCC; ++c) wc[c] = ld16(W + 512 * c);
+        }
+
+        // ---------------------------------------------------------------- B: attention over this split
+        if (attn) {
+            // the rotation of pos and the norm weights do not depend on the step's projections: load them first
+            const int grp = t >> 7, d = t & 127;
+            const float cs = a.cos_t[size_t(pos) * 64 + (d & 63)], sn = a.sin_t[size_t(pos) * 64 + (d & 63)];
+            const float nwt = bf2f(t < 256 ? a.q_norm[l * 128 + d] : a.k_norm[l * 128 + d]);
+            const uint64_t* src = xl + X.qkv;
+            const int qo = 2 * hk * 128, ko = QC + hk * 128, vo = QC + KC + hk * 128;
+            gather<1>([&](int i) { return src + (i < 256 ? qo + i : i < 384 ? ko + i - 256 : vo + i - 384); },
+                   has_pos ? 512 : 256, tag, vec, hdr, 2, s_fail);
+            if (s_fail) return;
+            // per-head RMSNorm (q heads: threads 0-255, the new key: 256-383), then the rotation of (d, d + 64); the
+            // split holding pos appends the rotated key and the value to the caches, rounded to fp16
+            const float val = (t < 256 || has_pos) ? vec[t] : 0.f;
+            const float sq = wave_sum(val * val);
+            if (lane == 0) red[w] = sq;
+            lds_barrier();
+            const float nr = nwt * (val * (1.0f / sqrtf((red[2 * grp] + red[2 * grp + 1]) / 128.0f + a.eps)));
+            if (t < 256)
+                qs[grp][d] = nr;
+            else if (t < 384)
+                knew[d] = nr;
+            lds_barrier();
+            float rot = 0.f;
+            if (t < 256)
+                rot = d < 64 ? nr * cs - qs[grp][d + 64] * sn : nr * cs + qs[grp][d - 64] * sn;
+            else if (t < 384)
+                rot = d < 64 ? nr * cs - knew[d + 64] * sn : nr * cs + knew[d - 64] * sn;
+            lds_barrier();
+            if (t < 256) {
+                qs[grp][d] = rot;
+            } else if (has_pos && t < 384) {
+                const uint16_t kh = f2h(rot);
+                knew[d] = h2f(kh);
+                a.kc[((size_t(l) * a.kvh + hk) * MP + pos) * 128 + d] = kh;
+            } else if (has_pos) {
+                const uint16_t vh = f2h(val);
+                vnew[d] = h2f(vh);
+                a.vc[((size_t(l) * a.kvh + hk) * 128 + d) * MP + pos] = vh;
+            }
+            lds_barrier();
+            // this thread's query dims and, for the split holding pos, its slices of the new key and value (read
+            // unconditionally, used through selects)
+            const int d0 = 8 * (t & 15);
+            float q0[8], q1[8], kn8[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                q0[e] = qs[0][d0 + e];
+                q1[e] = qs[1][d0 + e];
+                kn8[e] = knew[d0 + e];
+            }
+            const float vn = vnew[t >> 2];
+            float m_run = -INFINITY, l_run = 0.f;  // waves 0 and 1: the running statistics of head w
+            float o0 = 0.f, o1 = 0.f;              // dim t / 4 of both heads over keys 16 (t % 4) .. + 15
+            auto chunk = [&](auto set, auto tailc, int c) __attribute__((always_inline)) {
+                constexpr int SET = decltype(set)::value;
+                constexpr bool tail = decltype(tailc)::value;
+                const int cb = c * 64;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int key = (t >> 4) + 32 * i;
+                    float kf[8];
+                    unpack8h(kr[SET][i], kf);
+                    if constexpr (tail) {
+                        const bool is_new = has_pos && cb + key == jnew;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) kf[e] = is_new ? kn8[e] : kf[e];
+                    }
+                    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        a0 = fmaf(q0[e], kf[e], a0);
+                        a1 = fmaf(q1[e], kf[e], a1);
+                    }
+                    a0 = row_sum16(a0);
+                    a1 = row_sum16(a1);
+                    if ((t & 15) == 0) {
+                        const bool ok = !tail || cb + key < nk;
+                        ps[0][key] = ok ? a0 * a.scale_log2 : -INFINITY;
+                        ps[1][key] = ok ? a1 * a.scale_log2 : -INFINITY;
+                    }
+                }
+                lds_barrier();
+                if (w < 2) {  // online softmax of head w over the chunk (its key 0 is always valid)
+                    const float v = ps[w][lane];
+                    const float m_new = fmaxf(m_run, wave_max(v));
+                    const float e = exp2f(v - m_new);
+                    const float al = exp2f(m_run - m_new);  // 0 on the first chunk
+                    l_run = l_run * al + wave_sum(e);
+                    m_run = m_new;
+                    ps[w][lane] = e;
+                    if (lane == 0) alpha_s[w] = al;
+                }
+                lds_barrier();
+                const int kg = 16 * (t & 3);
+                float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    float vf[8];
+                    unpack8h(vr[SET][j], vf);
+                    if constexpr (tail) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int key = cb + kg + 8 * j + e;
+                            vf[e] = key >= nk ? 0.f : (has_pos && key == jnew ? vn : vf[e]);
+                        }
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        a0 = fmaf(ps[0][kg + 8 * j + e], vf[e], a0);
+                        a1 = fmaf(ps[1][kg + 8 * j + e], vf[e], a1);
+                    }
+                }
+                o0 = fmaf(o0, alpha_s[0], a0);
+                o1 = fmaf(o1, alpha_s[1], a1);
+                lds_barrier();  // ps and alpha_s are rewritten by the next chunk
+            };
+            using Body = std::false_type;
+            using Tail = std::true_type;
+            int c = 0;
+            for (; c + 2 < nch; c += 2) {  // whole pairs before the last chunk
+                chunk(C0{}, Body{}, c);
+                fetch(C0{}, c + 2);
+                chunk(C1{}, Body{}, c + 1);
+                fetch(C1{}, c + 3);
+            }
+            if (c + 1 < nch) {
+                chunk(C0{}, Body{}, c);
+                chunk(C1{}, Tail{}, c + 1);
+            } else {
+                chunk(C0{}, Tail{}, c);
+            }
+            // reduce the four key groups of each dim and write the partials of both heads
+            o0 = quad4_sum(o0);
+            o1 = quad4_sum(o1);
+            uint64_t* p0 = xl + X.part + size_t(2 * hk * S + s) * 130;
+            uint64_t* p1 = p0 + size_t(S) * 130;
+            if ((t & 3) == 0) {
+                xstore(p0 + 2 + (t >> 2), o0, tag);
+                xstore(p1 + 2 + (t >> 2), o1, tag);
+            }
+            if (w < 2 && lane == 0) {
+                uint64_t* pw = w == 0 ? p0 : p1;
+                xstore(pw, m_run, tag);
+                xstore(pw + 1, l_run, tag);
+            }
+        }
+
+        // ---------------------------------------------------------------- B': combine the splits
+        // item it = b + G j: query head it / 16, dims 8 (it % 16) .. + 7; wave j merges the S_used splits, one per lane
+        {
+            const int items = (a.qh * 16 - b + G - 1) / G;
+            const int per_item = S_used * 10;
+            const uint64_t* src = xl + X.part;
+            lds_barrier();  // vec may still be read by stage A's or B's waves
+            gather<1>(
+               [&](int i) {
+                   const int j = i / per_item, r = i - j * per_item, sp = r / 10, k = r - sp * 10;
+                   const int it = b + G * j, hq = it >> 4, d8 = (it & 15) * 8;
+                   return src + size_t(hq * S + sp) * 130 + (k < 2 ? k : d8 + k);
+               },
+               items * per_item, tag, vec, hdr, 3, s_fail);
+            if (s_fail) return;
+            if (w < items) {
+                const int it = b + G * w, hq = it >> 4, d8 = (it & 15) * 8;
+                const bool ok = lane < S_used;
+                const float* v = vec + w * per_item + (ok ? lane : 0) * 10;
+                const float m = ok ? v[0] : -INFINITY;
+                const float M = wave_max(m);
+                const float e = ok ? exp2f(m - M) : 0.f;
+                const float L = wave_sum(ok ? v[1] * e : 0.f);
+                float mine = 0.f;  // lane l: dim d8 + l % 8, stored into copy l / 8
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float sk = wave_sum(ok ? v[2 + k] * e : 0.f);
+                    if ((lane & 7) == k) mine = sk;
+                }
+                xstore(xl + X.o + (lane >> 3) * QC + hq * 128 + d8 + (lane & 7), mine / L, tag);
+            }
+        }
+
+        // ---------------------------------------------------------------- C: x += W_o . o
+        lds_barrier();  // the combine reads vec
+        {
+            const uint64_t* src = xl + X.o + rep * QC;
+            gather<NCC * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, QC, tag, vec, hdr, 4,
+                             s_fail);
+            if (s_fail) return;
+        }
+        {
+            float acc = 0.f;
+            const int kb0 = ks * (QC / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCC; ++c) acc = dot8_lds(wc[c], vec, kb0 + 512 * c, acc);
+            acc = wave_sum(acc);
+            if (lane == 0) red[w] = acc;
+        }
+        // stage D's gate/up weights: unit u = w UD + j is (row u / NCH of the workgroup's 2 PB, chunk j % NCH); rows
+        // 0 .. PB - 1 are gate rows b PB + r, the rest the matching up rows
+        u32x4 wd[UD], nd[NCH];
+#pragma unroll
+        for (int j = 0; j < UD; ++j) {
+            const int ri = (w * UD + j) / NCH, c = j % NCH;
+            const int grow = ri < PB ? b * PB + ri : I + b * PB + (ri - PB);
+            wd[j] = ld16(a.gate_up + (size_t(l) * 2 * I + grow) * H + 512 * c + 8 * lane);
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) nd[c] = ld16(a.post_norm + size_t(l) * H + 512 * c + 8 * lane);
+        lds_barrier();
+        if (t < RB * kReplicas) {  // thread t: row t / 8 into copy t % 8 (one wave: every read precedes the write)
+            const int i = t / kReplicas, r = t % kReplicas;
+            float sum = 0.f;
+            for (int k = 0; k < KS; ++k) sum += red[i * KS + k];
+            const float xn = xown[i] + sum;
+            if (r == 0) xown[i] = xn;
+            xstore(xl + X.x1 + r * H + b * RB + i, xn, tag);
+        }
+
+        // ---------------------------------------------------------------- D: a = silu(W_g . h) * (W_u . h)
+        {
+            const uint64_t* src = xl + X.x1 + rep * H;
+            gather<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, tag, vec, hdr, 5, s_fail);
+            if (s_fail) return;
+        }
+        {
+            float xv[NCH][8];
+            norm_lane<NCH>(vec, nd, a.eps, xv);
+#pragma unroll
+            for (int j = 0; j < UD; ++j) {
+                const int ri = (w * UD + j) / NCH, c = j % NCH;
+                float acc = dot8(wd[j], xv[c], 0.f);
+                acc = wave_sum(acc);
+                if (lane == 0) red[ri * NCH + c] = acc;
+            }
+        }
+        // stage E's down_proj weights: this wave's part of row rr
+        u32x4 we[NCE];
+        {
+            const uint16_t* W = a.down + (size_t(l) * H + rr) * I + ks * (I / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCE; ++c) we[c] = ld16(W + 512 * c);
+        }
+        lds_barrier();
+        if (t < PB * kReplicas) {  // thread t: pair t / 8 into copy t % 8
+            const int j = t / kReplicas, r = t % kReplicas;
+            float g = 0.f, u = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                g += red[j * NCH + c];
+                u += red[(PB + j) * NCH + c];
+            }
+            xstore(xl + X.a + r * I + b * PB + j, g / (1.0f + __expf(-g)) * u, tag);
+        }
+
+        // ---------------------------------------------------------------- E: x += W_d . a
+        {
+            const uint64_t* src = xl + X.a + rep * I;
+            gather<NCE * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, I, tag, vec, hdr, 6,
+                             s_fail);
+            if (s_fail) return;
+        }
+        {
+            float acc = 0.f;
+            const int kb0 = ks * (I / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCE; ++c) acc = dot8_lds(we[c], vec, kb0 + 512 * c, acc);
+            acc = wave_sum(acc);
+            if (lane == 0) red[w] = acc;
+        }
+        if (l + 1 < a.layers) issue_a(l + 1);
+        lds_barrier();
+        if (t < RB * kReplicas) {
+            const int i = t / kReplicas, r = t % kReplicas;
+            float sum = 0.f;
+            for (int k = 0; k < KS; ++k) sum += red[i * KS + k];
+            const float xn = xown[i] + sum;
+            if (r == 0) xown[i] = xn;
+            xstore(xl + X.x2 + r * H + b * RB + i, xn, tag);
+        }
+    }
+
+    // ---------------------------------------------------------------- lm_head over rows [r0, r1), then the argmax
+    const int V = a.vocab, per = (V + G - 1) / G, r0 = b * per, r1 = min(V, r0 + per);
+    u32x4 ra[4][NCH], rb4[4][NCH], nf[NCH];
+    auto load4 = [&](u32x4 (&dst)[4][NCH], int row) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint16_t* er = a.embed + size_t(min(row + r, V - 1)) * H + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) dst[r][c] = ld16(er + 512 * c);
+        }
+    };
+    load4(ra, r0 + 4 * w);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) nf[c] = ld16(a.final_norm + 512 * c + 8 * lane);
+    {
+        const uint64_t* src = a.xch + kHdrEntries + size_t(a.layers - 1) * X.per_layer + X.x2 + rep * H;
+        gather<NCH>([&](int i) { return src + i; }, H, tag, vec, hdr, 7, s_fail);
+        if (s_fail) return;
+    }
+    float xv[NCH][8];
+    norm_lane<NCH>(vec, nf, a.eps, xv);
+    float best = -INFINITY;
+    uint32_t besti = 0xFFFFFFFFu;
+    bool nan = false;
+    auto proc = [&](const u32x4 (&src)[4][NCH], int row) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) acc = dot8(src[r][c], xv[c], acc);
+            const float v = wave_sum(acc);
+            if (row + r >= r1) continue;
+            if (a.write_logits && lane == r) a.logits[row + r] = v;
+            if (v != v) {
+                nan = true;
+            } else if (besti == 0xFFFFFFFFu || v > best) {  // rows are visited in increasing order
+                best = v;
+                besti = uint32_t(row + r);
+            }
+        }
+    };
+    for (int row = r0 + 4 * w; row < r1; row += 8 * kWaves) {
+        const bool second = row + 4 * kWaves < r1;
+        if (second) load4(rb4, row + 4 * kWaves);
+        proc(ra, row);
+        if (row + 8 * kWaves < r1) load4(ra, row + 8 * kWaves);
+        if (second) proc(rb4, row + 4 * kWaves);
+    }
+    if (lane == 0) {
+        lmv[w] = best;
+        lmi[w] = nan ? 0xFFFFFFFEu : besti;
+    }
+    lds_barrier();
+    uint64_t* lmp = a.xch + kHdrEntries + size_t(a.layers) * X.per_layer;
+    if (t == 0) {
+        float bv = 0.f;
+        uint32_t ix = 0xFFFFFFFFu;
+        bool bn = false;
+        for (int i = 0; i < kWaves; ++i) {
+            if (lmi[i] == 0xFFFFFFFEu)
+                bn = true;
+            else if (lmi[i] != 0xFFFFFFFFu && (ix == 0xFFFFFFFFu || lmv[i] > bv || (lmv[i] == bv && lmi[i] < ix))) {
+                bv = lmv[i];
+                ix = lmi[i];
+            }
+        }
+        xstore(lmp + 2 * b, bv, tag);
+        xstore(lmp + 2 * b + 1, __uint_as_float(bn ? 0xFFFFFFFEu : ix), tag);
+    }
+    if (b != 0) return;
+
+    // workgroup 0: the lowest index of the maximum over the workgroups' pairs (0xFFFFFFFF when a logit is NaN)
+    gather<1>([&](int i) { return lmp + i; }, 2 * G, tag, vec, hdr, 8, s_fail);
+    if (s_fail) return;
+    float bv = 0.f;
+    uint32_t bi = 0xFFFFFFFFu;
+    bool bn = false;
+    for (int i = t; i < G; i += kThreads) {
+        const float v = vec[2 * i];
+        const uint32_t j = __float_as_uint(vec[2 * i + 1]);
+        if (j == 0xFFFFFFFEu)
+            bn = true;
+        else if (j != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || v > bv || (v == bv && j < bi))) {
+            bv = v;
+            bi = j;
+        }
+    }
+    lds_barrier();  // vec is reused for the tree below
+    float* sv = vec;
+    uint32_t* si = reinterpret_cast<uint32_t*>(vec + kThreads);
+    sv[t] = bv;
+    si[t] = bi;
+    if (t == 0) s_fail = 0;
+    lds_barrier();
+    if (bn) s_fail = 2;  // every writer stores the same value
+    for (int h = kThreads / 2; h > 0; h >>= 1) {
+        if (t < h) {
+            const float ov = sv[t + h];
+            const uint32_t oi = si[t + h];
+            if (oi != 0xFFFFFFFFu && (si[t] == 0xFFFFFFFFu || ov > sv[t] || (ov == sv[t] && oi < si[t]))) {
+                sv[t] = ov;
+                si[t] = oi;
+            }
+        }
+        lds_barrier();
+    }
+    if (t == 0) {
+        const uint32_t nid = s_fail == 2 ? 0xFFFFFFFFu : si[0];
+        if (step < uint32_t(a.max_steps)) a.out_ids[step] = nid;
+        a.state[1] = nid;
+        a.state[0] = pos + 1u;
+        a.state[2] = step + 1u;
+        __hip_atomic_store(hdr, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // the next launch's epoch
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- launcher (catalog id 38)
+// fields: embed, final_norm, in_norm, qkv, q_norm, k_norm, o_proj, post_norm, gate_up, down, k_cache, v_cache, cos,
+// sin, logits, state, out_ids, exchange, layers, hidden, q_heads, kv_heads, inter, vocab, max_pos, max_steps,
+// write_logits, eps, scale, blocks
+void launch_decode_persistent(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    const uint32_t* w = pd.words.data();
+    auto f32 = [](uint32_t u) {
+        float f;
+        std::memcpy(&f, &u, 4);
+        return f;
+    };
+    PArgs a;
+    a.embed = (const uint16_t*)p[0];
+    a.final_norm = (const uint16_t*)p[1];
+    a.in_norm = (const uint16_t*)p[2];
+    a.qkv = (const uint16_t*)p[3];
+    a.q_norm = (const uint16_t*)p[4];
+    a.k_norm = (const uint16_t*)p[5];
+    a.o_proj = (const uint16_t*)p[6];
+    a.post_norm = (const uint16_t*)p[7];
+    a.gate_up = (const uint16_t*)p[8];
+    a.down = (const uint16_t*)p[9];
+    a.kc = (uint16_t*)p[10];
+    a.vc = (uint16_t*)p[11];
+    a.cos_t = (const float*)p[12];
+    a.sin_t = (const float*)p[13];
+    a.logits = (float*)p[14];
+    a.state = (uint32_t*)p[15];
+    a.out_ids = (uint32_t*)p[16];
+    a.xch = (uint64_t*)p[17];
+    a.layers = int(w[19]);
+    a.hidden = int(w[20]);
+    a.qh = int(w[21]);
+    a.kvh = int(w[22]);
+    a.inter = int(w[23]);
+    a.vocab = int(w[24]);
+    a.max_pos = int(w[25]);
+    a.max_steps = int(w[26]);
+    a.write_logits = int(w[27]);
+    a.eps = f32(w[28]);
+    a.scale_log2 = f32(w[29]) * 1.4426950408889634f;
+    auto kern = k_decode_persist<kNCH, kRA, kNCC, kUD, kNCE, kKS>;
+    // every workgroup must be resident at once (they wait for each other): at least one per CU, G <= CUs
+    static int occupancy = -1;
+    if (occupancy < 0) hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occupancy, kern, kThreads, 0), "occupancy");
+    int dev = 0, cus = 0;
+    hip_check(hipGetDevice(&dev), "device");
+    hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "attribute");
+    if (occupancy < 1 || int64_t(pd.physical.x) > int64_t(cus) * occupancy)
+        throw HipError("decode_step_persistent: the grid does not fit on the device at once");
+    hipLaunchKernelGGL(kern, dim3(pd.physical.x), dim3(kThreads), 0, s, a);
+}
+
+}  // namespace lrm

@@ -1,11 +1,14 @@
 // The Qwen3 executor (see qwen_exec.hpp).
 #include "qwen_exec.hpp"
 
+#include "persist.hpp"
+
 #include <omp.h>
 #include <quadmath.h>
 
 #include <cmath>
 #include <cstdarg>
+#include <cstdlib>
 #include <cstring>
 
 namespace lrm {
@@ -203,10 +206,44 @@ void QwenExec::plan() {
     const uint32_t H = c.hidden, QC = c.heads * c.head_dim, KC = c.kv_heads * c.head_dim, I = c.intermediate,
                    V = c.vocab, MT = c.max_tokens, MP = c.max_pos, HD = c.head_dim;
     const bool fast = c.mode == 1;
+    const uint32_t L = uint32_t(c.layers), KVH = uint32_t(c.kv_heads), N1 = QC + 2 * KC;
+    // The one-launch decode step (one sequence) reads every layer through layer-stacked tensors, one per kind; the
+    // per-layer names are views of them. Each stack must fit one heap page.
+    if (fast && c.batch == 1) {
+        const char* env = std::getenv("LRM_HIP_DECODE");
+        const bool want = !(env && std::string(env) == "kernels");
+        const int G = 256;
+        const persist::Shape sh{c.hidden, c.heads, c.kv_heads, c.head_dim, c.intermediate, c.max_pos, G};
+        auto fits = [](uint64_t elems) { return elems * 2 <= kMaxPageBytes; };
+        persist_ = want && dev_.info().compute_units >= G && !persist::unsupported(sh) && fits(uint64_t(L) * N1 * H) &&
+                   fits(uint64_t(L) * 2 * I * H) && fits(uint64_t(L) * H * QC) && fits(uint64_t(L) * H * I) &&
+                   fits(uint64_t(L) * KVH * MP * HD);
+        persist_blocks_ = G;
+    }
     // pass one: placements (HeapLayout.fs:433-525); weights first, in contract arena order
     add("model.embed_tokens.weight", Weights, BF16, {V, H}, ReadOnly);
     add("model.norm.weight", Weights, BF16, {H}, ReadOnly);
-    for (int i = 0; i < c.layers; ++i) {
+    if (persist_) {
+        add("stack.input_layernorm", Weights, BF16, {L, H}, ReadOnly);
+        add("stack.qkv_proj", Weights, BF16, {L, N1, H}, ReadOnly);
+        add("stack.o_proj", Weights, BF16, {L, H, QC}, ReadOnly);
+        add("stack.q_norm", Weights, BF16, {L, HD}, ReadOnly);
+        add("stack.k_norm", Weights, BF16, {L, HD}, ReadOnly);
+        add("stack.post_attention_layernorm", Weights, BF16, {L, H}, ReadOnly);
+        add("stack.gate_up_proj", Weights, BF16, {L, 2 * I, H}, ReadOnly);
+        add("stack.down_proj", Weights, BF16, {L, H, I}, ReadOnly);
+        for (uint32_t i = 0; i < L; ++i) {
+            add_view(lname(int(i), kLayerWeights[0]), "stack.input_layernorm", {H}, uint64_t(i) * H);
+            add_view("L" + std::to_string(i) + ".qkv_proj", "stack.qkv_proj", {N1, H}, uint64_t(i) * N1 * H);
+            add_view(lname(int(i), kLayerWeights[4]), "stack.o_proj", {H, QC}, uint64_t(i) * H * QC);
+            add_view(lname(int(i), kLayerWeights[5]), "stack.q_norm", {HD}, uint64_t(i) * HD);
+            add_view(lname(int(i), kLayerWeights[6]), "stack.k_norm", {HD}, uint64_t(i) * HD);
+            add_view(lname(int(i), kLayerWeights[7]), "stack.post_attention_layernorm", {H}, uint64_t(i) * H);
+            add_view("L" + std::to_string(i) + ".gate_up_proj", "stack.gate_up_proj", {2 * I, H}, uint64_t(i) * 2 * I * H);
+            add_view(lname(int(i), kLayerWeights[10]), "stack.down_proj", {H, I}, uint64_t(i) * H * I);
+        }
+    }
+    for (int i = 0; i < c.layers && !persist_; ++i) {
         add(lname(i, kLayerWeights[0]), Weights, BF16, {H}, ReadOnly);
         if (fast) {
             add("L" + std::to_string(i) + ".qkv_proj", Weights, BF16, {QC + 2 * KC, H}, ReadOnly);
@@ -244,9 +281,16 @@ void QwenExec::plan() {
     }
     add("rope.cos", Rope, F32, {MP, HD / 2}, ReadOnly);
     add("rope.sin", Rope, F32, {MP, HD / 2}, ReadOnly);
+    if (persist_) {
+        add("stack.k_cache", KvCache, F16, {L, KVH, MP, HD});
+        add("stack.v_cache", KvCache, F16, {L, KVH, HD, MP});
+    }
     for (int i = 0; i < c.layers; ++i) {
         std::string p = "L" + std::to_string(i);
-        if (fast) {  // sequence b's heads follow sequence b - 1's
+        if (persist_) {
+            add_view(p + ".k_cache", "stack.k_cache", {KVH, MP, HD}, uint64_t(i) * KVH * MP * HD);
+            add_view(p + ".v_cache", "stack.v_cache", {KVH, HD, MP}, uint64_t(i) * KVH * MP * HD);
+        } else if (fast) {  // sequence b's heads follow sequence b - 1's
             add(p + ".k_cache", KvCache, F16, {uint32_t(c.batch * c.kv_heads), MP, HD});
             add(p + ".v_cache", KvCache, F16, {uint32_t(c.batch * c.kv_heads), HD, MP});
         } else {
@@ -273,6 +317,11 @@ void QwenExec::plan() {
             add("dec.o", Activations, F32, {QC});
             add("dec.a", Activations, F32, {I});
             add("dec.lm_partials", Scratch, F32, {2 * 1024});
+            if (persist_) {
+                const persist::Shape sh{c.hidden, c.heads, c.kv_heads, c.head_dim, c.intermediate, c.max_pos,
+                                        persist_blocks_};
+                add("dec.exchange", Scratch, U32, {uint32_t(2 * persist::exchange_entries(c.layers, sh))});
+            }
         } else {  // skinny MFMA GEMMs on the fp16 copies
             add("dec.h16", Activations, F16, {B, H});
             add("dec.o16", Activations, F16, {B, QC});
@@ -330,6 +379,10 @@ void QwenExec::plan() {
     table_->seal();
     dev_.create_heap(layout);
     dev_.write_table(table_->image().data(), kTableBytes);
+    if (persist_) {  // epoch 0, no abort, every entry untagged
+        std::vector<uint8_t> zero(dev_.table().row(token("dec.exchange")).extent_bytes(), 0);
+        upload_tensor("dec.exchange", zero.data(), zero.size());
+    }
     for (int i = 0; i < c.layers; ++i)
         for (int k = 0; k < 11; ++k) weight_names_.push_back(lname(i, kLayerWeights[k]));
     weight_names_.push_back("model.embed_tokens.weight");
@@ -363,7 +416,7 @@ void QwenExec::set_weight(const std::string& name, const uint16_t* data, uint64_
     uint64_t n = 1;
     for (uint32_t d : tt.dims) n *= d;
     if (tt.dtype != BF16 || n != elems) arg_fail("weight %s holds %llu bf16 elements, not %llu", name.c_str(), (unsigned long long)n, (unsigned long long)elems);
-    const std::string& base = tt.view_of.empty() ? name : tt.view_of;
+    const std::string base = f16_copy_.count(name) ? name : tt.view_of;  // the tensor with the fp16 copy, if any
     if (f16_copy_.count(base)) {
         // the fp16 copy must hold the same values: |w| >= 65536 has no fp16 counterpart
         for (uint64_t i = 0; i < elems; ++i) {
@@ -625,6 +678,17 @@ void QwenExec::record_decode_fast() {
         decode_list_ = l;
         return;
     }
+    if (persist_) {
+        dispatch(l, "decode_step_persistent",
+                 {tk("model.embed_tokens.weight"), tk("model.norm.weight"), tk("stack.input_layernorm"),
+                  tk("stack.qkv_proj"), tk("stack.q_norm"), tk("stack.k_norm"), tk("stack.o_proj"),
+                  tk("stack.post_attention_layernorm"), tk("stack.gate_up_proj"), tk("stack.down_proj"),
+                  tk("stack.k_cache"), tk("stack.v_cache"), tk("rope.cos"), tk("rope.sin"), tk("logits"), tk("dec.state"),
+                  tk("dec.out_ids"), tk("dec.exchange"), uint32_t(c.layers), H, uint32_t(c.heads), uint32_t(c.kv_heads),
+                  I, V, MP, MP, 1, eps, scale, uint32_t(persist_blocks_)});
+        decode_list_ = l;
+        return;
+    }
     dispatch(l, "embed_dec", {tk("model.embed_tokens.weight"), tk("dec.state"), tk("dec.x"), H, V, 1});
     for (int i = 0; i < c.layers; ++i) {
         const std::string p = "L" + std::to_string(i) + ".";
@@ -695,6 +759,10 @@ void QwenExec::set_decode_state(const int32_t* ids, const int32_t* pos) {
         st[size_t(B + b)] = uint32_t(ids[b]);
     }
     upload_tensor("dec.state", st.data(), st.size() * 4);
+    if (persist_) {  // clear an abort left by an earlier step
+        const uint32_t clear[2] = {0, 0};
+        upload_tensor("dec.exchange", clear, sizeof clear, 4);
+    }
 }
 
 void QwenExec::run_decode_steps(int steps) {
@@ -720,6 +788,13 @@ void QwenExec::run_decode_steps(int steps) {
     last_ms_ = ms;
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    if (persist_) {  // a workgroup that waited past its bound aborted the step (and every later one)
+        uint32_t hdr[3];
+        download_tensor("dec.exchange", hdr, sizeof hdr);
+        if (hdr[1])
+            throw std::runtime_error("decode_step_persistent: a workgroup waited past its bound at stage " +
+                                     std::to_string(hdr[2]) + "; the decode state did not advance from there");
+    }
 }
 
 void QwenExec::read_decode_ids(int32_t* out, int count) {

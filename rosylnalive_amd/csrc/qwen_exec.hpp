@@ -74,6 +74,10 @@ class QwenExec {
     void run_decode_steps(int steps);  // Fast mode: replays the recorded decode step `steps` times (state on device)
     void set_decode_state(const int32_t* ids, const int32_t* pos);
     void read_decode_ids(int32_t* out, int count);
+    // Fast mode, one sequence: true when the decode step is the single persistent launch (decode_step_persistent),
+    // false when it is the recorded list of per-stage kernels. The persistent step is used when the device has at least
+    // 256 CUs, the kernel covers the shape and LRM_HIP_DECODE is not "kernels" at construction.
+    bool persistent_decode() const { return persist_; }
 
   private:
     void plan();
@@ -107,6 +111,8 @@ class QwenExec {
     int last_t_ = 0;
     double last_ms_ = 0;
     CommandList* decode_list_ = nullptr;
+    bool persist_ = false;    // the decode step is decode_step_persistent (layer-stacked weights and caches)
+    int persist_blocks_ = 0;  // its workgroups
     std::map<std::string, std::string> f16_copy_;  // bf16 matrix -> its fp16 copy (Fast mode)
     std::set<std::string> f16_dirty_;
     void add(const std::string& name, uint32_t arena, uint32_t dtype, std::vector<uint32_t> dims, uint32_t flags = 0);

@@ -237,6 +237,11 @@ class QwenModel:
     def last_ms(self) -> float:
         return lib().lrm_qwen_last_ms(self._h)
 
+    def persistent_decode(self) -> bool:
+        """True when decode steps run as the single persistent launch (decode_step_persistent); set
+        LRM_HIP_DECODE=kernels before construction for the per-stage kernel list."""
+        return lib().lrm_qwen_persistent_decode(self._h) == 1
+
     def token(self, name: str) -> int:
         t = C.c_uint32()
         check(lib().lrm_qwen_token(self._h, name.encode(), C.byref(t)))

@@ -234,3 +234,85 @@ def test_fast_batched_decode_matches_oracle_per_sequence():
     finally:
         m.close()
         b_.close()
+
+
+# ---------------------------------------------------------------- the persistent decode step
+
+def _fast_model(cfg, w, kernels: bool, max_tokens: int = 64):
+    """A fast-mode model whose one-sequence decode step is the persistent launch (kernels=False) or the recorded
+    per-stage kernel list (kernels=True, LRM_HIP_DECODE=kernels at construction)."""
+    import os
+    old = os.environ.get("LRM_HIP_DECODE")
+    if kernels:
+        os.environ["LRM_HIP_DECODE"] = "kernels"
+    else:
+        os.environ.pop("LRM_HIP_DECODE", None)
+    try:
+        m = QwenModel(HipBackend(0), cfg, mode="fast", max_tokens=max_tokens)
+    finally:
+        if old is None:
+            os.environ.pop("LRM_HIP_DECODE", None)
+        else:
+            os.environ["LRM_HIP_DECODE"] = old
+    m.load_weights(w)
+    return m
+
+
+def test_fast_decode_runs_the_persistent_step(fast_setup):
+    """The Qwen3-0.6B layer shape on an MI355X (256 CUs) decodes through decode_step_persistent."""
+    cfg, w, orc, m = fast_setup
+    assert m.persistent_decode()
+
+
+def test_persistent_decode_step_matches_kernel_list():
+    """decode_step_persistent against the per-stage kernel list on the same weights and caches: teacher-forced steps
+    at short context (one split) and over random caches at positions whose splits take 1, 2 and 3 chunks of 64 keys,
+    then 20 greedy steps. Layer 0's q|k|v projections and appended cache rows are the same bits (same per-lane
+    arithmetic); after it the residual rows differ by the order of a few partial sums, and so do the logits."""
+    cfg = reduced_0_6b(layers=2, max_pos=4352)
+    w = synthetic_weights(cfg, seed=11)
+    mp = _fast_model(cfg, w, kernels=False)
+    mk = _fast_model(cfg, w, kernels=True)
+    try:
+        assert mp.persistent_decode() and not mk.persistent_decode()
+        worst = 0.0
+
+        def step(tok, pos):
+            nonlocal worst
+            lg = []
+            for m in (mp, mk):
+                m.decode_set(int(tok), pos)
+                m.decode_run(1)
+                lg.append(m.read_logits(1))
+            err = metrics.max_abs(lg[0], lg[1])
+            worst = max(worst, err)
+            assert err <= 1e-3, (pos, err)
+            assert np.all(metrics.top1_flip_gaps(lg[0], lg[1]) <= 2 * err + 1e-6), pos
+            assert int(mp.decode_ids(1)[0]) == int(np.argmax(lg[0][0]))
+            for layer in range(cfg.layers):
+                for which in ("k", "v"):
+                    a = mp.read_cache(layer, which, pos, 1)
+                    b = mk.read_cache(layer, which, pos, 1)
+                    if layer == 0:  # the same input row: the same bits
+                        assert np.array_equal(a, b), (pos, layer, which)
+                    else:  # the residual row entering the layer differs in the last bits
+                        assert np.max(np.abs(a - b)) <= 1e-2 * max(1.0, float(np.max(np.abs(b)))), (pos, layer, which)
+
+        prompt = synthetic_ids(11, "persist/prompt", 40, cfg.vocab)
+        cont = synthetic_ids(11, "persist/cont", 6, cfg.vocab)
+        for m in (mp, mk):
+            m.forward(prompt, 0, logits_rows=1)
+        for i, tok in enumerate(cont):
+            step(tok, prompt.size + i)
+        for m in (mp, mk):
+            m.fill_cache_random(5, 4320)
+        toks = synthetic_ids(11, "persist/long", 5, cfg.vocab)
+        for tok, pos in zip(toks, (63, 2047, 2048, 3000, 4319)):
+            step(tok, pos)
+        print(f"persistent vs kernel-list decode: worst logits max-abs {worst:.3g}", flush=True)
+        g = [m.greedy(prompt, 20) for m in (mp, mk)]
+        assert g[0].tolist() == g[1].tolist(), g
+    finally:
+        for m in (mp, mk):
+            m.close()
+            m.backend.close()
