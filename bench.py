@@ -2,13 +2,14 @@
 
 Headline (value): batch-1 greedy decode tok/s of a Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads,
 head_dim 128, SwiGLU 3072, vocab 151936, tied embeddings, random N(0, 0.02) bf16 weights, norm weights 1): a 128-token
-prompt, then W warmup steps and exactly K timed decode steps (one step = one token: the recorded decode step replayed
-as a HIP graph, position and token in device memory). Defaults K = 256, W = 8: context 136 .. 392.
+prompt, then W warmup steps and exactly K timed decode steps (one step = one token: one launch of the persistent decode
+step, replayed as a HIP graph, position and token in device memory). Defaults K = 256, W = 8: context 136 .. 392.
 
 Also measured in the same run (extra keys, skipped by --no-extras): 512-token prefill with all 512 x 151936 logits,
 2048-token prefill with last-row logits, decode at 4096 context, the isolated GQA prefill attention at T = 2048, and the
-batched decode of 16 sequences of a Qwen3-1.7B-shaped model at 8K context. The roofline is that of the dominant decode
-kernel (the fused gate/up SwiGLU GEMV, timed with HIP events on the device stream). cpu_baseline is the oracle on the
+batched decode of 16 sequences of a Qwen3-1.7B-shaped model at 8K context, and the same decode through the per-stage
+kernel list (LRM_HIP_DECODE=kernels). The roofline is that of the dominant decode kernel (decode_step_persistent, timed
+with HIP events on the device stream). cpu_baseline is the oracle on the
 host cores on a bounded sample of the decode workload (--no-cpu skips it); cpu_configs times the oracle on the other
 workloads (tiny model, attention, 512-token prefill, a sample of the batched decode).
 """
@@ -27,6 +28,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 FP32_PEAK_TFLOPS = 157.3
 GEMV_SWIGLU_TRAFFIC_BYTES = 12675736  # measured HBM bytes per gemv_swiglu_dec launch at the 0.6B shape
+PERSIST_TRAFFIC_BYTES = 1324494977    # measured HBM bytes per decode_step_persistent launch at context 393..424
 CPU_DECODE_STEPS = 128                # the bounded CPU decode sample (about 10 s on 16 host cores)
 
 
@@ -162,8 +164,41 @@ def main():
     log(f"decode: {args.steps} steps in {dev_ms:.2f} ms device ({wall * 1e3:.2f} ms wall): {tok_s:.1f} tok/s, "
         f"{step_bytes / (dev_ms / 1e3) / 1e9:.0f} GB/s algorithmic")
 
-    # ---------------------------------------------------------------- dominant kernel roofline (gate/up SwiGLU GEMV)
+    # ---------------------------------------------------------------- dominant kernel roofline
+    # The decode step is one launch of decode_step_persistent (the whole token: every layer, the lm_head and the
+    # argmax): its duration per launch, from HIP events on the device stream around `reps` launches recorded in one
+    # list, against the algorithmic bytes of each launch (every weight once, the KV cache up to its position, the
+    # appended K/V rows and the logits row).
     tok = model.token
+    persistent = model.persistent_decode()
+    pk = None
+    if persistent:
+        reps = 32
+        pos0 = ctx0 + args.steps
+        model.decode_set(5, pos0)
+        cl = backend.begin()
+        tm = cl.begin_timer("gpu.decode_step_persistent")
+        for _ in range(reps):
+            cl.dispatch("decode_step_persistent", ArgBlock.encode(
+                "decode_step_persistent", embed=tok("model.embed_tokens.weight"), final_norm=tok("model.norm.weight"),
+                in_norm=tok("stack.input_layernorm"), qkv=tok("stack.qkv_proj"), q_norm=tok("stack.q_norm"),
+                k_norm=tok("stack.k_norm"), o_proj=tok("stack.o_proj"),
+                post_norm=tok("stack.post_attention_layernorm"), gate_up=tok("stack.gate_up_proj"),
+                down=tok("stack.down_proj"), k_cache=tok("stack.k_cache"), v_cache=tok("stack.v_cache"),
+                cos=tok("rope.cos"), sin=tok("rope.sin"), logits=tok("logits"), state=tok("dec.state"),
+                out_ids=tok("dec.out_ids"), exchange=tok("dec.exchange"), layers=L, hidden=H, q_heads=QH,
+                kv_heads=KVH, inter=I, vocab=V, max_pos=cfg.max_pos, max_steps=cfg.max_pos, write_logits=1,
+                eps=cfg.eps, scale=float(np.float32(HD ** -0.5)), blocks=256))
+        cl.end_timer(tm)
+        comp = backend.wait(backend.submit(cl))
+        cl.release()
+        p_us = comp.timers[0].duration_ns / 1e3 / reps
+        p_bytes = sum(weight_bytes + kv_bytes(pos0 + r + 1) + 2 * L * KVH * HD * 2 + V * 4 for r in range(reps)) / reps
+        pk = {"us": p_us, "bytes": p_bytes, "gbs": p_bytes / (p_us * 1e-6) / 1e9}
+        log(f"decode_step_persistent: {p_us:.2f} us per launch at context {pos0 + 1}..{pos0 + reps}, "
+            f"{pk['gbs']:.0f} GB/s ({pk['gbs'] / HBM_PEAK_GBS:.1%} of HBM peak)")
+
+    # the fused gate/up SwiGLU GEMV of the per-stage decode list (the dominant kernel of that list)
     reps = 4
     cl = backend.begin()
     tm = cl.begin_timer("gpu.gemv_swiglu_dec")
@@ -208,19 +243,35 @@ def main():
             "layers": L, "hidden": H, "heads": f"{QH}/{KVH}", "head_dim": HD, "intermediate": I, "vocab": V,
             "batch": 1,
         },
-        "roofline": {
+        "roofline": ({
+            "bound": "hbm",
+            "kernel": "decode_step_persistent",
+            "achieved": round(pk["gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(pk["gbs"] / HBM_PEAK_GBS, 4),
+            # HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the same counters on the 8 MiB
+            # copy below (profiles/decode_persistent_traffic_qwen3_0.6b.md)
+            "traffic": PERSIST_TRAFFIC_BYTES,
+            "bytes_per_launch": int(pk["bytes"]),
+            "us_per_launch": round(pk["us"], 3),
+        } if persistent else {
             "bound": "hbm",
             "kernel": "gemv_swiglu_dec",
             "achieved": round(k_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(k_gbs / HBM_PEAK_GBS, 4),
-            # HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the same counters on the 8 MiB copy
-            # above (profiles/decode_gemv_traffic_qwen3_0.6b.md)
             "traffic": GEMV_SWIGLU_TRAFFIC_BYTES,
             "bytes_per_launch": k_bytes,
             "us_per_launch": round(k_us, 3),
-        },
+        }),
+        "decode_path": "decode_step_persistent (one launch per token)" if persistent else
+                       "per-stage kernel list (171 launches per token, one HIP graph)",
+        "gemv_swiglu_dec": {"us_per_launch": round(k_us, 3), "gbs": round(k_gbs, 1),
+                            "frac": round(k_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": k_bytes,
+                            # profiles/decode_gemv_traffic_qwen3_0.6b.md
+                            "traffic": GEMV_SWIGLU_TRAFFIC_BYTES},
         "decode_step_roofline": {
             "bound": "hbm",
             "achieved": round(step_bytes / (dev_ms / 1e3) / 1e9, 1),
@@ -281,6 +332,26 @@ def main():
                             "hbm_frac": round(b4 / (d_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                             "bytes_per_token": int(b4 / 64)}
         log("decode 4k:", out["decode_4k"])
+
+        # the same decode workload through the per-stage kernel list (171 launches per token in one HIP graph)
+        if persistent:
+            os.environ["LRM_HIP_DECODE"] = "kernels"
+            be_k = HipBackend(0)
+            m_k = QwenModel(be_k, cfg, mode="fast", max_tokens=256)
+            os.environ.pop("LRM_HIP_DECODE", None)
+            m_k.load_weights(weights)
+            _, f_k = m_k.forward(prompt, 0, logits_rows=1)
+            m_k.decode_set(int(f_k), 128)
+            if args.warmup:
+                m_k.decode_run(args.warmup)
+            m_k.decode_run(args.steps)
+            k_ms = m_k.last_ms()
+            out["decode_kernel_list"] = {"tok_s": round(args.steps / (k_ms / 1e3), 1),
+                                         "ms_per_token": round(k_ms / args.steps, 4),
+                                         "workload": "the headline workload, LRM_HIP_DECODE=kernels"}
+            log("decode through the kernel list:", out["decode_kernel_list"])
+            m_k.close()
+            be_k.close()
 
         # batched decode: Qwen3-1.7B shape, 16 sequences whose caches hold 8192 positions of bf16-valued N(0, 1)
         # (stored fp16), 2 warmup + 64 timed steps of all 16 sequences
