@@ -54,7 +54,7 @@ using namespace persist;
 
 namespace {
 
-constexpr long long kWaitTicks = 20000000;  // 0.2 s of the 100 MHz constant clock
+constexpr long long kWaitTicks = 20000000;  // 0.2 s of the 100 MHz constant clock: the default bound of a wait
 
 struct PArgs {
     const uint16_t* embed;       // [V, H] bf16; also the tied lm_head
@@ -109,7 +109,8 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_c
 // the barrier that ends the wait. `fail` must stay an LDS access: a generic (flat) read would also wait for every
 // global load in flight, the prefetched weights included.
 template <int E, typename F>
-__device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, uint32_t* hdr, int stage, int& fail) {
+__device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, uint32_t* hdr, int stage, int& fail,
+                                       long long limit) {
     const int t = threadIdx.x;
     bool pend[E];
 #pragma unroll
@@ -131,7 +132,7 @@ __device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, u
         if (!any) break;
         if (it == 0) {
             start = wall_clock64();
-        } else if ((it & 15) == 0 && (word_load(hdr + 1) != 0u || wall_clock64() - start > kWaitTicks)) {
+        } else if (wall_clock64() - start > limit || ((it & 15) == 0 && word_load(hdr + 1) != 0u)) {
             abort_step(hdr, stage);
             fail = 1;
             break;
@@ -208,6 +209,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     const uint32_t pos = word_load(a.state), id = word_load(a.state + 1), step = word_load(a.state + 2);
     const uint32_t tag = word_load(hdr) + 1u;
     if (pos >= uint32_t(a.max_pos) || word_load(hdr + 1) != 0u) return;  // the same words for every workgroup
+    const uint32_t wait_word = word_load(hdr + 3);  // the bound of every wait, in constant-clock ticks (0: default)
+    const long long wait_ticks = wait_word ? (long long)wait_word : kWaitTicks;
     if (t == 0) s_fail = 0;
 
     const int H = a.hidden, QC = a.qh * 128, KC = a.kvh * 128, N1 = QC + 2 * KC, I = a.inter, MP = a.max_pos;
@@ -252,7 +255,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         // ---------------------------------------------------------------- A: q|k|v = W_qkv . RMSNorm(x)
         if (l > 0) {
             const uint64_t* src = xl - X.per_layer + X.x2 + rep * H;
-            gather<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, tag, vec, hdr, 1, s_fail);
+            gather<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, tag, vec, hdr, 1, s_fail, wait_ticks);
             if (s_fail) return;
         }
         // this split's first two 64-key chunks of K and V^T: they do not depend on this step, so they load while the
@@ -305,7 +308,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             const uint64_t* src = xl + X.qkv;
             const int qo = 2 * hk * 128, ko = QC + hk * 128, vo = QC + KC + hk * 128;
             gather<1>([&](int i) { return src + (i < 256 ? qo + i : i < 384 ? ko + i - 256 : vo + i - 384); },
-                   has_pos ? 512 : 256, tag, vec, hdr, 2, s_fail);
+                   has_pos ? 512 : 256, tag, vec, hdr, 2, s_fail, wait_ticks);
             if (s_fail) return;
             // per-head RMSNorm (q heads: threads 0-255, the new key: 256-383), then the rotation of (d, d + 64); the
             // split holding pos appends the rotated key and the value to the caches, rounded to fp16
@@ -457,7 +460,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                    const int it = b + G * j, hq = it >> 4, d8 = (it & 15) * 8;
                    return src + size_t(hq * S + sp) * 130 + (k < 2 ? k : d8 + k);
                },
-               items * per_item, tag, vec, hdr, 3, s_fail);
+               items * per_item, tag, vec, hdr, 3, s_fail, wait_ticks);
             if (s_fail) return;
             if (w < items) {
                 const int it = b + G * w, hq = it >> 4, d8 = (it & 15) * 8;
@@ -482,7 +485,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         {
             const uint64_t* src = xl + X.o + rep * QC;
             gather<NCC * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, QC, tag, vec, hdr, 4,
-                             s_fail);
+                             s_fail, wait_ticks);
             if (s_fail) return;
         }
         {
@@ -517,7 +520,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         // ---------------------------------------------------------------- D: a = silu(W_g . h) * (W_u . h)
         {
             const uint64_t* src = xl + X.x1 + rep * H;
-            gather<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, tag, vec, hdr, 5, s_fail);
+            gather<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, tag, vec, hdr, 5, s_fail, wait_ticks);
             if (s_fail) return;
         }
         {
@@ -554,7 +557,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         {
             const uint64_t* src = xl + X.a + rep * I;
             gather<NCE * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, I, tag, vec, hdr, 6,
-                             s_fail);
+                             s_fail, wait_ticks);
             if (s_fail) return;
         }
         {
@@ -593,7 +596,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     for (int c = 0; c < NCH; ++c) nf[c] = ld16(a.final_norm + 512 * c + 8 * lane);
     {
         const uint64_t* src = a.xch + kHdrEntries + size_t(a.layers - 1) * X.per_layer + X.x2 + rep * H;
-        gather<NCH>([&](int i) { return src + i; }, H, tag, vec, hdr, 7, s_fail);
+        gather<NCH>([&](int i) { return src + i; }, H, tag, vec, hdr, 7, s_fail, wait_ticks);
         if (s_fail) return;
     }
     float xv[NCH][8];
@@ -649,7 +652,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     if (b != 0) return;
 
     // workgroup 0: the lowest index of the maximum over the workgroups' pairs (0xFFFFFFFF when a logit is NaN)
-    gather<1>([&](int i) { return lmp + i; }, 2 * G, tag, vec, hdr, 8, s_fail);
+    gather<1>([&](int i) { return lmp + i; }, 2 * G, tag, vec, hdr, 8, s_fail, wait_ticks);
     if (s_fail) return;
     float bv = 0.f;
     uint32_t bi = 0xFFFFFFFFu;

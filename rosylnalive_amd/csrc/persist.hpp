@@ -8,7 +8,9 @@ namespace lrm {
 namespace persist {
 
 constexpr int kWaves = 8, kThreads = 512;
-constexpr int kHdrEntries = 32;  // 256-byte header before the entries: u32 word 0 = launch epoch, 1 = abort, 2 = stage
+// 256-byte header before the entries: u32 word 0 = launch epoch, 1 = abort, 2 = the stage that aborted, 3 = the bound
+// of every wait in 100 MHz constant-clock ticks (0: 0.2 s)
+constexpr int kHdrEntries = 32;
 constexpr int kVecMax = 4096;    // floats of the LDS vector a stage gathers its input into
 // Copies of every vector that all workgroups read (o, x after o_proj, the SwiGLU output, x after down_proj): the
 // workgroups of XCD r (blockIdx % 8 = r, the dispatch order) poll copy r, so no copy is polled by more than 1/8 of the

@@ -6,6 +6,7 @@
 #include <omp.h>
 #include <quadmath.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdlib>
@@ -759,9 +760,19 @@ void QwenExec::set_decode_state(const int32_t* ids, const int32_t* pos) {
         st[size_t(B + b)] = uint32_t(ids[b]);
     }
     upload_tensor("dec.state", st.data(), st.size() * 4);
-    if (persist_) {  // clear an abort left by an earlier step
-        const uint32_t clear[2] = {0, 0};
-        upload_tensor("dec.exchange", clear, sizeof clear, 4);
+    if (persist_) {
+        // clear an abort left by an earlier step, and move to a fresh epoch: entries an aborted step wrote carry the
+        // tag the next launch would otherwise use again
+        // LRM_HIP_PERSIST_WAIT_US bounds each wait of the step's workgroups (default 0.2 s): a tiny bound makes steps
+        // abort, which is how the failure path is tested
+        uint32_t hdr[4];
+        download_tensor("dec.exchange", hdr, sizeof hdr);
+        hdr[0] += 1u;
+        hdr[1] = hdr[2] = 0u;
+        const char* w = std::getenv("LRM_HIP_PERSIST_WAIT_US");
+        const long us = w ? std::strtol(w, nullptr, 10) : 0;
+        hdr[3] = us > 0 ? uint32_t(std::min<long>(us, 40000000L) * 100) : 0u;
+        upload_tensor("dec.exchange", hdr, sizeof hdr);
     }
 }
 

@@ -316,3 +316,28 @@ def test_persistent_decode_step_matches_kernel_list():
         for m in (mp, mk):
             m.close()
             m.backend.close()
+
+
+def test_persistent_decode_aborts_past_its_wait_bound_and_recovers(fast_setup):
+    """The failure path, forced from the host: a 1 us bound on every wait of the persistent step's workgroups
+    (LRM_HIP_PERSIST_WAIT_US, read by decode_set) makes the step abort; every workgroup still ends, decode_run raises,
+    and the position does not advance. decode_set with the default bound clears the abort, and the next step's logits
+    match the oracle."""
+    import os
+    cfg, w, orc, m = fast_setup
+    prompt = synthetic_ids(12, "persist/abort", 30, cfg.vocab)
+    tok = int(synthetic_ids(12, "persist/abort/tok", 1, cfg.vocab)[0])
+    m.forward(prompt, 0, logits_rows=1)
+    os.environ["LRM_HIP_PERSIST_WAIT_US"] = "1"
+    try:
+        m.decode_set(tok, prompt.size)
+        with pytest.raises(Exception, match="waited past its bound"):
+            m.decode_run(1)
+    finally:
+        os.environ.pop("LRM_HIP_PERSIST_WAIT_US", None)
+    m.decode_set(tok, prompt.size)
+    m.decode_run(1)
+    lg = m.read_logits(1)
+    ol = orc.forward(orc.new_cache(), 0, np.concatenate([prompt, [tok]]).astype(np.int32))[-1:]
+    assert metrics.max_abs(lg, ol) <= 2e-2
+    assert int(np.argmax(lg[0])) == int(np.argmax(ol[0])) == int(m.decode_ids(1)[0])
