@@ -13,13 +13,16 @@
 // 1 us between CUs), and every workgroup issues the weight loads of its next stage before it waits, so the weight
 // stream overlaps the hand-off latency.
 //
-// Exchange entries are 8 bytes: (tag << 32) | value bits, written by one agent-scope 64-bit store and read by
-// agent-scope 64-bit loads (both coherent across the XCDs' L2s without cache maintenance), so a consumer polls the
-// data itself: an entry is ready when it carries this launch's tag. The tag is the launch epoch + 1 (header word 0,
-// advanced by workgroup 0 at the end of every step), so entries left by earlier steps never match. Every entry is
-// written once per step; nothing is reset between steps. The vectors every workgroup reads are written in 8 copies,
-// one per XCD, so each copy is polled by 32 workgroups instead of 256 (all of them polling one copy measured 1.7-2.8
-// us per hand-off, the lines of the copy being the bottleneck).
+// Exchange entries carry their own ready mark, so a consumer polls the data itself. 8-byte entries (q|k|v, the
+// attention partials, the lm_head partials): (tag << 32) | value bits, written by one agent-scope 64-bit store and read
+// by agent-scope 64-bit loads (both coherent across the XCDs' L2s without cache maintenance); an entry is ready when
+// it carries this launch's tag, the launch epoch + 1 (header word 0, advanced by workgroup 0 at the end of every step),
+// so entries left by earlier steps never match. The vectors every workgroup reads (o, x after o_proj, the SwiGLU
+// output, x after down_proj) are 4-byte entries, the value with its lowest mantissa bit replaced by the tag's parity
+// (every such entry is written by every step, so the previous step's entries always carry the other parity; after an
+// aborted step the host zeroes the area), and are written in 8 copies, one per XCD, so each copy is polled by 32
+// workgroups instead of 256: halving the bytes and spreading the copies cut the polling traffic that bounds a
+// hand-off (all 256 workgroups polling one copy of 8-byte entries measured 1.7-2.8 us per hand-off).
 //
 // Stages of layer l (G = 256, Qwen3-0.6B: hidden 1024, 16/8 heads, intermediate 3072):
 //   A  q|k|v = W_qkv . RMSNorm(x): 2 rows per wave. Waits for x (all of it: the RMSNorm needs the whole row).
@@ -85,6 +88,11 @@ __device__ __forceinline__ uint64_t xload(const uint64_t* p) {
 __device__ __forceinline__ void xstore(uint64_t* p, float v, uint32_t tag) {
     __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 4-byte entries: the value with its lowest mantissa bit replaced by the launch parity (a change of at most one unit
+// in the last place, which the readers of these vectors see; the writers keep their exact values)
+__device__ __forceinline__ void xstore32(uint32_t* p, float v, uint32_t parity) {
+    __hip_atomic_store(p, (__float_as_uint(v) & ~1u) | parity, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ uint32_t word_load(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -103,30 +111,33 @@ __device__ __forceinline__ void unpack8bf(u32x4 v, float* f) {
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// Block-wide: waits until the entries at idx(i), i < n (n <= E * 512), carry `tag` and writes their values to dst[i]
-// in LDS. Thread t polls entries t, t + 512, ..., re-reading only those not yet ready. When the step is aborted (this
-// wait timed out or another workgroup aborted) it sets `fail` (the workgroup's LDS flag), which the caller reads after
-// the barrier that ends the wait. `fail` must stay an LDS access: a generic (flat) read would also wait for every
-// global load in flight, the prefetched weights included.
-template <int E, typename F>
-__device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, uint32_t* hdr, int stage, int& fail,
-                                       long long limit) {
+// Block-wide: waits until the entries at idx(i), i < n (1 <= n <= E * 512), are ready and writes their values to dst[i]
+// in LDS. Thread t polls entries t, t + 512, ..., re-reading only those not yet ready. When the step is
+// aborted (this wait timed out or another workgroup aborted) it sets `fail` (the workgroup's LDS flag), which the
+// caller reads after the barrier that ends the wait. `fail` must stay an LDS access: a generic (flat) read would also
+// wait for every global load in flight, the prefetched weights included.
+// READY(v) says whether a loaded entry is ready; VALUE(v) gives its value.
+template <int E, typename T, typename F, typename R, typename V>
+__device__ __forceinline__ void gather_entries(F idx, int n, R ready, V value, float* dst, uint32_t* hdr, int stage,
+                                               int& fail, long long limit) {
     const int t = threadIdx.x;
+    if (n <= 0) {
+        lds_barrier();
+        return;
+    }
+    T v[E];
     bool pend[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) pend[e] = t + e * kThreads < n;
     long long start = 0;
     for (int it = 0;; ++it) {
-        uint64_t v[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = pend[e] ? xload(idx(t + e * kThreads)) : 0ull;
+        for (int e = 0; e < E; ++e)
+            if (pend[e]) v[e] = __hip_atomic_load(idx(t + e * kThreads), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         bool any = false;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            if (pend[e] && uint32_t(v[e] >> 32) == tag) {
-                dst[t + e * kThreads] = __uint_as_float(uint32_t(v[e]));
-                pend[e] = false;
-            }
+            pend[e] = pend[e] && !ready(v[e]);
             any |= pend[e];
         }
         if (!any) break;
@@ -139,10 +150,32 @@ __device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, u
         }
         __builtin_amdgcn_s_sleep(1);
     }
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+        if (t + e * kThreads < n) dst[t + e * kThreads] = value(v[e]);
     lds_barrier();
     // Nothing is in flight now (every poll waited for all older loads and stores); saying so lets the compiler's
     // wait counting start from zero after the loop instead of waiting for loads issued later.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+}
+
+// 8-byte entries carrying `tag`
+template <int E, typename F>
+__device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, uint32_t* hdr, int stage, int& fail,
+                                       long long limit) {
+    gather_entries<E, uint64_t>(
+        idx, n, [&](uint64_t v) __attribute__((always_inline)) { return uint32_t(v >> 32) == tag; },
+        [](uint64_t v) __attribute__((always_inline)) { return __uint_as_float(uint32_t(v)); }, dst, hdr, stage, fail,
+        limit);
+}
+
+// 4-byte entries of the launch parity
+template <int E, typename F>
+__device__ __forceinline__ void gather32(F idx, int n, uint32_t parity, float* dst, uint32_t* hdr, int stage,
+                                         int& fail, long long limit) {
+    gather_entries<E, uint32_t>(
+        idx, n, [&](uint32_t v) __attribute__((always_inline)) { return (v & 1u) == parity; },
+        [](uint32_t v) __attribute__((always_inline)) { return __uint_as_float(v); }, dst, hdr, stage, fail, limit);
 }
 
 // This lane's values k = 512 c + 8 lane + e of RMSNorm(vec) (vec in LDS, 512 NCH wide): every wave reads the whole
@@ -208,6 +241,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     uint32_t* hdr = reinterpret_cast<uint32_t*>(a.xch);
     const uint32_t pos = word_load(a.state), id = word_load(a.state + 1), step = word_load(a.state + 2);
     const uint32_t tag = word_load(hdr) + 1u;
+    const uint32_t par = tag & 1u;  // the tag of the 4-byte entries
     if (pos >= uint32_t(a.max_pos) || word_load(hdr + 1) != 0u) return;  // the same words for every workgroup
     const uint32_t wait_word = word_load(hdr + 3);  // the bound of every wait, in constant-clock ticks (0: default)
     const long long wait_ticks = wait_word ? (long long)wait_word : kWaitTicks;
@@ -216,6 +250,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     const int H = a.hidden, QC = a.qh * 128, KC = a.kvh * 128, N1 = QC + 2 * KC, I = a.inter, MP = a.max_pos;
     const int S = G / a.kvh, RB = kWaves / KSX, KS = KSX, PB = I / G;
     const XLayout X(a.qh, a.kvh, H, I, G);
+    uint64_t* const lmp = a.xch + kHdrEntries + size_t(a.layers) * X.per_layer;  // lm_head partials
+    uint32_t* const x32 = reinterpret_cast<uint32_t*>(lmp + 2 * G);           // the 4-byte area
     const int gw = b * kWaves + w, NWv = G * kWaves;
     const int rr = b * RB + w / KS, ks = w % KS;  // stages C and E: this wave's row and its part of the row
     const int rep = b % kReplicas;                // the copy of the shared vectors this workgroup polls
@@ -252,10 +288,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
 
     for (int l = 0; l < a.layers; ++l) {
         uint64_t* xl = a.xch + kHdrEntries + size_t(l) * X.per_layer;
+        uint32_t* xv32 = x32 + size_t(l) * X.per_layer32;
         // ---------------------------------------------------------------- A: q|k|v = W_qkv . RMSNorm(x)
         if (l > 0) {
-            const uint64_t* src = xl - X.per_layer + X.x2 + rep * H;
-            gather<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, tag, vec, hdr, 1, s_fail, wait_ticks);
+            const uint32_t* src = xv32 - X.per_layer32 + X.x2 + rep * H;
+            gather32<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, par, vec, hdr, 1, s_fail,
+                          wait_ticks);
             if (s_fail) return;
         }
         // this split's first two 64-key chunks of K and V^T: they do not depend on this step, so they load while the
@@ -278,6 +316,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             fetch(C0{}, 0);
             fetch(C1{}, 1);
         }
+        // stage C's o_proj weights: this wave's part of row rr
+        u32x4 wc[NCC];
+        {
+            const uint16_t* W = a.o_proj + (size_t(l) * H + rr) * QC + ks * (QC / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCC; ++c) wc[c] = ld16(W + 512 * c);
+        }
         {
             float xv[NCH][8];
             norm_lane<NCH>(vec, na, a.eps, xv);
@@ -288,15 +333,15 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
 #pragma unroll
                 for (int c = 0; c < NCH; ++c) acc = dot8(wa[r][c], xv[c], acc);
                 acc = wave_sum(acc);
-                if (lane == 0 && row < N1) xstore(xl + X.qkv + row, acc, tag);
+                if (lane == 0) red[r * kWaves + w] = acc;
             }
         }
-        // stage C's o_proj weights: this wave's part of row rr
-        u32x4 wc[NCC];
-        {
-            const uint16_t* W = a.o_proj + (size_t(l) * H + rr) * QC + ks * (QC / KS) + 8 * lane;
-#pragma unroll
-            for (int c = 0; c < NCC; ++c) wc[c] = ld16(W + 512 * c);
+        // one wave stores the workgroup's rows (runs of kWaves consecutive rows), so each run is one write of whole
+        // 8-byte entries from one instruction (partial lines written by several waves cost a read-modify-write each)
+        lds_barrier();
+        if (t < RA * kWaves) {
+            const int row = b * kWaves + (t % kWaves) + (t / kWaves) * NWv;
+            if (row < N1) xstore(xl + X.qkv + row, red[t], tag);
         }
 
         // ---------------------------------------------------------------- B: attention over this split
@@ -448,7 +493,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         }
 
         // ---------------------------------------------------------------- B': combine the splits
-        // item it = b + G j: query head it / 16, dims 8 (it % 16) .. + 7; wave j merges the S_used splits, one per lane
+        // item it = b + G j: query head it / 16, dims 8 (it % 16) .. + 7, the S_used splits one per lane
         {
             const int items = (a.qh * 16 - b + G - 1) / G;
             const int per_item = S_used * 10;
@@ -462,39 +507,32 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                },
                items * per_item, tag, vec, hdr, 3, s_fail, wait_ticks);
             if (s_fail) return;
-            if (w < items) {
-                const int it = b + G * w, hq = it >> 4, d8 = (it & 15) * 8;
+            for (int j = 0; j < items; ++j) {  // wave w: dim d8 + w of item j; every wave forms the split weights
+                const int it = b + G * j, hq = it >> 4, d8 = (it & 15) * 8;
                 const bool ok = lane < S_used;
-                const float* v = vec + w * per_item + (ok ? lane : 0) * 10;
+                const float* v = vec + j * per_item + (ok ? lane : 0) * 10;
                 const float m = ok ? v[0] : -INFINITY;
                 const float M = wave_max(m);
                 const float e = ok ? exp2f(m - M) : 0.f;
                 const float L = wave_sum(ok ? v[1] * e : 0.f);
-                float mine = 0.f;  // lane l: dim d8 + l % 8, stored into copy l / 8
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const float sk = wave_sum(ok ? v[2 + k] * e : 0.f);
-                    if ((lane & 7) == k) mine = sk;
-                }
-                xstore(xl + X.o + (lane >> 3) * QC + hq * 128 + d8 + (lane & 7), mine / L, tag);
+                const float od = wave_sum(ok ? v[2 + w] * e : 0.f);
+                if (lane == 0) red[j * kWaves + w] = od / L;
+            }
+            // one wave stores every copy of the workgroup's dims: 8 consecutive dims per copy from one instruction
+            lds_barrier();
+            if (t < 64 * items) {
+                const int j = t / 64, it = b + G * j, hq = it >> 4, d8 = (it & 15) * 8, r = (t & 63) >> 3;
+                xstore32(xv32 + X.o + r * QC + hq * 128 + d8 + (t & 7), red[j * kWaves + (t & 7)], par);
             }
         }
 
         // ---------------------------------------------------------------- C: x += W_o . o
         lds_barrier();  // the combine reads vec
         {
-            const uint64_t* src = xl + X.o + rep * QC;
-            gather<NCC * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, QC, tag, vec, hdr, 4,
+            const uint32_t* src = xv32 + X.o + rep * QC;
+            gather32<NCC * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, QC, par, vec, hdr, 4,
                              s_fail, wait_ticks);
             if (s_fail) return;
-        }
-        {
-            float acc = 0.f;
-            const int kb0 = ks * (QC / KS) + 8 * lane;
-#pragma unroll
-            for (int c = 0; c < NCC; ++c) acc = dot8_lds(wc[c], vec, kb0 + 512 * c, acc);
-            acc = wave_sum(acc);
-            if (lane == 0) red[w] = acc;
         }
         // stage D's gate/up weights: unit u = w UD + j is (row u / NCH of the workgroup's 2 PB, chunk j % NCH); rows
         // 0 .. PB - 1 are gate rows b PB + r, the rest the matching up rows
@@ -507,6 +545,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         }
 #pragma unroll
         for (int c = 0; c < NCH; ++c) nd[c] = ld16(a.post_norm + size_t(l) * H + 512 * c + 8 * lane);
+        {
+            float acc = 0.f;
+            const int kb0 = ks * (QC / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCC; ++c) acc = dot8_lds(wc[c], vec, kb0 + 512 * c, acc);
+            acc = wave_sum(acc);
+            if (lane == 0) red[w] = acc;
+        }
         lds_barrier();
         if (t < RB * kReplicas) {  // thread t: row t / 8 into copy t % 8 (one wave: every read precedes the write)
             const int i = t / kReplicas, r = t % kReplicas;
@@ -514,14 +560,22 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             for (int k = 0; k < KS; ++k) sum += red[i * KS + k];
             const float xn = xown[i] + sum;
             if (r == 0) xown[i] = xn;
-            xstore(xl + X.x1 + r * H + b * RB + i, xn, tag);
+            xstore32(xv32 + X.x1 + r * H + b * RB + i, xn, par);
         }
 
         // ---------------------------------------------------------------- D: a = silu(W_g . h) * (W_u . h)
         {
-            const uint64_t* src = xl + X.x1 + rep * H;
-            gather<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, tag, vec, hdr, 5, s_fail, wait_ticks);
+            const uint32_t* src = xv32 + X.x1 + rep * H;
+            gather32<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, par, vec, hdr, 5, s_fail,
+                          wait_ticks);
             if (s_fail) return;
+        }
+        // stage E's down_proj weights: this wave's part of row rr
+        u32x4 we[NCE];
+        {
+            const uint16_t* W = a.down + (size_t(l) * H + rr) * I + ks * (I / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCE; ++c) we[c] = ld16(W + 512 * c);
         }
         {
             float xv[NCH][8];
@@ -534,13 +588,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 if (lane == 0) red[ri * NCH + c] = acc;
             }
         }
-        // stage E's down_proj weights: this wave's part of row rr
-        u32x4 we[NCE];
-        {
-            const uint16_t* W = a.down + (size_t(l) * H + rr) * I + ks * (I / KS) + 8 * lane;
-#pragma unroll
-            for (int c = 0; c < NCE; ++c) we[c] = ld16(W + 512 * c);
-        }
         lds_barrier();
         if (t < PB * kReplicas) {  // thread t: pair t / 8 into copy t % 8
             const int j = t / kReplicas, r = t % kReplicas;
@@ -550,16 +597,19 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 g += red[j * NCH + c];
                 u += red[(PB + j) * NCH + c];
             }
-            xstore(xl + X.a + r * I + b * PB + j, g / (1.0f + __expf(-g)) * u, tag);
+            xstore32(xv32 + X.a + r * I + b * PB + j, g / (1.0f + __expf(-g)) * u, par);
         }
 
         // ---------------------------------------------------------------- E: x += W_d . a
         {
-            const uint64_t* src = xl + X.a + rep * I;
-            gather<NCE * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, I, tag, vec, hdr, 6,
+            const uint32_t* src = xv32 + X.a + rep * I;
+            gather32<NCE * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, I, par, vec, hdr, 6,
                              s_fail, wait_ticks);
             if (s_fail) return;
         }
+        // the next layer's q|k|v rows load while this stage computes (after the last layer: the last one again, never
+        // used; unconditional, so the compiler's wait counting has one path to follow)
+        issue_a(min(l + 1, a.layers - 1));
         {
             float acc = 0.f;
             const int kb0 = ks * (I / KS) + 8 * lane;
@@ -568,7 +618,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             acc = wave_sum(acc);
             if (lane == 0) red[w] = acc;
         }
-        if (l + 1 < a.layers) issue_a(l + 1);
         lds_barrier();
         if (t < RB * kReplicas) {
             const int i = t / kReplicas, r = t % kReplicas;
@@ -576,7 +625,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             for (int k = 0; k < KS; ++k) sum += red[i * KS + k];
             const float xn = xown[i] + sum;
             if (r == 0) xown[i] = xn;
-            xstore(xl + X.x2 + r * H + b * RB + i, xn, tag);
+            xstore32(xv32 + X.x2 + r * H + b * RB + i, xn, par);
         }
     }
 
@@ -595,8 +644,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) nf[c] = ld16(a.final_norm + 512 * c + 8 * lane);
     {
-        const uint64_t* src = a.xch + kHdrEntries + size_t(a.layers - 1) * X.per_layer + X.x2 + rep * H;
-        gather<NCH>([&](int i) { return src + i; }, H, tag, vec, hdr, 7, s_fail, wait_ticks);
+        const uint32_t* src = x32 + size_t(a.layers - 1) * X.per_layer32 + X.x2 + rep * H;
+        gather32<NCH>([&](int i) { return src + i; }, H, par, vec, hdr, 7, s_fail, wait_ticks);
         if (s_fail) return;
     }
     float xv[NCH][8];
@@ -633,7 +682,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         lmi[w] = nan ? 0xFFFFFFFEu : besti;
     }
     lds_barrier();
-    uint64_t* lmp = a.xch + kHdrEntries + size_t(a.layers) * X.per_layer;
     if (t == 0) {
         float bv = 0.f;
         uint32_t ix = 0xFFFFFFFFu;

@@ -27,11 +27,14 @@ struct Shape {
     int hidden, heads, kv_heads, head_dim, inter, max_pos, blocks;
 };
 
-// Entry offsets (8-byte entries) of one layer's exchange area: the q|k|v projection, the attention partials per
-// (query head, split) as (max, sum, out[128]), then kReplicas copies each (copy r at + r * its length) of the combined
-// attention output, x after o_proj, the SwiGLU output and x after down_proj.
+// The exchange area. 8-byte entries, (tag << 32) | value bits, per layer: the q|k|v projection and the attention
+// partials per (query head, split) as (max, sum, out[128]); then the lm_head partials (value, index) per workgroup.
+// 4-byte entries per layer, value bits with the lowest mantissa bit replaced by the launch parity, kReplicas copies
+// each (copy r at + r * its length): the combined attention output o, x after o_proj, the SwiGLU output, x after
+// down_proj. The 4-byte area follows the 8-byte one.
 struct XLayout {
-    int qkv, part, o, x1, a, x2, per_layer;
+    int qkv, part, per_layer;  // 8-byte entries
+    int o, x1, a, x2, per_layer32;  // 4-byte entries
 #if defined(__HIPCC__)
     __host__ __device__
 #endif
@@ -39,18 +42,25 @@ struct XLayout {
         const int S = blocks / kvh;
         qkv = 0;
         part = (qh + 2 * kvh) * 128;
-        o = part + qh * S * 130;
+        per_layer = part + qh * S * 130;
+        o = 0;
         x1 = o + kReplicas * qh * 128;
         a = x1 + kReplicas * hidden;
         x2 = a + kReplicas * inter;
-        per_layer = x2 + kReplicas * hidden;
+        per_layer32 = x2 + kReplicas * hidden;
     }
 };
 
-// Entries of the whole exchange buffer: header, every layer, the lm_head partials (value, index) per workgroup.
-inline uint64_t exchange_entries(int layers, const Shape& s) {
+// 8-byte entries before the 4-byte area: header, every layer, the lm_head partials.
+inline uint64_t exchange_entries64(int layers, const Shape& s) {
     const XLayout X(s.heads, s.kv_heads, s.hidden, s.inter, s.blocks);
     return uint64_t(kHdrEntries) + uint64_t(layers) * uint64_t(X.per_layer) + 2ull * uint64_t(s.blocks);
+}
+
+// The whole exchange buffer in 8-byte units.
+inline uint64_t exchange_entries(int layers, const Shape& s) {
+    const XLayout X(s.heads, s.kv_heads, s.hidden, s.inter, s.blocks);
+    return exchange_entries64(layers, s) + (uint64_t(layers) * uint64_t(X.per_layer32) + 1) / 2;
 }
 
 // nullptr when the instantiated kernel covers the shape, else the reason it does not.

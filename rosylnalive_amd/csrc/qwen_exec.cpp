@@ -761,14 +761,17 @@ void QwenExec::set_decode_state(const int32_t* ids, const int32_t* pos) {
     }
     upload_tensor("dec.state", st.data(), st.size() * 4);
     if (persist_) {
-        // clear an abort left by an earlier step, and move to a fresh epoch: entries an aborted step wrote carry the
-        // tag the next launch would otherwise use again
-        // LRM_HIP_PERSIST_WAIT_US bounds each wait of the step's workgroups (default 0.2 s): a tiny bound makes steps
-        // abort, which is how the failure path is tested
+        // After an aborted step the exchange entries are in an unknown mix of steps: start over from zeros (epoch 0,
+        // every entry untagged); otherwise the entries of the last step carry its tag, which the next launch's differs
+        // from. LRM_HIP_PERSIST_WAIT_US bounds each wait of the step's workgroups (default 0.2 s): a tiny bound makes
+        // steps abort, which is how the failure path is tested.
         uint32_t hdr[4];
         download_tensor("dec.exchange", hdr, sizeof hdr);
-        hdr[0] += 1u;
-        hdr[1] = hdr[2] = 0u;
+        if (hdr[1]) {
+            std::vector<uint8_t> zero(dev_.table().row(token("dec.exchange")).extent_bytes(), 0);
+            upload_tensor("dec.exchange", zero.data(), zero.size());
+            hdr[0] = hdr[1] = hdr[2] = 0u;
+        }
         const char* w = std::getenv("LRM_HIP_PERSIST_WAIT_US");
         const long us = w ? std::strtol(w, nullptr, 10) : 0;
         hdr[3] = us > 0 ? uint32_t(std::min<long>(us, 40000000L) * 100) : 0u;
