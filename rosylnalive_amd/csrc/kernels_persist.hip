@@ -350,39 +350,34 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             const int grp = t >> 7, d = t & 127;
             const float cs = a.cos_t[size_t(pos) * 64 + (d & 63)], sn = a.sin_t[size_t(pos) * 64 + (d & 63)];
             const float nwt = bf2f(t < 256 ? a.q_norm[l * 128 + d] : a.k_norm[l * 128 + d]);
+            const float nwp = bf2f(t < 256 ? a.q_norm[l * 128 + (d ^ 64)] : a.k_norm[l * 128 + (d ^ 64)]);
             const uint64_t* src = xl + X.qkv;
             const int qo = 2 * hk * 128, ko = QC + hk * 128, vo = QC + KC + hk * 128;
             gather<1>([&](int i) { return src + (i < 256 ? qo + i : i < 384 ? ko + i - 256 : vo + i - 384); },
                    has_pos ? 512 : 256, tag, vec, hdr, 2, s_fail, wait_ticks);
             if (s_fail) return;
-            // per-head RMSNorm (q heads: threads 0-255, the new key: 256-383), then the rotation of (d, d + 64); the
-            // split holding pos appends the rotated key and the value to the caches, rounded to fp16
+            // per-head RMSNorm (q heads: threads 0-255, the new key: 256-383), then the rotation of (d, d + 64): each
+            // thread normalises its partner element d ^ 64 too (the same expression as the partner's own thread, so the
+            // same bits) instead of exchanging it through LDS; the split holding pos appends the rotated key and the
+            // value to the caches, rounded to fp16
             const float val = (t < 256 || has_pos) ? vec[t] : 0.f;
+            const float valp = (t < 256 || has_pos) ? vec[t ^ 64] : 0.f;
             const float sq = wave_sum(val * val);
             if (lane == 0) red[w] = sq;
             lds_barrier();
-            const float nr = nwt * (val * (1.0f / sqrtf((red[2 * grp] + red[2 * grp + 1]) / 128.0f + a.eps)));
-            if (t < 256)
-                qs[grp][d] = nr;
-            else if (t < 384)
-                knew[d] = nr;
-            lds_barrier();
-            float rot = 0.f;
-            if (t < 256)
-                rot = d < 64 ? nr * cs - qs[grp][d + 64] * sn : nr * cs + qs[grp][d - 64] * sn;
-            else if (t < 384)
-                rot = d < 64 ? nr * cs - knew[d + 64] * sn : nr * cs + knew[d - 64] * sn;
-            lds_barrier();
+            const float rn = 1.0f / sqrtf((red[2 * grp] + red[2 * grp + 1]) / 128.0f + a.eps);
+            const float nr = nwt * (val * rn), np = nwp * (valp * rn);
+            const float rot = d < 64 ? nr * cs - np * sn : nr * cs + np * sn;
             if (t < 256) {
                 qs[grp][d] = rot;
-            } else if (has_pos && t < 384) {
+            } else if (t < 384) {
                 const uint16_t kh = f2h(rot);
                 knew[d] = h2f(kh);
-                a.kc[((size_t(l) * a.kvh + hk) * MP + pos) * 128 + d] = kh;
-            } else if (has_pos) {
+                if (has_pos) a.kc[((size_t(l) * a.kvh + hk) * MP + pos) * 128 + d] = kh;
+            } else {
                 const uint16_t vh = f2h(val);
                 vnew[d] = h2f(vh);
-                a.vc[((size_t(l) * a.kvh + hk) * 128 + d) * MP + pos] = vh;
+                if (has_pos) a.vc[((size_t(l) * a.kvh + hk) * 128 + d) * MP + pos] = vh;
             }
             lds_barrier();
             // this thread's query dims and, for the split holding pos, its slices of the new key and value (read
@@ -459,7 +454,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 }
                 o0 = fmaf(o0, alpha_s[0], a0);
                 o1 = fmaf(o1, alpha_s[1], a1);
-                lds_barrier();  // ps and alpha_s are rewritten by the next chunk
+                if constexpr (!tail) lds_barrier();  // ps and alpha_s are rewritten by the next chunk
             };
             using Body = std::false_type;
             using Tail = std::true_type;
