@@ -388,8 +388,84 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         return;
     }
 
-    // SWIGLU and QKV pair column c (wave wn = 0) with column c + 64 (wave wn = 1, same lane and tile index): the
-    // second half goes through LDS to the first.
+    // QKV, q and k heads (head = the column tile: q heads, then k heads, then v heads; head_dim 128 = the tile's
+    // columns): every wave stages its accumulators in LDS as the f32 tile [128 rows][128 dims], the 4-float unit u of row
+    // r at unit u ^ (r % 16) (conflict-free both for these stores and for the row reads below), then thread t takes row
+    // t / 2, dims 32 (t % 2) .. + 31 and their RoPE partners + 64: RMSNorm over the row (the other half is lane t ^ 1),
+    // the rotation, and 16-byte stores of the q row or the K cache row.
+    if constexpr (EPI == EPI_QKV) {
+        const int head = tx;
+        if (head < p.qh + p.kvh) {
+            float* tile = reinterpret_cast<float*>(lds);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < JT; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = wm * 64 + i * 16 + 4 * g + r, col = wn * WN + j * 16 + c16;
+                        tile[row * 128 + (col ^ ((row & 15) << 2))] = acc[i][j][r];
+                    }
+            __syncthreads();
+            const bool is_q = head < p.qh;
+            const int row = t >> 1, hf = t & 1, m = m0 + row;
+            float x[2][32];
+#pragma unroll
+            for (int part = 0; part < 2; ++part)
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int unit = (part * 64 + hf * 32) / 4 + u;
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(tile + row * 128 + 4 * (unit ^ (row & 15)));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) x[part][4 * u + e] = v[e];
+                }
+            float ss = 0.f;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) ss = fmaf(x[1][k], x[1][k], fmaf(x[0][k], x[0][k], ss));
+            ss += dpp_f<0xB1>(ss);  // + the other half of the row (lane t ^ 1)
+            if (m >= p.M) return;
+            const int pos = p.pos0 + m;
+            const float rr = 1.0f / sqrtf(ss / 128.0f + p.eps);
+            const uint16_t* nw = (is_q ? p.qn : p.kn) + hf * 32;
+            const float* cst = p.cos_t + size_t(pos) * 64 + hf * 32;
+            const float* snt = p.sin_t + size_t(pos) * 64 + hf * 32;
+            uint16_t* out = is_q ? p.q_out + size_t(m) * (p.qh * 128) + head * 128
+                                 : p.kc + (size_t(head - p.qh) * p.max_pos + pos) * 128;
+            out += hf * 32;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {  // 8 dims d = 32 hf + 8 u + e and their partners d + 64
+                const u32x4 wl = *reinterpret_cast<const u32x4*>(nw + 8 * u);
+                const u32x4 wh = *reinterpret_cast<const u32x4*>(nw + 64 + 8 * u);
+                const f32x4 c0 = *reinterpret_cast<const f32x4*>(cst + 8 * u);
+                const f32x4 c1 = *reinterpret_cast<const f32x4*>(cst + 8 * u + 4);
+                const f32x4 s0 = *reinterpret_cast<const f32x4*>(snt + 8 * u);
+                const f32x4 s1 = *reinterpret_cast<const f32x4*>(snt + 8 * u + 4);
+                uint32_t lo[4], hi[4];
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    float rl[2], rh[2];
+#pragma unroll
+                    for (int h1 = 0; h1 < 2; ++h1) {
+                        const int e = 2 * e2 + h1, k = 8 * u + e;
+                        const float nl = __uint_as_float(h1 ? (wl[e2] & 0xFFFF0000u) : (wl[e2] << 16));
+                        const float nh = __uint_as_float(h1 ? (wh[e2] & 0xFFFF0000u) : (wh[e2] << 16));
+                        const float a = nl * (x[0][k] * rr), b = nh * (x[1][k] * rr);
+                        const float cs = e < 4 ? c0[e] : c1[e - 4], sn = e < 4 ? s0[e] : s1[e - 4];
+                        rl[h1] = a * cs - b * sn;
+                        rh[h1] = b * cs + a * sn;
+                    }
+                    lo[e2] = uint32_t(f2h(rl[0])) | (uint32_t(f2h(rl[1])) << 16);
+                    hi[e2] = uint32_t(f2h(rh[0])) | (uint32_t(f2h(rh[1])) << 16);
+                }
+                *reinterpret_cast<u32x4*>(out + 8 * u) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+                *reinterpret_cast<u32x4*>(out + 64 + 8 * u) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+            }
+            return;
+        }
+    }
+
+    // SWIGLU and the V heads of QKV pair column c (wave wn = 0) with column c + 64 (wave wn = 1, same lane and tile
+    // index): the second half goes through LDS to the first.
     float* x32 = reinterpret_cast<float*>(lds);  // 2 (wm) x 64 values x 64 lanes = 32 KiB
     if (wn == 1) {
 #pragma unroll
@@ -400,10 +476,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                 for (int r = 0; r < 4; ++r) x32[((wm * 16 + i * 4 + j) * 4 + r) * 64 + lane] = acc[i][j][r];
     }
     __syncthreads();
-    // QKV: head = the column tile (q heads, then k heads, then v heads), head_dim 128 = this tile's columns.
-    const int head = tx;
-    const bool is_q = head < p.qh, is_k = !is_q && head < p.qh + p.kvh;
-    if (wn == 1 && (EPI == EPI_SWIGLU || is_q || is_k)) return;  // V tiles: all four waves store the transpose
+    const int head = tx;  // QKV: a V head (the q and k heads returned above)
+    if (wn == 1 && EPI == EPI_SWIGLU) return;  // V tiles: all four waves store the transpose
     // the partner half of row tile i, read back from LDS
     auto load_hi = [&](int i, float (&hi)[4][4]) {
 #pragma unroll
@@ -435,7 +509,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         return;
     }
 
-    if (!is_q && !is_k) {
+    if (EPI == EPI_QKV) {
         // V: the cache is V^T ([dim][position]), so the tile is transposed through LDS (after the 32 KiB of x32, rows
         // of 128 positions padded to 136) and written as whole 256-byte rows of 16-byte stores, not 2-byte ones
         uint16_t* Vs = lds + 16384;
@@ -474,198 +548,190 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         }
         return;
     }
-    const uint16_t* nw = is_q ? p.qn : p.kn;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float hi[4][4];
-        load_hi(i, hi);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = m0 + wm * 64 + i * 16 + 4 * g + r;  // the same for the 16 lanes of group g
-            float ss = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) ss = fmaf(acc[i][j][r], acc[i][j][r], fmaf(hi[j][r], hi[j][r], ss));
-            ss += __shfl_xor(ss, 1, 64);
-            ss += __shfl_xor(ss, 2, 64);
-            ss += __shfl_xor(ss, 4, 64);
-            ss += __shfl_xor(ss, 8, 64);
-            if (m >= p.M) continue;
-            const int pos = p.pos0 + m;
-            const float rr = 1.0f / sqrtf(ss / 128.0f + p.eps);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = j * 16 + c16;  // 0..63
-                const float a = bf2f(nw[c]) * (acc[i][j][r] * rr);
-                const float b = bf2f(nw[c + 64]) * (hi[j][r] * rr);
-                const float cs = p.cos_t[size_t(pos) * 64 + c], sn = p.sin_t[size_t(pos) * 64 + c];
-                const float lo = a * cs - b * sn, h2 = b * cs + a * sn;
-                uint16_t* out = is_q ? p.q_out + size_t(m) * (p.qh * 128) + head * 128
-                                     : p.kc + (size_t(head - p.qh) * p.max_pos + pos) * 128;
-                out[c] = f2h(lo);
-                out[c + 64] = f2h(h2);
-            }
-        }
-    }
 }
 
 // ================================================================ 16 attention_prefill_f16
-// Causal GQA flash attention, two query heads per KV head. A workgroup takes 32 query rows of both heads of one KV
-// group (64 query columns: wave w owns head 2 kvhead + w / 2, rows (w % 2) * 16 .. + 15, one MFMA column tile) and
-// streams 64-key blocks of K and V^T through LDS, shared by the four waves; the next block's K and V^T are fetched
-// into registers while the current one is multiplied. Blocks are issued longest first, and 32-row tiles give twice
-// as many blocks as CUs at T = 2048, so the causal triangle packs onto the CUs.
-// S^T = K Q^T (A = K rows from LDS, B = Q^T from registers) puts one query per lane column, so the online-softmax
-// statistics stay per lane; P^T is then already in the B-operand layout of O^T = V^T P^T once the key slots of the
-// k-step are ordered {4g .. 4g + 3, 16 + 4g .. 16 + 4g + 3}. V^T is kept in LDS in that order (vt_slot), so each lane
-// reads its A operand as one 16-byte load (two 8-byte loads at a 144-byte row stride run at a third of the rate).
+// Causal GQA flash attention on v_mfma_f32_32x32x16_f16 (32 query columns per wave: half the LDS operand bytes per
+// FLOP of the 16-column form), two query heads per KV head. A workgroup takes 32 query rows of both heads of one KV group: wave w owns head 2 kvhead + w % 2
+// (32 query columns, one MFMA column tile) and key half w / 2 (keys 32 (w / 2) .. + 31) of every 64-key block, so the
+// four waves share each block's K and V^T in LDS (64 KB: two stages, one barrier per block) and each wave runs its own
+// online softmax over its half; the two halves of a head merge through LDS at the end.
+// S^T = K Q^T (A = 32 keys x 16 dims of K from LDS, B = Q^T from registers) puts one query per lane column; lanes
+// l and l + 32 hold the other 16 keys of the same column, so the row statistics take one v_permlane32_swap. The P^T
+// operand of O^T = V^T P^T needs keys 8 h .. 8 h + 7 of a 16-key step in lane half h; a lane holds keys
+// 4 h .. 4 h + 3 and 8 + 4 h .. 8 + 4 h + 3, and one swap of the packed halves with lane l ^ 32 gives the rest, so V^T
+// stays in LDS in its natural key order. LDS rows are padded by 16 bytes (K 272, V^T 144), so the 16 lanes of each
+// read phase hit distinct banks and every operand address is a per-lane base plus an immediate. The softmax keeps a
+// reference maximum per column that moves (rescaling O and the sum) only when a block's maximum exceeds it by more
+// than 8 in the exponent: P stays at most 2^8, and most blocks need no rescale. Blocks are issued longest first for the
+// first half of the grid and shortest first for the second, so the two workgroups of a CU carry about equal causal
+// work.
 constexpr int kAttnRows = 32;
 
-// The LDS column of key k (0..63) in a V^T row: 32-key chunks, inside a chunk keys 4g + j -> 8g + j and
-// 16 + 4g + j -> 8g + 4 + j (g, j < 4).
-__device__ __forceinline__ int vt_slot(int k) {
-    return (k & 32) + 8 * ((k & 15) >> 2) + 4 * ((k >> 4) & 1) + (k & 3);
-}
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                                       uint16_t* y, int T, int past, int qh, int max_pos,
                                                       float scale_log2) {
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[64 * 136];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[128 * 72];
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6, g = lane >> 4, c16 = lane & 15;
-    // Causal balance: the first half of the workgroups (in dispatch order, KV heads fastest) takes the long tiles,
-    // longest first, and the second half the short ones, shortest first, so workgroups L and L + half, which the
-    // dispatcher places in the two slots of one CU when the grid fills the chip once, carry about equal work together.
+    // stage s: K [64 keys][128 dims + 8] at s * kStage, V^T [128 dims][64 keys + 8] at s * kStage + kVtOff
+    constexpr int kKRow = 272, kVRow = 144, kVtOff = 64 * kKRow, kStage = kVtOff + 128 * kVRow;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, c32 = lane & 31, h = lane >> 5;
+    const int cg = w & 1, kh = w >> 1;
     const int ntile = (T + kAttnRows - 1) / kAttnRows, kvh = int(gridDim.y);
     const int L = int(blockIdx.y) * ntile + int(blockIdx.x), j = L / kvh, half = (ntile + 1) / 2;
     const int row0 = (j < half ? ntile - 1 - j : j - half) * kAttnRows;
     const int kvhead = L % kvh;
-    const int head = kvhead * 2 + (w >> 1);
-    const int row = row0 + (w & 1) * 16 + c16;  // this lane's query row
+    const int head = kvhead * 2 + cg;
+    const int row = row0 + c32;  // this lane's query row (its column of S^T and O^T)
     const int QC = qh * 128;
 
-    f16x8 qf[4];
+    // Q^T operand of k-step s (dims 16 s .. 16 s + 15): this lane's dims 16 s + 8 h .. + 7
+    f16x8 qf[8];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (row < T) v = *reinterpret_cast<const uint4*>(q + size_t(row) * QC + head * 128 + ks * 32 + 8 * g);
-        qf[ks] = as_f16x8(v);
+    for (int s = 0; s < 8; ++s) {
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (row < T) v = *reinterpret_cast<const u32x4*>(q + size_t(row) * QC + head * 128 + 16 * s + 8 * h);
+        qf[s] = as_f16x8(v);
     }
     float m_run = -INFINITY, l_run = 0.f;
-    f32x4 o[8];
+    f32x16 o[4];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
 
     const int last_row = min(row0 + kAttnRows - 1, T - 1);
     const int kend = past + last_row + 1;  // keys [0, kend) are visible to some row of the tile; kend <= max_pos
+    const int nkb = (kend + 63) / 64;
     const int qpos = past + row;
-    // this KV head's K rows and V^T rows as buffer resources: per-thread byte offsets stay fixed, the key block's
-    // offset is scalar
     const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kc + size_t(kvhead) * max_pos * 128, max_pos * 256);
     const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc + size_t(kvhead) * 128 * max_pos, max_pos * 256);
-    int koff[4], voff[4];
+    // thread t moves chunks t + 256 i of a block: K row c / 16, dims 8 (c % 16) ..; V^T row (dim) c / 8, keys 8 (c % 8) ..
+    int koff[4], voff[4], kst[4], vst[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int c = t + 256 * i;
-        koff[i] = ((c >> 4) * 128 + (c & 15) * 8) * 2;
-        voff[i] = ((c >> 3) * max_pos + (c & 7) * 8) * 2;
+        const int kr = c >> 4, kq = c & 15, vd = c >> 3, vq = c & 7;
+        koff[i] = (kr * 128 + kq * 8) * 2;
+        voff[i] = (vd * max_pos + vq * 8) * 2;
+        kst[i] = kr * kKRow + 16 * kq;
+        vst[i] = kVtOff + vd * kVRow + 16 * vq;
     }
+    // read offsets of the MFMA operands: K row 32 kh + c32, chunk 2 s + h; V^T row 32 dt + c32, chunk 4 kh + 2 ks + h
+    const int krd = (32 * kh + c32) * kKRow + 16 * h;
+    const int vrd = kVtOff + c32 * kVRow + 16 * (4 * kh + h);
 
     // The loads of a 64-key block are unconditional (kb + 63 < max_pos: kb < kend <= max_pos, both multiples of 64);
-    // keys at or past kend may hold anything. Their scores are masked, so K needs nothing; V is zeroed there after
-    // the load, since a zero weight times a NaN is still a NaN. Two register sets: key block j is loaded into set
-    // j % 2 two iterations before it is multiplied (the loop is unrolled by two so the sets are named statically).
+    // keys at or past kend may hold anything. Their scores are masked, so K needs nothing; V is zeroed there before it
+    // is stored, since a zero weight times a NaN is still a NaN. Two register sets: block j is loaded into set j % 2
+    // two blocks before it is stored (past the last block: the last one again, never stored).
     u32x4 rk[2][4], rv[2][4];
-    auto fetch = [&](auto set, int kb) __attribute__((always_inline)) {
+    auto fetch = [&](auto set, int jb) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value;
-        const int kbl = min(kb, kend - 1) & ~63;  // past the end: re-read the last block (never stored)
+        const int kbl = min(jb, nkb - 1) * 64;
 #pragma unroll
         for (int i = 0; i < 4; ++i) rk[S][i] = __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, koff[i], kbl * 256, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) rv[S][i] = __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, voff[i], kbl * 2, 0);
     };
-    auto block = [&](auto set, int kb) __attribute__((always_inline)) {
+    auto block = [&](auto set, int jb) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value;
-        // store the block (V^T zeroed past kend in LDS, last block only), then queue the block two ahead into the same
-        // set; the masking is not done on the registers, so no branch depends on data still in flight
-        lds_barrier();  // every wave is done with the previous block's K and V^T
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = t + 256 * i;
-            *reinterpret_cast<u32x4*>(Ks + (c >> 4) * 136 + (c & 15) * 8) = rk[S][i];
-            // keys k8 .. k8 + 3 and k8 + 4 .. k8 + 7 land 8 slots apart
-            uint16_t* vd = Vt + (c >> 3) * 72 + vt_slot((c & 7) * 8);
-            *reinterpret_cast<uint2*>(vd) = make_uint2(rv[S][i].x, rv[S][i].y);
-            *reinterpret_cast<uint2*>(vd + 8) = make_uint2(rv[S][i].z, rv[S][i].w);
-        }
-        if (kb + 64 > kend) {  // uniform
+        const int kb = jb * 64;
+        uint8_t* st = lds + S * kStage;
+        // stage S was last read by block jb - 2, which every wave finished before the previous barrier
+        if (kb + 64 > kend) {  // uniform: zero V^T past kend (8 keys per chunk, two per word)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int c = t + 256 * i, k8 = (c & 7) * 8;
+                const int k8 = kb + ((t + 256 * i) & 7) * 8;
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (kb + k8 + e >= kend) Vt[(c >> 3) * 72 + vt_slot(k8 + e)] = 0;
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t lo = k8 + 2 * e < kend ? 0x0000FFFFu : 0u;
+                    const uint32_t hi = k8 + 2 * e + 1 < kend ? 0xFFFF0000u : 0u;
+                    rv[S][i][e] &= lo | hi;
+                }
             }
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *reinterpret_cast<u32x4*>(st + kst[i]) = rk[S][i];
+            *reinterpret_cast<u32x4*>(st + vst[i]) = rv[S][i];
+        }
+        fetch(set, jb + 2);
         lds_barrier();
-        fetch(set, kb + 128);
         __builtin_amdgcn_sched_barrier(0);
 
-        f32x4 s[4];
+        // S^T for this wave's 32 keys (one accumulation chain over the 8 dim steps: the matrix core chains dependent
+        // accumulations; two chains and a final add measured slower)
+        f32x16 sa;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < 16; ++r) sa[r] = 0.f;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
+        for (int s = 0; s < 8; ++s) {
+            const f16x8 a0 = as_f16x8(*reinterpret_cast<const u32x4*>(st + krd + 32 * s));
+            sa = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[s], sa, 0, 0, 0);
+        }
+        float sc[16];
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                const f16x8 a = as_f16x8(*reinterpret_cast<const u32x4*>(Ks + (kt * 16 + c16) * 136 + ks * 32 + 8 * g));
-                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ks], s[kt], 0, 0, 0);
-            }
+        for (int r = 0; r < 16; ++r) sc[r] = sa[r];
 
-        // causal mask, branch-free, only where the key block crosses the diagonal or the tile runs past T (uniform)
+        // causal mask, only where the key block crosses the diagonal or the tile runs past T (uniform).
+        // Register r holds key kb + 32 kh + 8 (r / 4) + 4 h + r % 4.
         const bool need_mask = kb + 63 > past + row0 || row0 + kAttnRows > T;
-        const int lim = row < T ? qpos - kb : -1;  // key offsets in this block above lim are masked
-        // raw scores; the scale is folded into the exponent: p = 2^(s c - m c) with one FMA per score (c > 0, so
-        // the maximum of s c is c times the maximum of s)
+        if (need_mask) {  // a real branch (the empty asm keeps the compiler from running the mask on every block)
+            asm volatile("");
+            const int lim = row < T ? qpos - kb - 32 * kh - 4 * h : -1;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sc[r] = (8 * (r >> 2) + (r & 3) > lim) ? -INFINITY : sc[r];
+        }
         float mloc = -INFINITY;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (need_mask) s[kt][r] = (kt * 16 + 4 * g + r > lim) ? -INFINITY : s[kt][r];
-                mloc = fmaxf(mloc, s[kt][r]);
-            }
-        mloc = cross_rows_max(mloc);
-        const float m_new = fmaxf(m_run, mloc);  // running max of the raw scores
-        const float mc = m_new == -INFINITY ? 0.f : m_new * scale_log2;
-        // the hardware exp2 (results below 2^-126 flush to 0: weights that small are below fp16 P anyway)
-        const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - mc);
-        float lsum = 0.f;
-        float pv[4][4];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                pv[kt][r] = __builtin_amdgcn_exp2f(fmaf(s[kt][r], scale_log2, -mc));
-                lsum += pv[kt][r];
-            }
-        lsum = cross_rows_sum(lsum);
-        l_run = l_run * alpha + lsum;
-        m_run = m_new;
-        if (__any(alpha != 1.0f)) {  // rescale only when some row's maximum moved (wave-uniform branch)
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) o[dt][r] *= alpha;
+        for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sc[r]);
+        {
+            auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+            mloc = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
         }
+        // The reference maximum m_run moves only when this block's maximum exceeds it by more than 8 / c (the scale
+        // c > 0 is folded into the exponent: p = 2^(s c - m c), one FMA per score). A column with no visible key yet
+        // keeps m_run = -inf and gets p = 0.
+        const bool grow = (mloc - m_run) * scale_log2 > 8.0f;  // false for NaN (both -inf)
+        if (__any(grow)) {  // wave-uniform branch
+            // 1 for a column that does not grow (also one with no visible key yet: -inf - -inf would be NaN), 0 for a
+            // column whose first visible keys arrive
+            const float alpha = grow ? __builtin_amdgcn_exp2f((m_run - mloc) * scale_log2) : 1.0f;
+            const float m_new = grow ? mloc : m_run;
+            l_run *= alpha;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const f16x8 bq = as_f16x8(make_uint4(pack2h(pv[2 * kk][0], pv[2 * kk][1]), pack2h(pv[2 * kk][2], pv[2 * kk][3]),
-                                                 pack2h(pv[2 * kk + 1][0], pv[2 * kk + 1][1]),
-                                                 pack2h(pv[2 * kk + 1][2], pv[2 * kk + 1][3])));
+            for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-                const f16x8 a = as_f16x8(*reinterpret_cast<const u32x4*>(Vt + (dt * 16 + c16) * 72 + kk * 32 + 8 * g));
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, o[dt], 0, 0, 0);
+                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+            m_run = m_new;
+        }
+        const float mc = m_run == -INFINITY ? 0.f : m_run * scale_log2;
+        float lsum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], scale_log2, -mc));
+            lsum += sc[r];
+        }
+        {
+            auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum), __float_as_uint(lsum), false, false);
+            lsum = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+        }
+        l_run += lsum;
+        // O^T += V^T P^T over the two 16-key steps of this wave's half
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const uint32_t p0a = pack2h(sc[8 * ks], sc[8 * ks + 1]), p0b = pack2h(sc[8 * ks + 2], sc[8 * ks + 3]);
+            const uint32_t p1a = pack2h(sc[8 * ks + 4], sc[8 * ks + 5]), p1b = pack2h(sc[8 * ks + 6], sc[8 * ks + 7]);
+            // lane half 0 keeps keys 0-3 and takes 4-7 from lane l + 32; half 1 takes 8-11 from l - 32, keeps 12-15
+            const auto xa = __builtin_amdgcn_permlane32_swap(p0a, p1a, false, false);
+            const auto xb = __builtin_amdgcn_permlane32_swap(p0b, p1b, false, false);
+            const f16x8 bq = as_f16x8(u32x4{xa[0], xb[0], xa[1], xb[1]});
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const f16x8 a = as_f16x8(*reinterpret_cast<const u32x4*>(st + vrd + dt * 32 * kVRow + 32 * ks));
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bq, o[dt], 0, 0, 0);
             }
         }
     };
@@ -673,23 +739,47 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
     using A1 = std::integral_constant<int, 1>;
     fetch(A0{}, 0);
     __builtin_amdgcn_sched_barrier(0);  // set 0 issues before set 1, as in the loop, so the first wait can be partial
-    fetch(A1{}, 64);
-    // key blocks in pairs; a block past kend (odd count) is fully masked: P = 0 and V^T zeroed in LDS, so it leaves
-    // the running maximum, sum and output unchanged
-    for (int kb = 0; kb < kend; kb += 128) {
-        block(A0{}, kb);
-        block(A1{}, kb + 64);
+    fetch(A1{}, 1);
+    for (int jb = 0;; jb += 2) {
+        block(A0{}, jb);
+        if (jb + 1 >= nkb) break;
+        block(A1{}, jb + 1);
+        if (jb + 2 >= nkb) break;
     }
-    if (row < T) {
-        const float inv = 1.0f / l_run;
+
+    // merge the key halves: waves 2 and 3 hand (m, l, O^T) to waves 0 and 1 (same head) through LDS
+    lds_barrier();  // every wave is done with both stages
+    float* xo = reinterpret_cast<float*>(lds) + cg * 4224;  // per head: 64 x 64 O words, then m and l per lane
+    if (kh == 1) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                *reinterpret_cast<f32x4*>(xo + ((dt * 4 + r4) * 64 + lane) * 4) =
+                    f32x4{o[dt][4 * r4], o[dt][4 * r4 + 1], o[dt][4 * r4 + 2], o[dt][4 * r4 + 3]};
+        xo[4096 + lane] = m_run;
+        xo[4160 + lane] = l_run;
+    }
+    lds_barrier();
+    if (kh == 0 && row < T) {
+        const float m1 = xo[4096 + lane], l1 = xo[4160 + lane];
+        const float M = fmaxf(m_run, m1);
+        const float Mc = M == -INFINITY ? 0.f : M * scale_log2;
+        const float e0 = __builtin_amdgcn_exp2f(m_run * scale_log2 - Mc), e1 = __builtin_amdgcn_exp2f(m1 * scale_log2 - Mc);
+        const float inv = 1.0f / (l_run * e0 + l1 * e1);
+        const float f0 = e0 * inv, f1 = e1 * inv;
         uint16_t* yr = y + size_t(row) * QC + head * 128;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            uint2 v;
-            v.x = pack2h(o[dt][0] * inv, o[dt][1] * inv);
-            v.y = pack2h(o[dt][2] * inv, o[dt][3] * inv);
-            *reinterpret_cast<uint2*>(yr + dt * 16 + 4 * g) = v;
-        }
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const f32x4 b = *reinterpret_cast<const f32x4*>(xo + ((dt * 4 + r4) * 64 + lane) * 4);
+                uint2 v;
+                v.x = pack2h(o[dt][4 * r4] * f0 + b[0] * f1, o[dt][4 * r4 + 1] * f0 + b[1] * f1);
+                v.y = pack2h(o[dt][4 * r4 + 2] * f0 + b[2] * f1, o[dt][4 * r4 + 3] * f0 + b[3] * f1);
+                // register r of tile dt: dim 32 dt + 8 (r / 4) + 4 h + r % 4
+                *reinterpret_cast<uint2*>(yr + 32 * dt + 8 * r4 + 4 * h) = v;
+            }
     }
 }
 

@@ -112,7 +112,8 @@ __device__ __forceinline__ void unpack8bf(u32x4 v, float* f) {
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // Block-wide: waits until the entries at idx(i), i < n (1 <= n <= E * 512), are ready and writes their values to dst[i]
-// in LDS. Thread t polls entries t, t + 512, ..., re-reading only those not yet ready. When the step is
+// in LDS. Thread t polls entries t, t + 512, ..., re-reading only those not yet ready, back to back (a sleep between
+// polls measured slower: each 64 clocks of it added about 0.02 us per hand-off). When the step is
 // aborted (this wait timed out or another workgroup aborted) it sets `fail` (the workgroup's LDS flag), which the
 // caller reads after the barrier that ends the wait. `fail` must stay an LDS access: a generic (flat) read would also
 // wait for every global load in flight, the prefetched weights included.
@@ -148,7 +149,6 @@ __device__ __forceinline__ void gather_entries(F idx, int n, R ready, V value, f
             fail = 1;
             break;
         }
-        __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
     for (int e = 0; e < E; ++e)

@@ -136,7 +136,7 @@ def _caches(kb, vb, max_pos, fill=0):
     return kc, vc
 
 
-@pytest.mark.parametrize("T,past", [(64, 0), (100, 0), (2048, 0), (77, 300)])
+@pytest.mark.parametrize("T,past", [(64, 0), (100, 0), (2048, 0), (77, 300), (1, 0), (33, 31), (512, 2048)])
 def test_attention_prefill_f16(T, past):
     max_pos = ((past + T + 63) // 64) * 64 + 64
     qb, kb, vb = _qkv_inputs(T, past, max_pos, seed=T + past)
