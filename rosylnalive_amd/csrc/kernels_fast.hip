@@ -85,6 +85,61 @@ __global__ __launch_bounds__(256) void k_rmsnorm_f16_wave(const float* x, const 
     }
 }
 
+// ================================================================ 40 residual_add_norm
+// x[r, :] += p[0][r, :] + p[1][r, :] + ... (the k-split partial products of gemm_residual_split, added in split order),
+// then y[r, :] = f16(widen(w) * (x[r, :] * rr)) exactly as rmsnorm_rows_f16 forms it. One wave per row (cols = 256 NC),
+// four rows per block; the partial rows of two splits are loaded before their adds.
+template <int NC>
+__global__ __launch_bounds__(256) void k_resid_add_norm(float* x, const float* part, const uint16_t* w, uint16_t* y,
+                                                        uint32_t rows, uint32_t cols, uint32_t splits, float eps) {
+    const uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    float4* xr = reinterpret_cast<float4*>(x + size_t(r) * cols) + lane;
+    const float4* pr = reinterpret_cast<const float4*>(part + size_t(r) * cols) + lane;
+    const size_t ps = size_t(rows) * cols / 4;  // float4s from one split's partial to the next
+    const uint2* wr = reinterpret_cast<const uint2*>(w) + lane;
+    float4 v[NC], q[2][NC];
+    uint2 wv[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        v[j] = xr[64 * j];
+        wv[j] = wr[64 * j];
+    }
+    for (uint32_t k = 0; k < splits; k += 2) {  // two splits' rows in flight at a time (splits is 1 or even)
+        const bool two = k + 1 < splits;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            q[0][j] = pr[k * ps + 64 * j];
+            q[1][j] = two ? pr[(k + 1) * ps + 64 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            if (h == 0 || two)
+#pragma unroll
+                for (int j = 0; j < NC; ++j) {
+                    v[j].x += q[h][j].x;
+                    v[j].y += q[h][j].y;
+                    v[j].z += q[h][j].z;
+                    v[j].w += q[h][j].w;
+                }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        xr[64 * j] = v[j];
+        ss = fmaf(v[j].x, v[j].x, fmaf(v[j].y, v[j].y, fmaf(v[j].z, v[j].z, fmaf(v[j].w, v[j].w, ss))));
+    }
+    ss = wave_sum(ss);
+    const float rr = 1.0f / sqrtf(ss / float(cols) + eps);
+    uint2* yr = reinterpret_cast<uint2*>(y + size_t(r) * cols) + lane;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const float w0 = __uint_as_float(wv[j].x << 16), w1 = __uint_as_float(wv[j].x & 0xFFFF0000u);
+        const float w2 = __uint_as_float(wv[j].y << 16), w3 = __uint_as_float(wv[j].y & 0xFFFF0000u);
+        yr[64 * j] = make_uint2(pack2h(w0 * (v[j].x * rr), w1 * (v[j].y * rr)), pack2h(w2 * (v[j].z * rr), w3 * (v[j].w * rr)));
+    }
+}
+
 // ================================================================ GEMM (ids 15, 17, 18, 19)
 // C[m, n] = sum_k A[m, k] W[n, k] on f16 operands, 128 x 128 tiles (128 x 64 for the residual GEMMs of few tiles), k
 // in steps of 64, 4 waves each owning a 64 x 64 quarter as 4 x 4 MFMA tiles. Tiles are loaded from memory straight
@@ -106,7 +161,7 @@ __device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, uint
 #endif
 }
 
-enum Epi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
+enum Epi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3, EPI_PART = 4 };
 
 struct GemmArgs {
     const uint16_t* a;
@@ -126,6 +181,8 @@ struct GemmArgs {
     uint16_t* vc;         // [kvh, 128, max_pos] f16
     int qh, kvh, pos0, max_pos;
     float eps;
+    // PART: block z multiplies k range [z ksplit, (z + 1) ksplit) and writes its f32 partial to y32 + z M N
+    int ksplit;
 };
 
 // Two main loops, chosen by the launcher: DMA (a grid of at least two blocks per CU) moves tiles from memory
@@ -133,7 +190,13 @@ struct GemmArgs {
 // tiles go through two register sets into two padded LDS buffers with every load two k steps ahead.
 template <int EPI, int BN, bool DMA>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
-    static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID)), "SwiGLU and QKV pair 128 columns");
+    static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID || EPI == EPI_PART)),
+                  "SwiGLU and QKV pair 128 columns");
+    // the k range of this block: all of k, or split z of a PART launch (A and W then start kz columns in)
+    const int kz = EPI == EPI_PART ? int(blockIdx.z) * p.ksplit : 0;
+    const int KE = EPI == EPI_PART ? p.ksplit : p.K;
+    const uint16_t* const pa = p.a + kz;
+    const uint16_t* const pw = p.w + kz;
     constexpr int WN = BN / 2, JT = WN / 16;    // columns per wave, MFMA tiles per wave
     constexpr int GLD = GBK + 8;                // register path: LDS row stride (halves), padded against bank conflicts
     constexpr int STAGE = DMA ? (GBM + BN) * GBK : (GBM + BN) * GLD;  // halves: the A tile then the W tile
@@ -189,8 +252,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             }
             boff[i] = (n * p.K + c * 8) * 2;
         }
-        const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.M * p.K * 2);
-        const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(p.w, (EPI == EPI_SWIGLU ? 2 * p.inter : p.N) * p.K * 2);
+        const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(pa, (p.M * p.K - kz) * 2);
+        const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(pw, ((EPI == EPI_SWIGLU ? 2 * p.inter : p.N) * p.K - kz) * 2);
         auto issue = [&](int buf, int k0) __attribute__((always_inline)) {
             uint16_t* st = lds + buf * STAGE;
     #pragma unroll
@@ -227,7 +290,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         // Two stages: step kt waits for its tile (this wave's loads, then the barrier for everyone's, which also means
         // every wave is done reading the other stage), queues tile kt + 1 into the other stage and multiplies tile kt.
         // The LDS-only barrier: __syncthreads() would also make every wave wait for the loads just queued.
-        const int nk = p.K / GBK;
+        const int nk = KE / GBK;
         issue(0, 0);
         for (int kt = 0; kt < nk; ++kt) {
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile kt have landed in LDS
@@ -259,8 +322,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             }
             boff[i] = (n * p.K + kc) * 2;
         }
-        const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.M * p.K * 2);
-        const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(p.w, (EPI == EPI_SWIGLU ? 2 * p.inter : p.N) * p.K * 2);
+        const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(pa, (p.M * p.K - kz) * 2);
+        const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(pw, ((EPI == EPI_SWIGLU ? 2 * p.inter : p.N) * p.K - kz) * 2);
         // Two register sets, two LDS buffers: tile j is loaded into set j % 2 at the top of iteration j - 2 and stored to
         // LDS buffer j % 2 at the end of iteration j - 1, so each load has two iterations of MFMAs to land. The loop is
         // unrolled by two so every register set is named at compile time.
@@ -326,7 +389,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         using S1 = std::integral_constant<int, 1>;
         using K0 = std::integral_constant<int, 0>;
         using K1 = std::integral_constant<int, 1>;
-        const int nk = p.K / GBK;
+        const int nk = KE / GBK;
         // Tile t is loaded into register set t % 2 and stored to LDS buffer t % 2. Step t (parity P), with tile t in
         // buffer P and its ks-0 operands in F0, tiles t + 1 and t + 2 loaded (or landing) in sets 1 - P and P:
         //   store set 1 - P (tile t + 1) into buffer 1 - P (read up to the previous step, whose barrier every wave has
@@ -370,7 +433,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     }
     __syncthreads();  // the epilogues below reuse the LDS
 
-    if (EPI == EPI_F32 || EPI == EPI_RESID) {
+    if (EPI == EPI_F32 || EPI == EPI_RESID || EPI == EPI_PART) {
+        float* const y = EPI == EPI_PART ? p.y32 + size_t(blockIdx.z) * p.M * p.N : p.y32;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -382,7 +446,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                     int m = m0 + wm * 64 + i * 16 + 4 * g + r;
                     if (m >= p.M) continue;
                     size_t o = size_t(m) * p.N + n;
-                    p.y32[o] = EPI == EPI_RESID ? p.resid[o] + acc[i][j][r] : acc[i][j][r];
+                    y[o] = EPI == EPI_RESID ? p.resid[o] + acc[i][j][r] : acc[i][j][r];
                 }
             }
         return;
@@ -477,7 +541,6 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     }
     __syncthreads();
     const int head = tx;  // QKV: a V head (the q and k heads returned above)
-    if (wn == 1 && EPI == EPI_SWIGLU) return;  // V tiles: all four waves store the transpose
     // the partner half of row tile i, read back from LDS
     auto load_hi = [&](int i, float (&hi)[4][4]) {
 #pragma unroll
@@ -487,23 +550,35 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     };
 
     if (EPI == EPI_SWIGLU) {
-        // a[m, j0 + c] = silu(gate) * up, silu(g) = g / (1 + exp(-g))
+        // a[m, j0 + c] = silu(gate) * up, silu(g) = g / (1 + exp(-g)), into an fp16 tile in LDS after the 32 KiB of x32
+        // (rows of 64 columns padded to 72), then out as 16-byte row chunks by all four waves
+        uint16_t* As = lds + 16384;
+        if (wn == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float hi[4][4];
-            load_hi(i, hi);
+            for (int i = 0; i < 4; ++i) {
+                float hi[4][4];
+                load_hi(i, hi);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int col = tx * 64 + j * 16 + c16;
-                if (col >= p.inter) continue;
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int m = m0 + wm * 64 + i * 16 + 4 * g + r;
-                    if (m >= p.M) continue;
-                    const float gv = acc[i][j][r];
-                    const float sg = gv / (1.0f + __expf(-gv));
-                    p.y16[size_t(m) * p.inter + col] = f2h(sg * hi[j][r]);
-                }
+                    for (int r = 0; r < 4; ++r) {
+                        const float gv = acc[i][j][r];
+                        const float sg = gv / (1.0f + __expf(-gv));
+                        As[(wm * 64 + i * 16 + 4 * g + r) * 72 + j * 16 + c16] = f2h(sg * hi[j][r]);
+                    }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int q = t + 256 * k, row = q >> 3, ch = q & 7, m = m0 + row, col = tx * 64 + ch * 8;
+            if (m >= p.M || col >= p.inter) continue;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(As + row * 72 + ch * 8);
+            uint16_t* dst = p.y16 + size_t(m) * p.inter + col;
+            if (col + 8 <= p.inter && (p.inter & 7) == 0) {
+                *reinterpret_cast<u32x4*>(dst) = v;
+            } else {
+                for (int e = 0; e < 8 && col + e < p.inter; ++e) dst[e] = uint16_t(v[e >> 1] >> (16 * (e & 1)));
             }
         }
         return;
@@ -1860,6 +1935,37 @@ static void l_prefetch(const PreparedDispatch& pd, void* const* p, hipStream_t s
                        (const u32x4*)p[2], n[2], (const u32x4*)p[3], n[3]);
 }
 
+// 39 gemm_residual_split: a, w, partials, m, n, k, splits. 128 x 64 tiles, blockIdx.z = the k split.
+static void l_gemm_resid_split(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    const uint32_t* w = pd.words.data();
+    GemmArgs a = gemm_base(p, w[4], w[5], w[6]);
+    a.y32 = (float*)p[2];
+    a.ksplit = int(w[6] / w[7]);
+    const dim3 grid((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM, w[7]);
+    const uint64_t blocks = uint64_t(grid.x) * grid.y * grid.z;
+    if (blocks % 512 == 0)  // whole rounds of two blocks per CU: the direct-to-LDS loop
+        hipLaunchKernelGGL((k_gemm<EPI_PART, 64, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemm<EPI_PART, 64, false>), grid, dim3(256), 0, s, a);
+}
+
+// 40 residual_add_norm: x, partials, w, y, rows, cols, splits, eps
+static void l_resid_add_norm(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
+    const uint32_t rows = pd.words[5], cols = pd.words[6], splits = pd.words[7];
+    const float eps = f32_of(pd.words[8]);
+#define L_RAN(NC)                                                                                                    \
+    hipLaunchKernelGGL(k_resid_add_norm<NC>, dim3((rows + 3) / 4), dim3(256), 0, s, (float*)p[0], (const float*)p[1], \
+                       (const uint16_t*)p[2], (uint16_t*)p[3], rows, cols, splits, eps)
+    switch (cols / 256) {
+        case 1: L_RAN(1); break;
+        case 2: L_RAN(2); break;
+        case 4: L_RAN(4); break;
+        case 8: L_RAN(8); break;
+        default: L_RAN(16); break;  // 4096 (the catalog admits no other width)
+    }
+#undef L_RAN
+}
+
 // 38 decode_step_persistent (kernels_persist.hip)
 void launch_decode_persistent(const PreparedDispatch& pd, void* const* p, hipStream_t s);
 
@@ -1871,11 +1977,11 @@ const LaunchFn* fast_launchers() {
                                  l_gemv_swiglu, l_lmhead,    l_argmax_dec,   l_embed_dec,    l_fill_normal,
                                  l_convert,     l_argmax_partial, l_argmax_final, l_gemm_skinny_f32,
                                  l_gemm_skinny_resid, l_gemm_skinny_swiglu, l_attn_combine_f16, l_decode_advance,
-                                 l_prefetch,    launch_decode_persistent};
+                                 l_prefetch,    launch_decode_persistent, l_gemm_resid_split, l_resid_add_norm};
     return t;
 }
 
-// ---------------------------------------------------------------- catalog entries (ids 14..38)
+// ---------------------------------------------------------------- catalog entries (ids 14..40)
 
 #define DT(x) (1u << (x))
 #define TOK_R(n, m) FieldSpec{n, FieldKind::Token, Access::Read, m, nullptr}
@@ -2216,6 +2322,40 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 15, 3, "decode_step_persistent", "state");
                      need(c, 16, w[26], "decode_step_persistent", "out_ids");
                      need(c, 17, 2 * int64_t(persist::exchange_entries(int(L), sh)), "decode_step_persistent", "exchange");
+                 }});
+    // 39 gemm_residual_split: a, w, partials, m, n, k, splits. partials[z] = a[:, k range z] . w[:, k range z]^T, the k
+    // range split in `splits` equal parts of multiples of 64; residual_add_norm adds them to the residual stream.
+    c.push_back({"gemm_residual_split", "fast", {256, 1, 1}, false,
+                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 63) / 64, (int64_t(w[4]) + 127) / 128, w[7]}; },
+                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("partials", DT(F32)), U32F("m"), U32F("n"), U32F("k"),
+                  U32F("splits")},
+                 [](const uint32_t* w, const uint32_t* c) {
+                     const int64_t m = w[4], n = w[5], k = w[6], sp = w[7];
+                     if (sp != 1 && sp != 2 && sp != 4 && sp != 8)
+                         contract_fail("gemm_residual_split: splits must be 1, 2, 4 or 8");
+                     if (k < 64 * sp || k % (64 * sp))
+                         contract_fail("gemm_residual_split: k must be a positive multiple of 64 * splits");
+                     if (m < 1 || n < 1) contract_fail("gemm_residual_split: m and n must be at least 1");
+                     need(c, 0, m * k, "gemm_residual_split", "a");
+                     need(c, 1, n * k, "gemm_residual_split", "w");
+                     need(c, 2, sp * m * n, "gemm_residual_split", "partials");
+                 }});
+    // 40 residual_add_norm: x, partials, w, y, rows, cols, splits, eps. x += the partials in split order, then
+    // y = RMSNorm(x) in f16 (as rmsnorm_rows_f16)
+    c.push_back({"residual_add_norm", "fast", {256, 1, 1}, true,
+                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 3) / 4, 1, 1}; },
+                 {TOK_RW("x", DT(F32)), TOK_R("partials", DT(F32)), TOK_R("w", DT(BF16)), TOK_W("y", DT(F16)),
+                  U32F("rows"), U32F("cols"), U32F("splits"), F32F("eps")},
+                 [](const uint32_t* w, const uint32_t* c) {
+                     const int64_t rows = w[5], cols = w[6], sp = w[7];
+                     if (cols != 256 && cols != 512 && cols != 1024 && cols != 2048 && cols != 4096)
+                         contract_fail("residual_add_norm: cols must be 256, 512, 1024, 2048 or 4096");
+                     if (sp != 1 && sp != 2 && sp != 4 && sp != 8)
+                         contract_fail("residual_add_norm: splits must be 1, 2, 4 or 8");
+                     need(c, 0, rows * cols, "residual_add_norm", "x");
+                     need(c, 1, sp * rows * cols, "residual_add_norm", "partials");
+                     need(c, 2, cols, "residual_add_norm", "w");
+                     need(c, 3, rows * cols, "residual_add_norm", "y");
                  }});
     return c;
 }

@@ -307,6 +307,7 @@ void QwenExec::plan() {
         add("q", Activations, F16, {MT, QC});
         add("o", Activations, F16, {MT, QC});
         add("a", Activations, F16, {MT, I});
+        add("resid.partials", Scratch, F32, {2 * MT, H});  // the k-split partials of the prefill residual GEMMs
         const uint32_t B = uint32_t(c.batch);
         add("dec.x", Activations, F32, {B, H});
         add("dec.qkv", Scratch, F32, {B, QC + 2 * KC});
@@ -600,6 +601,15 @@ uint32_t QwenExec::forward_fp32(int pos0, int T, float* logits, int lr) {
     return am;
 }
 
+// The k splits of a prefill residual GEMM of m rows (128 x 64 output tiles): the fewest of 1, 2, 4, 8 that give at
+// least 512 blocks (two per CU), within the partials tensor (2 max_tokens rows) and with k a multiple of 64 per split.
+static uint32_t resid_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t max_tokens) {
+    const uint64_t tiles = uint64_t((n + 63) / 64) * ((m + 127) / 128);
+    uint32_t s = 1;
+    while (s < 8 && tiles * s < 512 && 2 * s * m <= 2 * max_tokens && k % (128 * s) == 0) s *= 2;
+    return s;
+}
+
 uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr) {
     const std::string sq = ".s" + std::to_string(seq);
     const QwenConfig& c = cfg_;
@@ -612,19 +622,36 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
     sync_f16();
     CommandList* l = dev_.begin();
     dispatch(l, "embed_gather_bf16", {tk("ids"), tk("model.embed_tokens.weight"), tk("x"), U, H, V});
+    // x += a . W^T, then h = RMSNorm(x) with norm weights nw: a k-split GEMM into partials and one pass that adds them
+    // and normalises (the split fills the CUs: at 2048 rows the 128 x 64 tiles alone give one block per CU), or, with no
+    // split, the residual GEMM and the norm
+    const uint32_t MT = uint32_t(c.max_tokens);
+    auto residual_norm = [&](const std::string& a, const std::string& wname, uint32_t K, uint32_t nw) {
+        const uint32_t sp = resid_splits(U, H, K, MT);
+        if (sp > 1) {
+            dispatch(l, "gemm_residual_split", {tk(a), tk(wname), tk("resid.partials"), U, H, K, sp});
+            dispatch(l, "residual_add_norm", {tk("x"), tk("resid.partials"), nw, tk("h"), U, H, sp, eps});
+        } else {
+            dispatch(l, "gemm_residual", {tk(a), tk(wname), tk("x"), U, H, K});
+            dispatch(l, "rmsnorm_rows_f16", {tk("x"), nw, tk("h"), U, H, eps, 0});
+        }
+    };
+    dispatch(l, "rmsnorm_rows_f16", {tk("x"), tk(lname(0, kLayerWeights[0])), tk("h"), U, H, eps, 0});
     for (int i = 0; i < c.layers; ++i) {
         const std::string p = "L" + std::to_string(i) + ".";
         auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
-        dispatch(l, "rmsnorm_rows_f16", {tk("x"), w(0), tk("h"), U, H, eps, 0});
+        // h = RMSNorm(x) with this layer's input norm: done by the previous layer's down_proj step (or above)
         dispatch(l, "gemm_qkv_rope", {tk("h"), tk(p + "qkv_proj.f16"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
                                       tk("q"), tk(p + "k_cache" + sq), tk(p + "v_cache" + sq), U, H,
                                       uint32_t(c.heads), uint32_t(c.kv_heads), uint32_t(pos0), MP, eps});
         dispatch(l, "attention_prefill_f16", {tk("q"), tk(p + "k_cache" + sq), tk(p + "v_cache" + sq), tk("o"), U,
                                               uint32_t(pos0), uint32_t(c.heads), uint32_t(c.kv_heads), MP, scale});
-        dispatch(l, "gemm_residual", {tk("o"), tk(p + "o_proj.f16"), tk("x"), U, H, QC});
-        dispatch(l, "rmsnorm_rows_f16", {tk("x"), w(7), tk("h"), U, H, eps, 0});
+        residual_norm("o", p + "o_proj.f16", QC, w(7));
         dispatch(l, "gemm_swiglu", {tk("h"), tk(p + "gate_up_proj.f16"), tk("a"), U, I, H});
-        dispatch(l, "gemm_residual", {tk("a"), tk(p + "down_proj.f16"), tk("x"), U, H, I});
+        // the next layer's input norm (after the last layer: the final norm, which the lm_head pass below recomputes
+        // on its rows)
+        residual_norm("a", p + "down_proj.f16", I,
+                      i + 1 < c.layers ? tk(lname(i + 1, kLayerWeights[0])) : tk("model.norm.weight"));
     }
     // logits of the last lr rows, LC rows per lm_head dispatch
     hipEvent_t e0, e1;

@@ -61,6 +61,45 @@ def test_gemm_f32_and_residual(m, n, k):
         s.close()
 
 
+@pytest.mark.parametrize("m,n,k,splits", [(2048, 1024, 3072, 2), (512, 1024, 2048, 8), (300, 256, 512, 4),
+                                          (128, 512, 1024, 1), (77, 1024, 1024, 2)])
+def test_gemm_residual_split_and_add_norm(m, n, k, splits):
+    """The k-split residual GEMM: each split's partial product against float64 (whole and partial tiles, the
+    direct-to-LDS loop at 512 blocks and the register loop otherwise); residual_add_norm: x + p0 + p1 + ... in split
+    order, bit for bit with float32 arithmetic on the same partials, and its f16 norm output bit for bit with
+    rmsnorm_rows_f16 on the resulting x."""
+    r = np.random.default_rng(m + n + k + splits)
+    a = f16(r.standard_normal((m, k)))
+    w = f16(r.standard_normal((n, k)) * 0.05)
+    x0 = r.standard_normal((m, n)).astype(np.float32)
+    nw = bf16(1 + 0.1 * r.standard_normal(n))
+    s = Session({"a": (F16, (m, k), 0, a), "w": (F16, (n, k), RO, w), "p": (F32, (splits, m, n), 0, None),
+                 "x": (F32, (m, n), 0, x0), "nw": (BF16, (n,), RO, nw), "h": (F16, (m, n), 0, None),
+                 "h2": (F16, (m, n), 0, None)})
+    try:
+        part = s.run("gemm_residual_split", ["p"], a="a", w="w", partials="p", m=m, n=n, k=k, splits=splits)["p"]
+        part = part.reshape(splits, m, n)
+        ks = k // splits
+        for z in range(splits):
+            ref = hwiden(a[:, z * ks:(z + 1) * ks]).astype(np.float64) @ hwiden(w[:, z * ks:(z + 1) * ks]).astype(np.float64).T
+            assert metrics.rel_l2(part[z], ref) < 1e-6, (z, metrics.rel_l2(part[z], ref))
+        cl = s.backend.begin()
+        cl.dispatch("residual_add_norm", s.fields("residual_add_norm", x="x", partials="p", w="nw", y="h", rows=m,
+                                                  cols=n, splits=splits, eps=1e-6))
+        cl.barrier()
+        cl.dispatch("rmsnorm_rows_f16", s.fields("rmsnorm_rows_f16", x="x", w="nw", y="h2", rows=m, cols=n, eps=1e-6,
+                                                 x_row0=0))
+        s.backend.wait(s.backend.submit(cl))
+        cl.release()
+        xe = x0.copy()
+        for z in range(splits):
+            xe = xe + part[z]  # float32, split order
+        assert np.array_equal(s.read("x").view(np.uint32), xe.view(np.uint32))
+        assert np.array_equal(s.read("h"), s.read("h2"))
+    finally:
+        s.close()
+
+
 def test_gemm_swiglu():
     m, inter, k = 200, 192, 128
     r = np.random.default_rng(3)
