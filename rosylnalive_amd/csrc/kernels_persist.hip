@@ -286,6 +286,32 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     lds_barrier();
     if (t < RB) xown[t] = vec[b * RB + t];
 
+    // This split's first 64-key chunks of K and V^T (one when the split holds one, else two): they do not depend on
+    // this step, so the chunks of layer l + 1 load at the end of layer l (layer 0's here), away from stage A, where
+    // loads in flight would hold back this workgroup's q|k|v rows. K: thread t holds key slots t / 16 and t / 16 + 32
+    // of a chunk, dims 8 (t % 16) .. + 7; V^T: dim t / 4, keys 16 (t % 4) .. + 15. Past the last chunk: re-read it
+    // (never used).
+    u32x4 kr[2][2], vr[2][2];
+    auto fetch = [&](auto set, int l, int c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set)::value;
+        const uint16_t* kb = a.kc + ((size_t(l) * a.kvh + hk) * MP + k0) * 128 + 8 * (t & 15);
+        const uint16_t* vb = a.vc + ((size_t(l) * a.kvh + hk) * 128 + (t >> 2)) * MP + k0 + 16 * (t & 3);
+        const int cc = min(c, nch - 1) * 64;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) kr[SET][i] = ld16(kb + size_t(cc + (t >> 4) + 32 * i) * 128);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) vr[SET][j] = ld16(vb + cc + 8 * j);
+    };
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    auto prefetch_kv = [&](int l) __attribute__((always_inline)) {
+        if (attn) {
+            fetch(C0{}, l, 0);
+            if (nch > 1) fetch(C1{}, l, 1);
+        }
+    };
+    prefetch_kv(0);
+
     for (int l = 0; l < a.layers; ++l) {
         uint64_t* xl = a.xch + kHdrEntries + size_t(l) * X.per_layer;
         uint32_t* xv32 = x32 + size_t(l) * X.per_layer32;
@@ -295,26 +321,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             gather32<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, par, vec, hdr, 1, s_fail,
                           wait_ticks);
             if (s_fail) return;
-        }
-        // this split's first two 64-key chunks of K and V^T: they do not depend on this step, so they load while the
-        // projections are computed and handed over. K: thread t holds key slots t / 16 and t / 16 + 32 of a chunk,
-        // dims 8 (t % 16) .. + 7; V^T: dim t / 4, keys 16 (t % 4) .. + 15. Past the last chunk: re-read it (never used).
-        const uint16_t* kb = a.kc + ((size_t(l) * a.kvh + hk) * MP + k0) * 128 + 8 * (t & 15);
-        const uint16_t* vb = a.vc + ((size_t(l) * a.kvh + hk) * 128 + (t >> 2)) * MP + k0 + 16 * (t & 3);
-        u32x4 kr[2][2], vr[2][2];
-        auto fetch = [&](auto set, int c) __attribute__((always_inline)) {
-            constexpr int SET = decltype(set)::value;
-            const int cc = min(c, nch - 1) * 64;
-#pragma unroll
-            for (int i = 0; i < 2; ++i) kr[SET][i] = ld16(kb + size_t(cc + (t >> 4) + 32 * i) * 128);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) vr[SET][j] = ld16(vb + cc + 8 * j);
-        };
-        using C0 = std::integral_constant<int, 0>;
-        using C1 = std::integral_constant<int, 1>;
-        if (attn) {
-            fetch(C0{}, 0);
-            fetch(C1{}, 1);
         }
         // stage C's o_proj weights: this wave's part of row rr
         u32x4 wc[NCC];
@@ -461,9 +467,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             int c = 0;
             for (; c + 2 < nch; c += 2) {  // whole pairs before the last chunk
                 chunk(C0{}, Body{}, c);
-                fetch(C0{}, c + 2);
+                fetch(C0{}, l, c + 2);
                 chunk(C1{}, Body{}, c + 1);
-                fetch(C1{}, c + 3);
+                fetch(C1{}, l, c + 3);
             }
             if (c + 1 < nch) {
                 chunk(C0{}, Body{}, c);
@@ -622,6 +628,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             if (r == 0) xown[i] = xn;
             xstore32(xv32 + X.x2 + r * H + b * RB + i, xn, par);
         }
+        if (l + 1 < a.layers) prefetch_kv(l + 1);
     }
 
     // ---------------------------------------------------------------- lm_head over rows [r0, r1), then the argmax
