@@ -322,13 +322,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                           wait_ticks);
             if (s_fail) return;
         }
-        // stage C's o_proj weights: this wave's part of row rr
         u32x4 wc[NCC];
-        {
-            const uint16_t* W = a.o_proj + (size_t(l) * H + rr) * QC + ks * (QC / KS) + 8 * lane;
-#pragma unroll
-            for (int c = 0; c < NCC; ++c) wc[c] = ld16(W + 512 * c);
-        }
         {
             float xv[NCH][8];
             norm_lane<NCH>(vec, na, a.eps, xv);
@@ -348,6 +342,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         if (t < RA * kWaves) {
             const int row = b * kWaves + (t % kWaves) + (t / kWaves) * NWv;
             if (row < N1) xstore(xl + X.qkv + row, red[t], tag);
+        }
+        // stage C's o_proj weights (this wave's part of row rr), issued after the rows above have left: a load issue
+        // that waits for room in the memory queue would otherwise hold them back
+        {
+            const uint16_t* W = a.o_proj + (size_t(l) * H + rr) * QC + ks * (QC / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCC; ++c) wc[c] = ld16(W + 512 * c);
         }
 
         // ---------------------------------------------------------------- B: attention over this split
@@ -535,17 +536,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                              s_fail, wait_ticks);
             if (s_fail) return;
         }
-        // stage D's gate/up weights: unit u = w UD + j is (row u / NCH of the workgroup's 2 PB, chunk j % NCH); rows
-        // 0 .. PB - 1 are gate rows b PB + r, the rest the matching up rows
-        u32x4 wd[UD], nd[NCH];
-#pragma unroll
-        for (int j = 0; j < UD; ++j) {
-            const int ri = (w * UD + j) / NCH, c = j % NCH;
-            const int grow = ri < PB ? b * PB + ri : I + b * PB + (ri - PB);
-            wd[j] = ld16(a.gate_up + (size_t(l) * 2 * I + grow) * H + 512 * c + 8 * lane);
-        }
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) nd[c] = ld16(a.post_norm + size_t(l) * H + 512 * c + 8 * lane);
         {
             float acc = 0.f;
             const int kb0 = ks * (QC / KS) + 8 * lane;
@@ -563,6 +553,17 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             if (r == 0) xown[i] = xn;
             xstore32(xv32 + X.x1 + r * H + b * RB + i, xn, par);
         }
+        // stage D's gate/up weights, after the rows above: unit u = w UD + j is (row u / NCH of the workgroup's 2 PB, chunk j % NCH); rows
+        // 0 .. PB - 1 are gate rows b PB + r, the rest the matching up rows
+        u32x4 wd[UD], nd[NCH];
+#pragma unroll
+        for (int j = 0; j < UD; ++j) {
+            const int ri = (w * UD + j) / NCH, c = j % NCH;
+            const int grow = ri < PB ? b * PB + ri : I + b * PB + (ri - PB);
+            wd[j] = ld16(a.gate_up + (size_t(l) * 2 * I + grow) * H + 512 * c + 8 * lane);
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) nd[c] = ld16(a.post_norm + size_t(l) * H + 512 * c + 8 * lane);
 
         // ---------------------------------------------------------------- D: a = silu(W_g . h) * (W_u . h)
         {
@@ -570,13 +571,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             gather32<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, par, vec, hdr, 5, s_fail,
                           wait_ticks);
             if (s_fail) return;
-        }
-        // stage E's down_proj weights: this wave's part of row rr
-        u32x4 we[NCE];
-        {
-            const uint16_t* W = a.down + (size_t(l) * H + rr) * I + ks * (I / KS) + 8 * lane;
-#pragma unroll
-            for (int c = 0; c < NCE; ++c) we[c] = ld16(W + 512 * c);
         }
         {
             float xv[NCH][8];
@@ -600,6 +594,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             }
             xstore32(xv32 + X.a + r * I + b * PB + j, g / (1.0f + __expf(-g)) * u, par);
         }
+        // stage E's down_proj weights (this wave's part of row rr), after the outputs above
+        u32x4 we[NCE];
+        {
+            const uint16_t* W = a.down + (size_t(l) * H + rr) * I + ks * (I / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCE; ++c) we[c] = ld16(W + 512 * c);
+        }
 
         // ---------------------------------------------------------------- E: x += W_d . a
         {
@@ -608,9 +609,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                              s_fail, wait_ticks);
             if (s_fail) return;
         }
-        // the next layer's q|k|v rows load while this stage computes (after the last layer: the last one again, never
-        // used; unconditional, so the compiler's wait counting has one path to follow)
-        issue_a(min(l + 1, a.layers - 1));
         {
             float acc = 0.f;
             const int kb0 = ks * (I / KS) + 8 * lane;
@@ -628,6 +626,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             if (r == 0) xown[i] = xn;
             xstore32(xv32 + X.x2 + r * H + b * RB + i, xn, par);
         }
+        // the next layer's q|k|v rows and K/V chunks, after the rows above (after the last layer: its q|k|v rows
+        // again, never used; unconditional, so the compiler's wait counting has one path to follow)
+        issue_a(min(l + 1, a.layers - 1));
         if (l + 1 < a.layers) prefetch_kv(l + 1);
     }
 
