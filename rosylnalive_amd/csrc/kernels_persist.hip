@@ -572,6 +572,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                           wait_ticks);
             if (s_fail) return;
         }
+        // stage E's down_proj weights (this wave's part of row rr), before this stage computes: issued after its
+        // outputs they land only after the hand-off to stage E
+        u32x4 we[NCE];
+        {
+            const uint16_t* W = a.down + (size_t(l) * H + rr) * I + ks * (I / KS) + 8 * lane;
+#pragma unroll
+            for (int c = 0; c < NCE; ++c) we[c] = ld16(W + 512 * c);
+        }
         {
             float xv[NCH][8];
             norm_lane<NCH>(vec, nd, a.eps, xv);
@@ -593,13 +601,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 u += red[(PB + j) * NCH + c];
             }
             xstore32(xv32 + X.a + r * I + b * PB + j, g / (1.0f + __expf(-g)) * u, par);
-        }
-        // stage E's down_proj weights (this wave's part of row rr), after the outputs above
-        u32x4 we[NCE];
-        {
-            const uint16_t* W = a.down + (size_t(l) * H + rr) * I + ks * (I / KS) + 8 * lane;
-#pragma unroll
-            for (int c = 0; c < NCE; ++c) we[c] = ld16(W + 512 * c);
         }
 
         // ---------------------------------------------------------------- E: x += W_d . a
