@@ -1488,15 +1488,19 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* part, uint32_t
 // k + 8g, so 64 contiguous bytes per row per 32-k step) with the A rows from L2, 128 k per iteration, and the next
 // iteration's loads in flight while the current one multiplies (two named register sets). The partial tiles of the 8
 // waves are summed in LDS in a fixed order (deterministic). Rows of A past M and columns past N are clamped in range
-// and never stored.
+// and never stored. SK_PART (gemm_residual_split with m <= 16): block (x, z) multiplies k range z of K / gridDim.y
+// and writes its partial tile to y32 + z M N.
 constexpr int kSkWaves = 8;
-enum SkEpi { SK_F32 = 0, SK_RESID = 1, SK_SWIGLU = 2 };
+enum SkEpi { SK_F32 = 0, SK_RESID = 1, SK_SWIGLU = 2, SK_PART = 3 };
 
-template <int EPI>
+template <int EPI, int NT>
 __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const uint16_t* w, float* y32, uint16_t* y16,
                                                      int M, int N, int K, int inter) {
-    constexpr int NT = EPI == SK_RESID ? 1 : 2;  // MFMA column tiles per block
+    static_assert(NT == 1 || NT == 2, "MFMA column tiles per block");
+    static_assert(EPI != SK_SWIGLU || NT == 2, "SwiGLU pairs a gate and an up tile");
     __shared__ float red[kSkWaves][NT][256];
+    // the k range of this block (a part of k for SK_PART); the A and W rows are still K long
+    const int KS = EPI == SK_PART ? K / int(gridDim.y) : K, kz = EPI == SK_PART ? int(blockIdx.y) * KS : 0;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6, g = lane >> 4, c16 = lane & 15;
     int n0, n1 = 0;
     if (EPI == SK_SWIGLU) {
@@ -1507,8 +1511,8 @@ __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const ui
         n0 = min(int(blockIdx.x) * (16 * NT) + c16, N - 1);
         n1 = min(int(blockIdx.x) * (16 * NT) + 16 + c16, N - 1);
     }
-    const int kper = K / kSkWaves, niter = kper / 128;  // kper a multiple of 128
-    const int kb = wv * kper + 8 * g;
+    const int kper = KS / kSkWaves, niter = kper / 128;  // kper a multiple of 128
+    const int kb = kz + wv * kper + 8 * g;
     const uint16_t* ap = a + size_t(min(c16, M - 1)) * K + kb;
     const uint16_t* w0 = w + size_t(n0) * K + kb;
     const uint16_t* w1 = w + size_t(n1) * K + kb;
@@ -1589,6 +1593,8 @@ __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const ui
     if (row >= M || col >= N) return;
     if (EPI == SK_RESID)
         y32[size_t(row) * N + col] += v;
+    else if (EPI == SK_PART)
+        y32[(size_t(blockIdx.y) * M + row) * N + col] = v;
     else
         y32[size_t(row) * N + col] = v;
 }
@@ -1904,19 +1910,26 @@ static void l_argmax_final(const PreparedDispatch& pd, void* const* p, hipStream
 }
 
 // 32 gemm_skinny_f32, 33 gemm_skinny_residual: a, w, y, m, n, k; 34 gemm_skinny_swiglu: a, w, y, m, inter, k
+// One 16-column tile per block while that still leaves under two blocks per CU; two for wide N (the lm_head), whose
+// A rows would otherwise be read from L2 once per 16 columns.
+static bool skinny_one_tile(uint32_t n) { return (n + 15) / 16 < 512; }
 static void l_gemm_skinny_f32(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    hipLaunchKernelGGL((k_gemm_skinny<SK_F32>), dim3((w[5] + 31) / 32), dim3(512), 0, s, (const uint16_t*)p[0],
-                       (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
+    if (skinny_one_tile(w[5]))
+        hipLaunchKernelGGL((k_gemm_skinny<SK_F32, 1>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
+                           (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
+    else
+        hipLaunchKernelGGL((k_gemm_skinny<SK_F32, 2>), dim3((w[5] + 31) / 32), dim3(512), 0, s, (const uint16_t*)p[0],
+                           (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
 }
 static void l_gemm_skinny_resid(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    hipLaunchKernelGGL((k_gemm_skinny<SK_RESID>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
+    hipLaunchKernelGGL((k_gemm_skinny<SK_RESID, 1>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
                        (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
 }
 static void l_gemm_skinny_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    hipLaunchKernelGGL((k_gemm_skinny<SK_SWIGLU>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
+    hipLaunchKernelGGL((k_gemm_skinny<SK_SWIGLU, 2>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
                        (const uint16_t*)p[1], (float*)nullptr, (uint16_t*)p[2], int(w[4]), 0, int(w[6]), int(w[5]));
 }
 
@@ -1936,8 +1949,18 @@ static void l_prefetch(const PreparedDispatch& pd, void* const* p, hipStream_t s
 }
 
 // 39 gemm_residual_split: a, w, partials, m, n, k, splits. 128 x 64 tiles, blockIdx.z = the k split.
+// the skinny (m <= 16) form of gemm_residual_split: 8 waves over each split's k, 128 per wave per step
+static bool resid_split_skinny(uint32_t m, uint32_t k, uint32_t splits) {
+    return m <= 16 && (k / splits) % (kSkWaves * 128) == 0;
+}
 static void l_gemm_resid_split(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
+    if (resid_split_skinny(w[4], w[6], w[7])) {
+        hipLaunchKernelGGL((k_gemm_skinny<SK_PART, 1>), dim3((w[5] + 15) / 16, w[7]), dim3(512), 0, s,
+                           (const uint16_t*)p[0], (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]),
+                           int(w[5]), int(w[6]), 0);
+        return;
+    }
     GemmArgs a = gemm_base(p, w[4], w[5], w[6]);
     a.y32 = (float*)p[2];
     a.ksplit = int(w[6] / w[7]);
@@ -2248,7 +2271,9 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 32 gemm_skinny_f32: a, w, y, m, n, k
     c.push_back({"gemm_skinny_f32", "fast", {512, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 31) / 32, 1, 1}; },
+                 [](const uint32_t* w) {
+                     return Grid3{skinny_one_tile(w[5]) ? (int64_t(w[5]) + 15) / 16 : (int64_t(w[5]) + 31) / 32, 1, 1};
+                 },
                  {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F32)), U32F("m"), U32F("n"), U32F("k")},
                  [](const uint32_t* w, const uint32_t* c) { check_skinny("gemm_skinny_f32", w, c, w[5], w[5]); }});
     // 33 gemm_skinny_residual: a, w, x, m, n, k
@@ -2324,9 +2349,13 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 17, 2 * int64_t(persist::exchange_entries(int(L), sh)), "decode_step_persistent", "exchange");
                  }});
     // 39 gemm_residual_split: a, w, partials, m, n, k, splits. partials[z] = a[:, k range z] . w[:, k range z]^T, the k
-    // range split in `splits` equal parts of multiples of 64; residual_add_norm adds them to the residual stream.
+    // range split in `splits` equal parts of multiples of 64; residual_add_norm adds them to the residual stream. For
+    // m <= 16 with 1024-multiples per split it runs as a skinny GEMM (512 threads, one block per 16 columns and split).
     c.push_back({"gemm_residual_split", "fast", {256, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 63) / 64, (int64_t(w[4]) + 127) / 128, w[7]}; },
+                 [](const uint32_t* w) {
+                     if (resid_split_skinny(w[4], w[6], w[7])) return Grid3{(int64_t(w[5]) + 15) / 16, w[7], 1};
+                     return Grid3{(int64_t(w[5]) + 63) / 64, (int64_t(w[4]) + 127) / 128, w[7]};
+                 },
                  {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("partials", DT(F32)), U32F("m"), U32F("n"), U32F("k"),
                   U32F("splits")},
                  [](const uint32_t* w, const uint32_t* c) {

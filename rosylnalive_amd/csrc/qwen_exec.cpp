@@ -753,11 +753,24 @@ void QwenExec::record_decode_batch(CommandList* l) {
     uint32_t chunks = 1;
     while (chunks < 16 && B * uint32_t(c.kv_heads) * (MP / 64) / (2 * chunks) >= 2048) chunks *= 2;
     auto tk = [&](const std::string& n) { return token(n); };
+    // x += a . W^T, then h = RMSNorm(x) with norm weights nw: the GEMM split over k in two (twice the blocks: one
+    // block per 16 columns alone leaves half the CUs idle at hidden 2048) into partials, then one pass that adds them
+    // and normalises; or, when k does not split in 1024-multiples, the residual GEMM and the norm
+    auto residual_norm = [&](const std::string& a, const std::string& wname, uint32_t K, uint32_t nw) {
+        if (K % 2048 == 0) {
+            dispatch(l, "gemm_residual_split", {tk(a), tk(wname), tk("resid.partials"), B, H, K, 2});
+            dispatch(l, "residual_add_norm", {tk("dec.x"), tk("resid.partials"), nw, tk("dec.h16"), B, H, 2, eps});
+        } else {
+            dispatch(l, "gemm_skinny_residual", {tk(a), tk(wname), tk("dec.x"), B, H, K});
+            dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), nw, tk("dec.h16"), B, H, eps, 0});
+        }
+    };
     dispatch(l, "embed_dec", {tk("model.embed_tokens.weight"), tk("dec.state"), tk("dec.x"), H, V, B});
+    dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), tk(lname(0, kLayerWeights[0])), tk("dec.h16"), B, H, eps, 0});
     for (int i = 0; i < c.layers; ++i) {
         const std::string p = "L" + std::to_string(i) + ".";
         auto w = [&](int k) { return tk(lname(i, kLayerWeights[k])); };
-        dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), w(0), tk("dec.h16"), B, H, eps, 0});
+        // h = RMSNorm(x) with this layer's input norm: done above or by the previous layer's down_proj step
         dispatch(l, "gemm_skinny_f32", {tk("dec.h16"), tk(p + "qkv_proj.f16"), tk("dec.qkv"), B, QC + 2 * KC, H});
         dispatch(l, "attention_decode_f16", {tk("dec.qkv"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
                                              tk(p + "k_cache"), tk(p + "v_cache"), tk("dec.attn_partials"),
@@ -765,12 +778,12 @@ void QwenExec::record_decode_batch(CommandList* l) {
                                              B, chunks});
         dispatch(l, "attention_combine_f16", {tk("dec.attn_partials"), tk("dec.o16"), tk("dec.state"),
                                               uint32_t(c.heads), MP, B, chunks});
-        dispatch(l, "gemm_skinny_residual", {tk("dec.o16"), tk(p + "o_proj.f16"), tk("dec.x"), B, H, QC});
-        dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), w(7), tk("dec.h16"), B, H, eps, 0});
+        residual_norm("dec.o16", p + "o_proj.f16", QC, w(7));
         dispatch(l, "gemm_skinny_swiglu", {tk("dec.h16"), tk(p + "gate_up_proj.f16"), tk("dec.a16"), B, I, H});
-        dispatch(l, "gemm_skinny_residual", {tk("dec.a16"), tk(p + "down_proj.f16"), tk("dec.x"), B, H, I});
+        // the next layer's input norm (after the last layer: the final norm, the lm_head's input)
+        residual_norm("dec.a16", p + "down_proj.f16", I,
+                      i + 1 < c.layers ? tk(lname(i + 1, kLayerWeights[0])) : tk("model.norm.weight"));
     }
-    dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), tk("model.norm.weight"), tk("dec.h16"), B, H, eps, 0});
     dispatch(l, "gemm_skinny_f32", {tk("dec.h16"), tk("embed.f16"), tk("logits"), B, V, H});
     dispatch(l, "argmax_rows_partial", {tk("logits"), tk("argmax.partials"), B, V});
     dispatch(l, "argmax_rows_final", {tk("argmax.partials"), tk("argmax"), B});

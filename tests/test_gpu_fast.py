@@ -62,10 +62,11 @@ def test_gemm_f32_and_residual(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,splits", [(2048, 1024, 3072, 2), (512, 1024, 2048, 8), (300, 256, 512, 4),
-                                          (128, 512, 1024, 1), (77, 1024, 1024, 2)])
+                                          (128, 512, 1024, 1), (77, 1024, 1024, 2), (16, 2048, 6144, 2),
+                                          (5, 2048, 2048, 2), (16, 1024, 4096, 4)])
 def test_gemm_residual_split_and_add_norm(m, n, k, splits):
     """The k-split residual GEMM: each split's partial product against float64 (whole and partial tiles, the
-    direct-to-LDS loop at 512 blocks and the register loop otherwise); residual_add_norm: x + p0 + p1 + ... in split
+    direct-to-LDS loop at 512 blocks and the register loop otherwise, the skinny form for m <= 16); residual_add_norm: x + p0 + p1 + ... in split
     order, bit for bit with float32 arithmetic on the same partials, and its f16 norm output bit for bit with
     rmsnorm_rows_f16 on the resulting x."""
     r = np.random.default_rng(m + n + k + splits)
@@ -454,7 +455,7 @@ def test_argmax_rows_split_matches_cpuref():
 
 # ---------------------------------------------------------------- batched decode kernels
 
-@pytest.mark.parametrize("m,n,k", [(1, 96, 1024), (5, 4096, 1024), (16, 2048, 2048), (16, 1000, 3072)])
+@pytest.mark.parametrize("m,n,k", [(1, 96, 1024), (5, 4096, 1024), (16, 2048, 2048), (16, 1000, 3072), (3, 9000, 1024)])
 def test_gemm_skinny(m, n, k):
     r = np.random.default_rng(m * 31 + n + k)
     a = f16(r.standard_normal((m, k)))
