@@ -947,8 +947,10 @@ __global__ __launch_bounds__(256) void k_gemv_norm_dec(const float* x, const uin
 
 // ---------------------------------------------------------------- 21 attention_decode_f16
 // Split-KV decode attention over positions 0 .. pos = state[b]. Block (s, kv head, b) takes keys [64 C s, 64 C s +
-// 64 C) (C = chunks per split, chosen by the caller so the grid still fills the chip: 1 for one sequence, more for a
-// batch at long context) for the two query heads of the group, 64 keys at a time. It issues the loads of its first two
+// 64 C) for the two query heads of the group, 64 keys at a time. C = chunks per split: given by the caller (1 for one
+// sequence, whose splits are its only parallelism), or, with chunks = 0, the fewest that cover 0 .. pos in the grid's
+// S splits, C = ceil((pos + 1) / 64 S): every sequence's keys then spread evenly over its S blocks, so a grid sized to
+// one round of resident blocks ends with them all instead of a partly filled last round. It issues the loads of its first two
 // chunks, then applies the q RMSNorm and RoPE to the raw projection; the block whose split holds pos also computes the
 // new key (k RMSNorm + RoPE) and value, appends them (fp16) to the caches and uses the same rounded values in place of
 // the stale slot it loaded. Per chunk: scores (each key's dot over 16 lanes), an online softmax per head in the log2
@@ -977,11 +979,12 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
     kc += size_t(b) * kvh * max_pos * 128;
     vc += size_t(b) * kvh * 128 * max_pos;
     part += size_t(b) * qh * S * 130;
-    const int key0 = s * 64 * chunks;
-    const int nkeys = min(64 * chunks, pos + 1 - key0);  // keys of this split at or before pos
+    const int ck = chunks > 0 ? chunks : (pos + 64 * S) / (64 * S);  // chunks per split of this sequence
+    const int key0 = s * 64 * ck;
+    const int nkeys = min(64 * ck, pos + 1 - key0);  // keys of this split at or before pos
     if (nkeys <= 0) return;
     const int nch = (nkeys + 63) / 64;  // chunks to run; the last one ends inside max_pos (a multiple of 64)
-    const bool has_pos = pos < key0 + 64 * chunks;  // uniform over the block
+    const bool has_pos = pos < key0 + 64 * ck;  // uniform over the block
     const int jnew = pos - key0;                     // the new key's offset in the split when has_pos
 
     // thread mapping: K as 4 keys (wv * 16 + it * 4 + lane / 16) x 8 dims (d0); V^T as 4 dims (rg + 32 dd) x 8 keys
@@ -1176,7 +1179,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
 
 // ---------------------------------------------------------------- 22 attention_combine
 // y[h, d] = sum_s 2^(m_s - M) o_s[d] / sum_s 2^(m_s - M) l_s over the splits that hold keys; one block per head, the
-// splits spread over the threads (every load of a pass is independent of the others).
+// splits spread over the threads (every load of a pass is independent of the others). split_keys = 0: the splits of
+// each sequence are the even ones of attention_decode_f16 with chunks = 0, 64 ceil((pos + 1) / 64 splits) keys each.
 constexpr int kMaxSplits = 1024;
 template <typename OUT>
 __global__ __launch_bounds__(256) void k_attn_combine(const float* part, OUT* y, const uint32_t* state, int splits,
@@ -1187,7 +1191,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* part, OUT* y,
     const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int pos = int(state[b]);
     if (pos < 0 || pos >= max_pos) return;
-    const int used = min(pos / split_keys + 1, splits);
+    const int sk = split_keys > 0 ? split_keys : 64 * ((pos + 64 * splits) / (64 * splits));
+    const int used = min(pos / sk + 1, splits);
     const float* hp = part + (size_t(b) * gridDim.x + h) * splits * 130;
     float m = -INFINITY;
     for (int i = t; i < used; i += 256) m = fmaxf(m, hp[size_t(i) * 130]);
@@ -1798,7 +1803,7 @@ static void l_gemv_norm(const PreparedDispatch& pd, void* const* p, hipStream_t 
 }
 
 // 21 attention_decode_f16: qkv, q_norm, k_norm, cos, sin, k_cache, v_cache, partials, state, q_heads, kv_heads,
-// max_pos, eps, scale
+// max_pos, eps, scale, batch, chunks, splits
 // 64-key chunks per split block: the `chunks` field, 0 meaning 1 (the field is the last one; callers that predate it
 // leave its word 0)
 static int dec_chunks(uint32_t w) { return w == 0 ? 1 : int(w); }
@@ -1807,29 +1812,37 @@ static uint32_t dec_splits(uint32_t max_pos, uint32_t chunks) {
     return (max_pos + keys - 1) / keys;
 }
 
+// the splits per sequence: the `splits` field when set (then each sequence's keys spread evenly over them), else one
+// per 64 C keys of max_pos
+static uint32_t dec_grid_splits(uint32_t max_pos, uint32_t chunks, uint32_t splits) {
+    return splits ? splits : dec_splits(max_pos, chunks);
+}
+
 static void l_attn_dec(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     const int max_pos = int(w[12]);
-    const dim3 grid(dec_splits(w[12], w[16]), w[11], w[15]);
+    const bool even = w[17] != 0;
+    const dim3 grid(dec_grid_splits(w[12], w[16], w[17]), w[11], w[15]);
 #define L_DEC(M)                                                                                                     \
     hipLaunchKernelGGL(k_attn_dec<M>, grid, dim3(256), 0, s, (const float*)p[0], (const uint16_t*)p[1],             \
                        (const uint16_t*)p[2], (const float*)p[3], (const float*)p[4], (uint16_t*)p[5],              \
                        (uint16_t*)p[6], (float*)p[7], (const uint32_t*)p[8], int(w[10]), int(w[11]), max_pos,       \
-                       f32_of(w[13]), f32_of(w[14]) * kLog2e, dec_chunks(w[16]))
-    if (dec_chunks(w[16]) == 1)
+                       f32_of(w[13]), f32_of(w[14]) * kLog2e, even ? 0 : dec_chunks(w[16]))
+    if (!even && dec_chunks(w[16]) == 1)
         L_DEC(false);
     else
         L_DEC(true);
 #undef L_DEC
 }
 
-// 22 attention_combine, 35 attention_combine_f16: partials, y, state, q_heads, max_pos, batch, chunks
+// 22 attention_combine, 35 attention_combine_f16: partials, y, state, q_heads, max_pos, batch, chunks, splits
 template <typename OUT>
 static void l_attn_combine_t(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     const int max_pos = int(w[5]);
     hipLaunchKernelGGL((k_attn_combine<OUT>), dim3(w[4], w[6]), dim3(256), 0, s, (const float*)p[0], (OUT*)p[1],
-                       (const uint32_t*)p[2], int(dec_splits(w[5], w[7])), 64 * dec_chunks(w[7]), max_pos);
+                       (const uint32_t*)p[2], int(dec_grid_splits(w[5], w[7], w[8])), w[8] ? 0 : 64 * dec_chunks(w[7]),
+                       max_pos);
 }
 static void l_attn_combine(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     l_attn_combine_t<float>(pd, p, s);
@@ -2036,10 +2049,16 @@ static void need_chunks(const char* k, uint32_t chunks) {
     if (chunks > 64) contract_fail("%s: chunks must be in 0 .. 64 (0 = 1)", k);
 }
 
+// splits (0 = one per 64 chunks keys of max_pos): at most max_pos / 64, the most the partials hold
+static void need_splits(const char* k, uint32_t splits, uint32_t max_pos) {
+    if (splits > max_pos / 64) contract_fail("%s: splits must be in 0 .. max_pos / 64 (0 = by chunks)", k);
+}
+
 static void check_combine(const char* k, const uint32_t* w, const uint32_t* c) {
     const int64_t qh = w[4], mp = w[5], B = w[6];
     need_batch(k, w[6]);
     need_chunks(k, w[7]);
+    need_splits(k, w[8], w[5]);
     if (mp < 64 || mp % 64 || mp > 64 * kMaxSplits) contract_fail("%s: max_pos must be a multiple of 64 in 64 .. %d", k, 64 * kMaxSplits);
     need(c, 0, B * qh * (mp / 64) * 130, k, "partials");
     need(c, 1, B * qh * 128, k, "y");
@@ -2158,17 +2177,19 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 21 attention_decode_f16
     c.push_back({"attention_decode_f16", "fast", {256, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{dec_splits(w[12], w[16]), w[11], w[15]}; },
+                 [](const uint32_t* w) { return Grid3{dec_grid_splits(w[12], w[16], w[17]), w[11], w[15]}; },
                  {TOK_R("qkv", DT(F32)), TOK_R("q_norm", DT(BF16)), TOK_R("k_norm", DT(BF16)),
                   TOK_R("cos_table", DT(F32)), TOK_R("sin_table", DT(F32)), TOK_RW("k_cache", DT(F16)),
                   TOK_RW("v_cache", DT(F16)), TOK_W("partials", DT(F32)), TOK_R("state", DT(U32)), U32F("q_heads"),
-                  U32F("kv_heads"), U32F("max_pos"), F32F("eps"), F32F("scale"), U32F("batch"), U32F("chunks")},
+                  U32F("kv_heads"), U32F("max_pos"), F32F("eps"), F32F("scale"), U32F("batch"), U32F("chunks"),
+                  U32F("splits")},
                  [](const uint32_t* w, const uint32_t* c) {
                      const int64_t qh = w[10], kvh = w[11], mp = w[12], B = w[15];
                      need_group2("attention_decode_f16", w[10], w[11]);
                      need_max_pos("attention_decode_f16", w[12]);
                      need_batch("attention_decode_f16", w[15]);
                      need_chunks("attention_decode_f16", w[16]);
+                     need_splits("attention_decode_f16", w[17], w[12]);
                      need(c, 0, B * (qh + 2 * kvh) * 128, "attention_decode_f16", "qkv");
                      need(c, 1, 128, "attention_decode_f16", "q_norm");
                      need(c, 2, 128, "attention_decode_f16", "k_norm");
@@ -2182,7 +2203,7 @@ std::vector<KernelSpec> fast_catalog() {
     // 22 attention_combine: partials, y, state, q_heads, max_pos
     c.push_back({"attention_combine", "fast", {256, 1, 1}, false, [](const uint32_t* w) { return Grid3{w[4], w[6], 1}; },
                  {TOK_R("partials", DT(F32)), TOK_W("y", DT(F32)), TOK_R("state", DT(U32)), U32F("q_heads"),
-                  U32F("max_pos"), U32F("batch"), U32F("chunks")},
+                  U32F("max_pos"), U32F("batch"), U32F("chunks"), U32F("splits")},
                  [](const uint32_t* w, const uint32_t* c) { check_combine("attention_combine", w, c); }});
     // 23 gemv_residual_dec: a, w, x, n, k
     c.push_back({"gemv_residual_dec", "fast", {256, 1, 1}, true,
@@ -2292,7 +2313,7 @@ std::vector<KernelSpec> fast_catalog() {
     c.push_back({"attention_combine_f16", "fast", {256, 1, 1}, false,
                  [](const uint32_t* w) { return Grid3{w[4], w[6], 1}; },
                  {TOK_R("partials", DT(F32)), TOK_W("y", DT(F16)), TOK_R("state", DT(U32)), U32F("q_heads"),
-                  U32F("max_pos"), U32F("batch"), U32F("chunks")},
+                  U32F("max_pos"), U32F("batch"), U32F("chunks"), U32F("splits")},
                  [](const uint32_t* w, const uint32_t* c) { check_combine("attention_combine_f16", w, c); }});
     // 36 decode_advance: argmax, state, out_ids, batch, max_steps
     c.push_back({"decode_advance", "fast", {256, 1, 1}, true, [](const uint32_t*) { return Grid3{1, 1, 1}; },

@@ -748,10 +748,12 @@ void QwenExec::record_decode_batch(CommandList* l) {
                    V = c.vocab, HD = c.head_dim, MP = c.max_pos, B = uint32_t(c.batch);
     const uint32_t eps = fbits(c.eps);
     const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
-    // 64-key chunks per decode-attention block: as many as keep about 2048 blocks (8 per CU) at full context, so a
-    // block streams several chunks with its loads ahead instead of paying its set-up latency per 64 keys
-    uint32_t chunks = 1;
-    while (chunks < 16 && B * uint32_t(c.kv_heads) * (MP / 64) / (2 * chunks) >= 2048) chunks *= 2;
+    // decode-attention splits per (sequence, KV head): the multi-chunk attention block holds two blocks per CU, so
+    // 2 x CUs blocks are one round; each sequence's keys spread evenly over its splits (sized on the device from its
+    // position), so the blocks finish together instead of leaving a partly filled last round
+    const uint32_t pairs = B * uint32_t(c.kv_heads);
+    const uint32_t splits =
+        std::min(MP / 64, std::max(1u, 2u * uint32_t(dev_.info().compute_units) / pairs));
     auto tk = [&](const std::string& n) { return token(n); };
     // x += a . W^T, then h = RMSNorm(x) with norm weights nw: the GEMM split over k in two (twice the blocks: one
     // block per 16 columns alone leaves half the CUs idle at hidden 2048) into partials, then one pass that adds them
@@ -775,9 +777,9 @@ void QwenExec::record_decode_batch(CommandList* l) {
         dispatch(l, "attention_decode_f16", {tk("dec.qkv"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
                                              tk(p + "k_cache"), tk(p + "v_cache"), tk("dec.attn_partials"),
                                              tk("dec.state"), uint32_t(c.heads), uint32_t(c.kv_heads), MP, eps, scale,
-                                             B, chunks});
+                                             B, 0, splits});
         dispatch(l, "attention_combine_f16", {tk("dec.attn_partials"), tk("dec.o16"), tk("dec.state"),
-                                              uint32_t(c.heads), MP, B, chunks});
+                                              uint32_t(c.heads), MP, B, 0, splits});
         residual_norm("dec.o16", p + "o_proj.f16", QC, w(7));
         dispatch(l, "gemm_skinny_swiglu", {tk("dec.h16"), tk(p + "gate_up_proj.f16"), tk("dec.a16"), B, I, H});
         // the next layer's input norm (after the last layer: the final norm, the lm_head's input)

@@ -141,6 +141,19 @@ def test_dispatch_rules_raise_contract_errors():
         prepare(sealed, 12, ArgBlock.encode("matmul_bf16w", x=1, w=2, y=1, m=1, n=1, k=4))
 
 
+def test_attention_combine_splits_bound():
+    """The partials hold max_pos / 64 splits per head: an even-split count past that is a contract error."""
+    sealed, _ = _table([("part", DType.F32, [16 * 2 * 130], 0), ("y", DType.F16, [2048], 0),
+                        ("state", DType.U32, [4], TensorFlags.READ_ONLY)])
+    kid = 35  # attention_combine_f16
+    for splits in (0, 1, 2):
+        prepare(sealed, kid, ArgBlock.encode("attention_combine_f16", partials=1, y=2, state=3, q_heads=16,
+                                             max_pos=128, batch=1, chunks=0, splits=splits))
+    with pytest.raises(GpuContractException, match="splits"):
+        prepare(sealed, kid, ArgBlock.encode("attention_combine_f16", partials=1, y=2, state=3, q_heads=16,
+                                             max_pos=128, batch=1, chunks=0, splits=3))
+
+
 def test_tensor_row_vectors_T1_T2():
     out = (ctypes.c_uint32 * 16)()
     dims = (ctypes.c_uint32 * 2)(151936, 1024)

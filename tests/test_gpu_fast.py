@@ -488,10 +488,11 @@ def test_gemm_skinny_swiglu():
         s.close()
 
 
-@pytest.mark.parametrize("chunks", [1, 4])
-def test_attention_decode_batched_f16_combine(chunks):
+@pytest.mark.parametrize("chunks,splits", [(1, 0), (4, 0), (0, 3), (0, 16)])
+def test_attention_decode_batched_f16_combine(chunks, splits):
     """Three sequences at positions 5, 64 and 700 in one dispatch (batch on the grid), then the fp16 combine; each
-    sequence against CpuRef F64 on its own cache."""
+    sequence against CpuRef F64 on its own cache. splits > 0: each sequence's keys spread evenly over that many
+    splits (3: 64, 64 and 256 keys per split; 16: one chunk each, 1, 2 and 11 splits holding keys)."""
     max_pos, S = 1024, 16
     positions = [5, 64, 700]
     B = len(positions)
@@ -518,9 +519,10 @@ def test_attention_decode_batched_f16_combine(chunks):
                                                              sin_table="sin", k_cache="kc", v_cache="vc",
                                                              partials="part", state="state", q_heads=16, kv_heads=8,
                                                              max_pos=max_pos, eps=1e-6, scale=scale, batch=B,
-                                                             chunks=chunks)),
+                                                             chunks=chunks, splits=splits)),
                                ("attention_combine_f16", dict(partials="part", y="y", state="state", q_heads=16,
-                                                              max_pos=max_pos, batch=B, chunks=chunks))],
+                                                              max_pos=max_pos, batch=B, chunks=chunks,
+                                                              splits=splits))],
                               ["y"])["y"])
         kc2 = s.read("kc").reshape(B, 8, max_pos, 128)
         vc2 = s.read("vc").reshape(B, 8, 128, max_pos)
