@@ -958,13 +958,18 @@ __global__ __launch_bounds__(256) void k_gemv_norm_dec(const float* x, const uin
 // ahead loading meanwhile; the 8 key groups are reduced once at the end. Each block writes, per head, (max, sum,
 // unnormalised output[128]); splits past pos do nothing. Positions past pos are loaded (they lie inside max_pos) but
 // masked by selects: the scores to -inf, the values to 0 (unwritten positions may hold anything).
-// MULTI = false is the one-chunk form (chunks == 1): no second register set and no loop, so the registers stay low
-// enough for many blocks per CU, which the one-sequence decode needs (its splits are its only parallelism).
+// MULTI = false is the one-chunk form (chunks == 1): 256 threads, no second register set and no loop, so the
+// registers stay low enough for many blocks per CU, which the one-sequence decode needs (its splits are its only
+// parallelism). MULTI = true streams chunks with 512 threads: a chunk's scores and P V spread over 8 waves, halving
+// each wave's share of the per-chunk chain (scores, softmax, P V, three barriers) that bounds a block's rate.
 template <bool MULTI>
-__global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16_t* qn, const uint16_t* kn,
-                                                  const float* cos_t, const float* sin_t, uint16_t* kc, uint16_t* vc,
-                                                  float* part, const uint32_t* state, int qh, int kvh, int max_pos,
-                                                  float eps, float scale_log2, int chunks) {
+__global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv, const uint16_t* qn,
+                                                                const uint16_t* kn, const float* cos_t,
+                                                                const float* sin_t, uint16_t* kc, uint16_t* vc,
+                                                                float* part, const uint32_t* state, int qh, int kvh,
+                                                                int max_pos, float eps, float scale_log2, int chunks) {
+    // waves per block; keys per wave and 4-key rows per thread for the scores; V^T row groups and rows per thread
+    constexpr int NT = MULTI ? 512 : 256, NW = NT / 64, ITS = 64 / NW / 4, RG = NT / 8, DD = 128 / RG;
     __shared__ float qs[2][128];
     __shared__ float knew[128];
     __shared__ float vnew[128];
@@ -985,22 +990,24 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
     if (nkeys <= 0) return;
     const int nch = (nkeys + 63) / 64;  // chunks to run; the last one ends inside max_pos (a multiple of 64)
     const bool has_pos = pos < key0 + 64 * ck;  // uniform over the block
-    const int jnew = pos - key0;                     // the new key's offset in the split when has_pos
+    const int jnew = pos - key0;                 // the new key's offset in the split when has_pos
 
-    // thread mapping: K as 4 keys (wv * 16 + it * 4 + lane / 16) x 8 dims (d0); V^T as 4 dims (rg + 32 dd) x 8 keys
+    // thread mapping: K as ITS keys (wv * 4 ITS + it * 4 + lane / 16) x 8 dims (d0); V^T as DD dims (rg + RG dd) x 8
+    // keys (8 sub ..)
     const int d0 = 8 * (lane & 15), sub = t & 7, rg = t >> 3;
     const uint16_t* kb = kc + (size_t(kvhead) * max_pos + key0) * 128 + d0;
     const uint16_t* vb = vc + size_t(kvhead) * 128 * max_pos + key0 + sub * 8;
-    u32x4 kv4[2][4], vv[2][4];
+    u32x4 kv4[2][ITS], vv[2][DD];
     auto fetch = [&](auto set, int c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set)::value;
         c = min(c, nch - 1) * 64;  // past the last chunk: re-read it (an L2 hit, never used)
 #pragma unroll
-        for (int it = 0; it < 4; ++it)
-            kv4[SET][it] = *reinterpret_cast<const u32x4*>(kb + size_t(c + wv * 16 + it * 4 + (lane >> 4)) * 128);
+        for (int it = 0; it < ITS; ++it)
+            kv4[SET][it] =
+                *reinterpret_cast<const u32x4*>(kb + size_t(c + wv * 4 * ITS + it * 4 + (lane >> 4)) * 128);
 #pragma unroll
-        for (int dd = 0; dd < 4; ++dd)
-            vv[SET][dd] = *reinterpret_cast<const u32x4*>(vb + size_t(rg + 32 * dd) * max_pos + c);
+        for (int dd = 0; dd < DD; ++dd)
+            vv[SET][dd] = *reinterpret_cast<const u32x4*>(vb + size_t(rg + RG * dd) * max_pos + c);
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
@@ -1011,45 +1018,50 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // the raw projections, the norm weights and the rotation of pos
-    const int hh = t >> 7, d = t & 127;  // thread t: q head 2 kvhead + hh; new key (hh = 0) or value (hh = 1); dim d
+    // the raw projections, the norm weights and the rotation of pos (threads 0 .. 255; the rest wait at the barriers)
+    const int hh = (t >> 7) & 1, d = t & 127;  // thread t: q head 2 kvhead + hh; new key (hh = 0) or value (hh = 1)
+    const bool pro = t < 256;
     const int QC = qh * 128, KC = kvh * 128;
-    const float qv = qkv[(kvhead * 2 + hh) * 128 + d];
-    const float kvv = has_pos ? qkv[QC + hh * KC + kvhead * 128 + d] : 0.f;
+    const float qv = pro ? qkv[(kvhead * 2 + hh) * 128 + d] : 0.f;
+    const float kvv = pro && has_pos ? qkv[QC + hh * KC + kvhead * 128 + d] : 0.f;
     const float cs = cos_t[size_t(pos) * 64 + (d & 63)], sn = sin_t[size_t(pos) * 64 + (d & 63)];
     const float qw = bf2f(qn[d]), kw = bf2f(kn[d]);
 
     // per-head RMSNorm (head hh = waves 2 hh, 2 hh + 1; the new key = waves 0, 1), then the rotation of (d, d + 64)
     const float sq = wave_sum(qv * qv), sk = wave_sum(kvv * kvv);
-    if (lane == 0) {
+    if (lane == 0 && pro) {
         redq[wv] = sq;
         redk[wv] = sk;
     }
     __syncthreads();
     const float qr = qw * (qv * (1.0f / sqrtf((redq[2 * hh] + redq[2 * hh + 1]) / 128.0f + eps)));
     const float kr = kw * (kvv * (1.0f / sqrtf((redk[0] + redk[1]) / 128.0f + eps)));
-    qs[hh][d] = qr;
-    if (hh == 0) knew[d] = kr;
+    if (pro) {
+        qs[hh][d] = qr;
+        if (hh == 0) knew[d] = kr;
+    }
     __syncthreads();
     const float qrot = d < 64 ? qr * cs - qs[hh][d + 64] * sn : qr * cs + qs[hh][d - 64] * sn;
     const float krot = d < 64 ? kr * cs - knew[d + 64] * sn : kr * cs + knew[d - 64] * sn;
     __syncthreads();
-    qs[hh][d] = qrot;
-    if (has_pos) {
-        if (hh == 0) {
-            const uint16_t kh = f2h(krot);
-            knew[d] = h2f(kh);
-            kc[(size_t(kvhead) * max_pos + pos) * 128 + d] = kh;
-        } else {
-            const uint16_t vh = f2h(kvv);
-            vnew[d] = h2f(vh);
-            vc[(size_t(kvhead) * 128 + d) * max_pos + pos] = vh;
+    if (pro) {
+        qs[hh][d] = qrot;
+        if (has_pos) {
+            if (hh == 0) {
+                const uint16_t kh = f2h(krot);
+                knew[d] = h2f(kh);
+                kc[(size_t(kvhead) * max_pos + pos) * 128 + d] = kh;
+            } else {
+                const uint16_t vh = f2h(kvv);
+                vnew[d] = h2f(vh);
+                vc[(size_t(kvhead) * 128 + d) * max_pos + pos] = vh;
+            }
         }
     }
     __syncthreads();
     // this thread's query dims and, for the split holding pos, its slices of the new key and value (read
     // unconditionally, used only through selects: a conditional LDS read would become a branch per element)
-    float q0[8], q1[8], kn8[8], vn4[4];
+    float q0[8], q1[8], kn8[8], vnd[DD];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         q0[e] = qs[0][d0 + e];
@@ -1057,10 +1069,12 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
         kn8[e] = knew[d0 + e];
     }
 #pragma unroll
-    for (int dd = 0; dd < 4; ++dd) vn4[dd] = vnew[rg + 32 * dd];
+    for (int dd = 0; dd < DD; ++dd) vnd[dd] = vnew[rg + RG * dd];
 
     float m_run = -INFINITY, l_run = 0.f;  // waves 0 and 1: the running statistics of head wv
-    float o0[4] = {0.f, 0.f, 0.f, 0.f}, o1[4] = {0.f, 0.f, 0.f, 0.f};
+    float o0[DD], o1[DD];
+#pragma unroll
+    for (int dd = 0; dd < DD; ++dd) o0[dd] = o1[dd] = 0.f;
     // masked keys (past pos) and the new key (= pos, when this split holds it) lie in the split's last chunk only:
     // TAIL instantiates the selects for it, the other chunks run without them
     auto chunk = [&](auto set, auto tailc, int c) __attribute__((always_inline)) {
@@ -1069,8 +1083,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
         const int cb = c * 64;  // the chunk's first key, as an offset in the split
         // scores of the chunk's keys for both heads
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int key = wv * 16 + it * 4 + (lane >> 4);
+        for (int it = 0; it < ITS; ++it) {
+            const int key = wv * 4 * ITS + it * 4 + (lane >> 4);
             float kf[8];
             unpack8h(kv4[SET][it], kf);
             if constexpr (tail) {
@@ -1104,7 +1118,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
             if (lane == 0) alpha_s[wv] = al;
         }
         __syncthreads();
-        // P V: thread t covers V^T rows rg + 32 dd and keys 8 sub .. + 7 of the chunk
+        // P V: thread t covers V^T rows rg + RG dd and keys 8 sub .. + 7 of the chunk
         float e0[8], e1[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -1113,14 +1127,14 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
         }
         const float al0 = alpha_s[0], al1 = alpha_s[1];
 #pragma unroll
-        for (int dd = 0; dd < 4; ++dd) {
+        for (int dd = 0; dd < DD; ++dd) {
             float vf[8];
             unpack8h(vv[SET][dd], vf);
             if constexpr (tail) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int key = cb + sub * 8 + e;
-                    vf[e] = key >= nkeys ? 0.f : (has_pos && key == jnew ? vn4[dd] : vf[e]);
+                    vf[e] = key >= nkeys ? 0.f : (has_pos && key == jnew ? vnd[dd] : vf[e]);
                 }
             }
             float a0 = 0.f, a1 = 0.f;
@@ -1159,7 +1173,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
     // reduce the 8 key groups (lanes differing in t & 7) and write the partials
     float* myp = part + (size_t(kvhead * 2) * S + s) * 130;  // head 2 kvhead + hh at + hh * S * 130
 #pragma unroll
-    for (int dd = 0; dd < 4; ++dd) {
+    for (int dd = 0; dd < DD; ++dd) {
         float a0 = o0[dd], a1 = o1[dd];
 #pragma unroll
         for (int o = 1; o < 8; o <<= 1) {
@@ -1167,8 +1181,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* qkv, const uint16
             a1 += __shfl_xor(a1, o, 64);
         }
         if (sub == 0) {
-            myp[2 + rg + 32 * dd] = a0;
-            myp[size_t(S) * 130 + 2 + rg + 32 * dd] = a1;
+            myp[2 + rg + RG * dd] = a0;
+            myp[size_t(S) * 130 + 2 + rg + RG * dd] = a1;
         }
     }
     if (wv < 2 && lane == 0) {
@@ -1824,7 +1838,7 @@ static void l_attn_dec(const PreparedDispatch& pd, void* const* p, hipStream_t s
     const bool even = w[17] != 0;
     const dim3 grid(dec_grid_splits(w[12], w[16], w[17]), w[11], w[15]);
 #define L_DEC(M)                                                                                                     \
-    hipLaunchKernelGGL(k_attn_dec<M>, grid, dim3(256), 0, s, (const float*)p[0], (const uint16_t*)p[1],             \
+    hipLaunchKernelGGL(k_attn_dec<M>, grid, dim3(M ? 512 : 256), 0, s, (const float*)p[0], (const uint16_t*)p[1],  \
                        (const uint16_t*)p[2], (const float*)p[3], (const float*)p[4], (uint16_t*)p[5],              \
                        (uint16_t*)p[6], (float*)p[7], (const uint32_t*)p[8], int(w[10]), int(w[11]), max_pos,       \
                        f32_of(w[13]), f32_of(w[14]) * kLog2e, even ? 0 : dec_chunks(w[16]))
