@@ -1432,7 +1432,8 @@ __global__ void k_convert_bf16_f16(const uint16_t* x, uint16_t* y, uint64_t n) {
 // ---------------------------------------------------------------- 30 argmax_rows_partial, 31 argmax_rows_final
 // argmaxRows over logits rows in two passes: block (b, r) reduces columns [b per, (b + 1) per) of row r to (max, lowest
 // index) or a NaN mark, then one wave per row merges the kArgmaxParts pairs: the lowest index of the row maximum, or
-// 0xFFFFFFFF for a row holding a NaN (CpuRef.argmaxRows semantics, CpuRef.fs:453-467).
+// 0xFFFFFFFF for a row holding a NaN (CpuRef.argmaxRows semantics, CpuRef.fs:453-467). The rows are x's rows row0 ..
+// row0 + rows - 1 (row0 = 0 for all of them; a forward that needs only its last row's id reduces that row alone).
 constexpr int kArgmaxParts = 64;
 
 struct ArgBest {
@@ -1454,7 +1455,7 @@ __device__ __forceinline__ ArgBest arg_wave(ArgBest a) {
     return a;
 }
 
-__global__ __launch_bounds__(256) void k_argmax_partial(const float* x, float* part, int rows, int cols) {
+__global__ __launch_bounds__(256) void k_argmax_partial(const float* x, float* part, int rows, int cols, int row0) {
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
     __shared__ int snan;
@@ -1463,7 +1464,7 @@ __global__ __launch_bounds__(256) void k_argmax_partial(const float* x, float* p
     __syncthreads();
     const int per = (cols + kArgmaxParts - 1) / kArgmaxParts;
     const int c0 = b * per, c1 = min(cols, c0 + per);
-    const float* xr = x + size_t(r) * cols;
+    const float* xr = x + size_t(row0 + r) * cols;
     ArgBest best{0.f, 0xFFFFFFFFu};
     bool nan = false;
     for (int c = c0 + t; c < c1; c += 256) {  // increasing per thread: the first of equal values is kept
@@ -1924,10 +1925,10 @@ static void l_convert(const PreparedDispatch& pd, void* const* p, hipStream_t s)
                        (const uint16_t*)p[0], (uint16_t*)p[1], n);
 }
 
-// 30 argmax_rows_partial: x, partials, rows, cols
+// 30 argmax_rows_partial: x, partials, rows, cols, row0
 static void l_argmax_partial(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     hipLaunchKernelGGL(k_argmax_partial, dim3(kArgmaxParts, pd.words[3]), dim3(256), 0, s, (const float*)p[0],
-                       (float*)p[1], int(pd.words[3]), int(pd.words[4]));
+                       (float*)p[1], int(pd.words[3]), int(pd.words[4]), int(pd.words[5]));
 }
 
 // 31 argmax_rows_final: partials, out, rows
@@ -2288,13 +2289,13 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 0, w[3], "convert_bf16_f16", "x");
                      need(c, 1, w[3], "convert_bf16_f16", "y");
                  }});
-    // 30 argmax_rows_partial: x, partials, rows, cols
+    // 30 argmax_rows_partial: x, partials, rows, cols, row0
     c.push_back({"argmax_rows_partial", "fast", {256, 1, 1}, false,
                  [](const uint32_t* w) { return Grid3{kArgmaxParts, w[3], 1}; },
-                 {TOK_R("x", DT(F32)), TOK_W("partials", DT(F32)), U32F("rows"), U32F("cols")},
+                 {TOK_R("x", DT(F32)), TOK_W("partials", DT(F32)), U32F("rows"), U32F("cols"), U32F("row0")},
                  [](const uint32_t* w, const uint32_t* c) {
                      if (w[3] < 1 || w[4] < 1) contract_fail("argmax_rows_partial: rows and cols must be at least 1");
-                     need(c, 0, int64_t(w[3]) * w[4], "argmax_rows_partial", "x");
+                     need(c, 0, (int64_t(w[5]) + w[3]) * w[4], "argmax_rows_partial", "x");
                      need(c, 1, int64_t(w[3]) * kArgmaxParts * 2, "argmax_rows_partial", "partials");
                  }});
     // 31 argmax_rows_final: partials, out, rows

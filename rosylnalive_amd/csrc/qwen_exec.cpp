@@ -667,17 +667,20 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
         CommandList* l2 = dev_.begin();
         dispatch(l2, "rmsnorm_rows_f16", {tk("x"), tk("model.norm.weight"), tk("h"), n, H, eps, uint32_t(r0)});
         dispatch(l2, "gemm_f32", {tk("h"), tk("embed.f16"), tk("logits"), n, V, H});
-        dispatch(l2, "argmax_rows_partial", {tk("logits"), tk("argmax.partials"), n, V});
-        dispatch(l2, "argmax_rows_final", {tk("argmax.partials"), tk("argmax"), n});
+        const bool last = r0 + int(n) == T;
+        if (last) {  // the forward returns the last row's id: reduce that row alone
+            dispatch(l2, "argmax_rows_partial", {tk("logits"), tk("argmax.partials"), 1, V, n - 1});
+            dispatch(l2, "argmax_rows_final", {tk("argmax.partials"), tk("argmax"), 1});
+        }
         uint64_t f2 = dev_.submit(l2);
         dev_.wait(f2);
         dev_.release(l2);
-        if (r0 + int(n) == T) {
+        if (last) {
             hip_check(hipEventRecord(e1, dev_.stream()), "event");
             hip_check(hipEventSynchronize(e1), "event");
+            download_tensor("argmax", &am, 4, 0);
         }
         if (logits) download_tensor("logits", logits + size_t(r0 - (T - lr)) * V, uint64_t(n) * V * 4);
-        download_tensor("argmax", &am, 4, uint64_t(n - 1) * 4);
     }
     float ms = 0;
     hip_check(hipEventElapsedTime(&ms, e0, e1), "event");

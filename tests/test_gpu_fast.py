@@ -449,6 +449,11 @@ def test_argmax_rows_split_matches_cpuref():
         ref = cpuref.argmax_rows(x)
         assert out.tolist() == ref.tolist(), (out, ref)
         assert out[1] == 5 and out[2] == 0xFFFFFFFF and out[3] == 0 and out[4] == 0 and out[5] == cols - 1
+        # row0: rows row0 .. row0 + n - 1 alone (the forward reduces only its last row)
+        for row0, n in ((rows - 1, 1), (5, 2), (0, 1)):
+            sub = s.run_list([("argmax_rows_partial", dict(x="x", partials="part", rows=n, cols=cols, row0=row0)),
+                              ("argmax_rows_final", dict(partials="part", out="out", rows=n))], ["out"])["out"][:n]
+            assert sub.tolist() == ref[row0:row0 + n].tolist(), (row0, n, sub)
     finally:
         s.close()
 
