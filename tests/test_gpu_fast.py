@@ -478,8 +478,9 @@ def test_gemm_skinny(m, n, k):
         s.close()
 
 
-def test_gemm_skinny_swiglu():
-    m, inter, k = 11, 3072, 1024
+@pytest.mark.parametrize("m,inter,k", [(11, 3072, 1024), (16, 6144, 2048), (3, 100, 1024)])
+def test_gemm_skinny_swiglu(m, inter, k):
+    """Each block pairs 16 gate columns with the matching 16 up columns; inter 100 ends in a partial block."""
     r = np.random.default_rng(21)
     a = f16(r.standard_normal((m, k)))
     w = f16(r.standard_normal((2 * inter, k)) * 0.05)
