@@ -2190,7 +2190,8 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 2, int64_t(w[5]) * w[6], "gemv_norm_dec", "w");
                      need(c, 3, w[5], "gemv_norm_dec", "y");
                  }});
-    // 21 attention_decode_f16
+    // 21 attention_decode_f16 (the catalog's block size is the one-chunk form's; the multi-chunk form, chunks > 1 or
+    // splits set, launches 512 threads)
     c.push_back({"attention_decode_f16", "fast", {256, 1, 1}, false,
                  [](const uint32_t* w) { return Grid3{dec_grid_splits(w[12], w[16], w[17]), w[11], w[15]}; },
                  {TOK_R("qkv", DT(F32)), TOK_R("q_norm", DT(BF16)), TOK_R("k_norm", DT(BF16)),
