@@ -478,19 +478,25 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             } else {
                 chunk(C0{}, Tail{}, c);
             }
-            // reduce the four key groups of each dim and write the partials of both heads
+            // reduce the four key groups of each dim, then the partial rows of both heads, (max, sum, out[128]) and
+            // the padding, each written whole by one wave (wave hh: head 2 hk + hh) from LDS (qs and red are free
+            // after the chunks)
             o0 = quad4_sum(o0);
             o1 = quad4_sum(o1);
-            uint64_t* p0 = xl + X.part + size_t(2 * hk * S + s) * 130;
-            uint64_t* p1 = p0 + size_t(S) * 130;
             if ((t & 3) == 0) {
-                xstore(p0 + 2 + (t >> 2), o0, tag);
-                xstore(p1 + 2 + (t >> 2), o1, tag);
+                qs[0][t >> 2] = o0;
+                qs[1][t >> 2] = o1;
             }
             if (w < 2 && lane == 0) {
-                uint64_t* pw = w == 0 ? p0 : p1;
-                xstore(pw, m_run, tag);
-                xstore(pw + 1, l_run, tag);
+                red[2 * w] = m_run;
+                red[2 * w + 1] = l_run;
+            }
+            lds_barrier();
+            if (w < 2) {
+                uint64_t* pr = xl + X.part + size_t((2 * hk + w) * S + s) * kPartStride;
+#pragma unroll
+                for (int i = lane; i < kPartStride; i += 64)
+                    xstore(pr + i, i < 2 ? red[2 * w + i] : i < 130 ? qs[w][i - 2] : 0.f, tag);
             }
         }
 
@@ -505,7 +511,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                [&](int i) {
                    const int j = i / per_item, r = i - j * per_item, sp = r / 10, k = r - sp * 10;
                    const int it = b + G * j, hq = it >> 4, d8 = (it & 15) * 8;
-                   return src + size_t(hq * S + sp) * 130 + (k < 2 ? k : d8 + k);
+                   return src + size_t(hq * S + sp) * kPartStride + (k < 2 ? k : d8 + k);
                },
                items * per_item, tag, vec, hdr, 3, s_fail, wait_ticks);
             if (s_fail) return;

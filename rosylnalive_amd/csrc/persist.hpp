@@ -16,6 +16,9 @@ constexpr int kVecMax = 4096;    // floats of the LDS vector a stage gathers its
 // workgroups of XCD r (blockIdx % 8 = r, the dispatch order) poll copy r, so no copy is polled by more than 1/8 of the
 // grid.
 constexpr int kReplicas = 8;
+// 8-byte entries per (query head, split) attention partial row: (max, sum, out[128]) padded to whole 128-byte lines, so
+// one wave writes every line of a row whole (lines written in part by several waves cost a read-modify-write each)
+constexpr int kPartStride = 144;
 
 // The one instantiated shape family: per-lane and per-wave work counts of every stage, derived from the model sizes
 // and the grid. NCH: 512-wide chunks of the hidden vector per lane; RA: q|k|v rows per wave; NCC: chunks per wave of
@@ -28,7 +31,7 @@ struct Shape {
 };
 
 // The exchange area. 8-byte entries, (tag << 32) | value bits, per layer: the q|k|v projection and the attention
-// partials per (query head, split) as (max, sum, out[128]); then the lm_head partials (value, index) per workgroup.
+// partials per (query head, split) as (max, sum, out[128]) in rows of kPartStride entries; then the lm_head partials (value, index) per workgroup.
 // 4-byte entries per layer, value bits with the lowest mantissa bit replaced by the launch parity, kReplicas copies
 // each (copy r at + r * its length): the combined attention output o, x after o_proj, the SwiGLU output, x after
 // down_proj. The 4-byte area follows the 8-byte one.
@@ -42,7 +45,7 @@ struct XLayout {
         const int S = blocks / kvh;
         qkv = 0;
         part = (qh + 2 * kvh) * 128;
-        per_layer = part + qh * S * 130;
+        per_layer = part + qh * S * kPartStride;
         o = 0;
         x1 = o + kReplicas * qh * 128;
         a = x1 + kReplicas * hidden;
