@@ -225,3 +225,14 @@ def test_synthetic_inputs_are_deterministic_normals():
     assert abs(a.mean()) < 0.01 and abs(a.std() - 1) < 0.01
     # a prefix of a longer draw is the shorter draw: element values depend only on (seed, stream, index)
     assert synthetic_normal_f32(7, "probe", (1001,)).tobytes() == a[:1001].tobytes()
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 exits with status 2 and says so, before touching a device."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2, (r.returncode, r.stdout, r.stderr)
+    assert "one GPU" in (r.stdout + r.stderr)
+    assert r.stdout.strip() == ""  # no JSON line
