@@ -641,7 +641,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
 
     // ---------------------------------------------------------------- lm_head over rows [r0, r1), then the argmax
     const int V = a.vocab, per = (V + G - 1) / G, r0 = b * per, r1 = min(V, r0 + per);
-    u32x4 ra[4][NCH], rb4[4][NCH], nf[NCH];
+    u32x4 ra[4][NCH], rb4[4][NCH], rc4[4][NCH], nf[NCH];
     auto load4 = [&](u32x4 (&dst)[4][NCH], int row) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -650,7 +650,11 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             for (int c = 0; c < NCH; ++c) dst[r][c] = ld16(er + 512 * c);
         }
     };
+    // wave w visits rows r0 + 4 w + 32 j, four at a time, through three register sets (the next two sets in flight
+    // while one is reduced); the first two are issued before the wait for x
+    constexpr int RS = 4 * kWaves;  // rows between a wave's consecutive sets
     load4(ra, r0 + 4 * w);
+    load4(rb4, r0 + 4 * w + RS);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) nf[c] = ld16(a.final_norm + 512 * c + 8 * lane);
     {
@@ -680,12 +684,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             }
         }
     };
-    for (int row = r0 + 4 * w; row < r1; row += 8 * kWaves) {
-        const bool second = row + 4 * kWaves < r1;
-        if (second) load4(rb4, row + 4 * kWaves);
+    for (int row = r0 + 4 * w; row < r1; row += 3 * RS) {  // sets ra, rb4, rc4 hold rows row, + RS, + 2 RS
+        if (row + 2 * RS < r1) load4(rc4, row + 2 * RS);
         proc(ra, row);
-        if (row + 8 * kWaves < r1) load4(ra, row + 8 * kWaves);
-        if (second) proc(rb4, row + 4 * kWaves);
+        if (row + 3 * RS < r1) load4(ra, row + 3 * RS);
+        if (row + RS < r1) proc(rb4, row + RS);
+        if (row + 4 * RS < r1) load4(rb4, row + 4 * RS);
+        if (row + 2 * RS < r1) proc(rc4, row + 2 * RS);
     }
     if (lane == 0) {
         lmv[w] = best;
