@@ -29,6 +29,7 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 FP32_PEAK_TFLOPS = 157.3
 GEMV_SWIGLU_TRAFFIC_BYTES = 12675736  # measured HBM bytes per gemv_swiglu_dec launch at the 0.6B shape
 PERSIST_TRAFFIC_BYTES = 1306827662    # measured HBM bytes per decode_step_persistent launch at context 393..424
+ROOFLINE_POS0 = 392                   # the roofline launches run at context ROOFLINE_POS0 + 1 .. ROOFLINE_POS0 + 32
 CPU_DECODE_STEPS = 128                # the bounded CPU decode sample (about 10 s on 16 host cores)
 
 
@@ -47,10 +48,11 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_configs(seed, cfg06, w06, threads):
+def cpu_configs(seed, cfg06, w06, threads, e_sample):
     """The oracle timed on the other workloads of the hot path (wall clock, one run each): the tiny model's whole
     run, the isolated attention at T = 2048, the 0.6B prefill of 512 tokens with every logit, and a stated sample of
-    the batched 1.7B decode (its 15 GB cache does not fit a CPU run: one sequence at context 8192, 2 steps)."""
+    the batched 1.7B decode (its 15 GB cache does not fit a CPU run: sequence 0 over the device's own caches at
+    context 8192, 2 steps, whose greedy ids are compared with the device's)."""
     from oracle import cpuref
     from rosylnalive_amd.qwen import QwenConfig, inv_freq_bits, synthetic_ids, synthetic_normal_f32, synthetic_weights
     res = {"cores": threads, "kind": "port"}
@@ -90,24 +92,29 @@ def cpu_configs(seed, cfg06, w06, threads):
     res["C_prefill_512_tok_s"] = round(512 / tc, 1)
     res["C_prefill_512_gflops"] = round(640588005376 / tc / 1e9, 1)
     del oc
-    # E (sample): the 1.7B shape, one sequence whose cache holds 8192 positions of bf16-valued N(0, 1), 2 steps
-    ce = QwenConfig.qwen3_1_7b(max_pos=8192 + 64)
-    we = synthetic_weights(ce, seed=seed)
-    cos, sin = cpuref.rope_table(inv_freq_bits(128), ce.max_pos)
-    oe = cpuref.QwenOracle(ce.oracle_dict(), we, cos, sin)
-    kc, vc = oe.new_cache()
-    for name, arr in (("k", kc), ("v", vc)):
-        vals = synthetic_normal_f32(seed, f"bench/cpu_cache/{name}", (ce.layers, 8192, ce.kv_heads * ce.head_dim))
-        arr[:, :8192] = cpuref.bf16_widen(cpuref.bf16_narrow(vals))
-    tok = np.array([int(synthetic_ids(seed, "bench/batch16", 1, ce.vocab)[0])], np.int32)
-    t0 = time.perf_counter()
-    for s_ in range(2):
-        lg = oe.forward((kc, vc), 8192 + s_, tok)
-        tok = np.array([int(np.argmax(lg[-1]))], np.int32)
-    te = time.perf_counter() - t0
-    res["E_sample"] = "1 sequence x 2 steps at context 8193..8194 (of the 16-sequence, 64-step workload)"
-    res["E_sample_s"] = round(te, 3)
-    res["E_tok_s_per_sequence"] = round(2 / te, 3)
+    # E (sample): the 1.7B shape, sequence 0 over the 8192 cached positions the device holds (N(0, 1) fp16), 2 steps
+    if e_sample is not None:
+        ce = e_sample["cfg"]
+        we = synthetic_weights(ce, seed=seed)
+        cos, sin = cpuref.rope_table(inv_freq_bits(128), ce.max_pos)
+        oe = cpuref.QwenOracle(ce.oracle_dict(), we, cos, sin)
+        kc, vc = oe.new_cache()
+        for l_ in range(ce.layers):
+            kc[l_, :8192] = e_sample["k"][l_]
+            vc[l_, :8192] = e_sample["v"][l_]
+        tok = np.array([e_sample["tok"]], np.int32)
+        ids = []
+        t0 = time.perf_counter()
+        for s_ in range(2):
+            lg = oe.forward((kc, vc), 8192 + s_, tok)
+            tok = np.array([int(np.argmax(lg[-1]))], np.int32)
+            ids.append(int(tok[0]))
+        te = time.perf_counter() - t0
+        res["E_sample"] = ("sequence 0 x 2 steps at context 8193..8194 over the device's caches (of the 16-sequence, "
+                           "64-step workload)")
+        res["E_sample_s"] = round(te, 3)
+        res["E_tok_s_per_sequence"] = round(2 / te, 3)
+        res["E_ids_equal_device"] = ids == e_sample["ids"]
     return res
 
 
@@ -159,6 +166,8 @@ def main():
     model.decode_run(args.steps)
     wall = time.perf_counter() - t1
     dev_ms = model.last_ms()
+    # the greedy ids of the run (the prefill's, then every decode step's), checked against the oracle's below
+    gpu_ids = [int(first)] + model.decode_ids(args.warmup + args.steps).tolist()
     tok_s = args.steps / (dev_ms / 1e3)
     step_bytes = sum(weight_bytes + kv_bytes(ctx0 + s + 1) for s in range(args.steps))
     log(f"decode: {args.steps} steps in {dev_ms:.2f} ms device ({wall * 1e3:.2f} ms wall): {tok_s:.1f} tok/s, "
@@ -173,9 +182,12 @@ def main():
     persistent = model.persistent_decode()
     pk = None
     if persistent:
+        # at a fixed context, 393..424, whatever --steps is (the context the traffic profile was taken at): a prefill
+        # of 392 tokens writes the caches the launches read
         reps = 32
-        pos0 = ctx0 + args.steps
-        model.decode_set(5, pos0)
+        pos0 = ROOFLINE_POS0
+        _, nxt = model.forward(synthetic_ids(args.seed, "bench/roofline", pos0, V), 0, logits_rows=1)
+        model.decode_set(int(nxt), pos0)
         cl = backend.begin()
         tm = cl.begin_timer("gpu.decode_step_persistent")
         for _ in range(reps):
@@ -235,7 +247,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "bf16 weights; fp16 MFMA operands and KV cache; fp32 accumulate",
         "data": "synthetic (random N(0,0.02) bf16 weights, norm weights 1, uniform token ids; seed %d)" % args.seed,
         "config": {
             "workload": "Qwen3-0.6B-shaped greedy decode with KV cache, batch 1, prompt 128, then %d warmup + %d timed "
@@ -282,6 +294,7 @@ def main():
         },
     }
 
+    e_sample = None
     if not args.no_extras:
         # 512-token prefill with every logit row (all 512 x 151936 logits)
         ids = synthetic_ids(args.seed, "bench/prefill512", 512, V)
@@ -363,7 +376,7 @@ def main():
         del w_e
         m_e.fill_cache_random(args.seed, 8192)
         toks = synthetic_ids(args.seed, "bench/batch16", 16, cfg_e.vocab)
-        m_e.decode_batch(toks, [8192] * 16, 2)
+        e_ids = m_e.decode_batch(toks, [8192] * 16, 2)
         m_e.decode_batch(toks, [8192] * 16, 64)
         e_ms = m_e.last_ms()
         e_w = cfg_e.param_count() * 2
@@ -377,6 +390,10 @@ def main():
             "workload": "Qwen3-1.7B shape, 16 sequences, context 8193..8256, greedy, skinny MFMA GEMMs over fp16 "
                         "weight copies"}
         log("decode batch 16 (1.7B, 8K):", out["decode_batch16_1.7b_8k"])
+        if not args.no_cpu:  # sequence 0's caches, for the oracle's sample of this workload
+            e_sample = {"cfg": cfg_e, "tok": int(toks[0]), "ids": e_ids[:, 0].tolist(),
+                        "k": [m_e.read_cache(l, "k", 0, 8192, seq=0) for l in range(cfg_e.layers)],
+                        "v": [m_e.read_cache(l, "v", 0, 8192, seq=0) for l in range(cfg_e.layers)]}
         m_e.close()
         be_e.close()
 
@@ -396,12 +413,22 @@ def main():
         lg = orc.forward(cache, 0, prompt)
         t_pre = time.perf_counter() - t2
         nxt = int(np.argmax(lg[-1]))
+        cpu_ids = [nxt]
         t3 = time.perf_counter()
         steps = CPU_DECODE_STEPS
         for s_ in range(steps):
             lg = orc.forward(cache, 128 + s_, np.array([nxt], np.int32))
             nxt = int(np.argmax(lg[-1]))
+            cpu_ids.append(nxt)
         t_dec = time.perf_counter() - t3
+        # the oracle's greedy ids against the device's over the ids both runs produced
+        n_cmp = min(len(gpu_ids), len(cpu_ids))
+        same = [a == b for a, b in zip(gpu_ids[:n_cmp], cpu_ids[:n_cmp])]
+        prefix = same.index(False) if False in same else n_cmp
+        out["ids_vs_oracle"] = {"compared": n_cmp, "equal": int(sum(same)), "identical_prefix": prefix,
+                                "what": "greedy ids of the headline decode (the prefill's id, then each step's) against "
+                                        "the oracle's greedy ids from the same prompt"}
+        log("greedy ids vs oracle:", out["ids_vs_oracle"])
         out["cpu_baseline"] = {"value": round(steps / t_dec, 4), "unit": "tok/s (batch-1 decode)", "cores": threads,
                                "kind": "port", "cpu": cpu_model,
                                "sample": f"oracle (CpuRef F32 in C) on the same weights: 128-token prefill "
@@ -409,7 +436,7 @@ def main():
                                          f"context 129..{128 + steps} ({t_dec:.2f} s)"}
         log("cpu baseline:", out["cpu_baseline"])
         if not args.no_extras:
-            out["cpu_configs"] = cpu_configs(args.seed, cfg, weights, threads)
+            out["cpu_configs"] = cpu_configs(args.seed, cfg, weights, threads, e_sample)
             log("cpu configs:", out["cpu_configs"])
 
     model.close()

@@ -207,6 +207,7 @@ def argmax_rows(x: np.ndarray) -> np.ndarray:
 
 
 def softmax_rows(x: np.ndarray) -> np.ndarray:
+    """CpuRef.softmax (CpuRef.fs:405-420) with Rows.softmax (Rows.fs:101-110): a NaN anywhere makes the row NaN."""
     s, _, _ = _mode(x.dtype)
     x = np.ascontiguousarray(x)
     y = np.empty_like(x)
@@ -215,6 +216,7 @@ def softmax_rows(x: np.ndarray) -> np.ndarray:
 
 
 def logsumexp_rows(x: np.ndarray) -> np.ndarray:
+    """Rows.logSumExp (Rows.fs:112-135) per row: an infinite row maximum is the answer, a NaN gives NaN."""
     s, _, npt = _mode(x.dtype)
     x = np.ascontiguousarray(x)
     y = np.empty(x.shape[0], npt)

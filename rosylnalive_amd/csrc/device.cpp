@@ -484,7 +484,12 @@ const Completion& Device::wait(uint64_t fence) {
     auto d = done_.find(fence);
     if (d != done_.end()) return d->second;
     auto it = pending_.find(fence);
-    if (it == pending_.end()) contract_fail("submission %llu was never made on this backend", (unsigned long long)fence);
+    if (it == pending_.end()) {
+        if (fence >= 1 && fence < next_fence_)
+            contract_fail("submission %llu completed and its completion was dropped: the backend keeps the last %zu",
+                          (unsigned long long)fence, kKeptCompletions);
+        contract_fail("submission %llu was never made on this backend", (unsigned long long)fence);
+    }
     Pending& p = it->second;
     hipError_t e = hipEventSynchronize(p.done);
     if (e != hipSuccess) {
@@ -503,6 +508,10 @@ const Completion& Device::wait(uint64_t fence) {
     }
     (void)hipEventDestroy(p.done);
     pending_.erase(it);
+    // Waiting again returns the same completion (gpu-backend.md, IGpuBackend.Wait), for the most recent
+    // kKeptCompletions submissions waited on; older ones are dropped, so a decode loop that submits and waits once per
+    // token holds bounded host memory.
+    while (done_.size() >= kKeptCompletions) done_.erase(done_.begin());
     return done_.emplace(fence, std::move(c)).first->second;
 }
 

@@ -172,7 +172,12 @@ class Device {
         CommandList* owned;  // one-shot list to free after completion
     };
     std::map<uint64_t, Pending> pending_;
-    std::map<uint64_t, Completion> done_;
+    std::map<uint64_t, Completion> done_;  // the last kKeptCompletions waited on, by fence
+
+  public:
+    static constexpr size_t kKeptCompletions = 1024;
+
+  private:
     std::vector<std::unique_ptr<CommandList>> lists_;
     // dispatch timing (TimeDispatches)
     std::vector<std::pair<hipEvent_t, hipEvent_t>> dispatch_events_;

@@ -605,7 +605,12 @@ uint32_t QwenExec::forward_fp32(int pos0, int T, float* logits, int lr) {
 // 512 blocks (two per CU), within the partials tensor (2 max_tokens rows) and with k a multiple of 64 per split. Not 8:
 // at 512 rows (64 tiles) 8 splits leave each block 4-6 k steps and the add pass 8 partials to read, and the 512-token
 // forward measured 2.53 ms against 2.40 ms with 4.
+// Row widths residual_add_norm (one wave per row, 256-column steps) takes; other hidden sizes run the residual GEMM
+// and a separate norm.
+static bool add_norm_width(uint32_t n) { return n == 256 || n == 512 || n == 1024 || n == 2048 || n == 4096; }
+
 static uint32_t resid_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t max_tokens) {
+    if (!add_norm_width(n)) return 1;
     const uint64_t tiles = uint64_t((n + 63) / 64) * ((m + 127) / 128);
     uint32_t s = 1;
     while (s < 4 && tiles * s < 512 && 2 * s * m <= 2 * max_tokens && k % (128 * s) == 0) s *= 2;
@@ -764,7 +769,7 @@ void QwenExec::record_decode_batch(CommandList* l) {
     // block per 16 columns alone leaves half the CUs idle at hidden 2048) into partials, then one pass that adds them
     // and normalises; or, when k does not split in 1024-multiples, the residual GEMM and the norm
     auto residual_norm = [&](const std::string& a, const std::string& wname, uint32_t K, uint32_t nw) {
-        if (K % 2048 == 0) {
+        if (K % 2048 == 0 && add_norm_width(H)) {
             dispatch(l, "gemm_residual_split", {tk(a), tk(wname), tk("resid.partials"), B, H, K, 2});
             dispatch(l, "residual_add_norm", {tk("dec.x"), tk("resid.partials"), nw, tk("dec.h16"), B, H, 2, eps});
         } else {
@@ -836,6 +841,7 @@ void QwenExec::run_decode_steps(int steps) {
         if (int64_t(st[size_t(b)]) + steps > cfg_.max_pos)
             arg_fail("%d decode steps from position %u pass max_pos %d", steps, st[size_t(b)], cfg_.max_pos);
     if (!decode_list_) record_decode_fast();
+    sync_f16();  // the batched step's skinny GEMMs read the fp16 copies: weights set since the last forward
     hipEvent_t e0, e1;
     hip_check(hipEventCreate(&e0), "event");
     hip_check(hipEventCreate(&e1), "event");

@@ -12,6 +12,7 @@ from gpu_session import Session, written_everywhere
 from oracle import cpuref, metrics
 from rosylnalive_amd.gpu_core import (ArgBlock, DType, GpuContractException, HeapLayout, HipBackend,
                                       HipBackendProvider, TensorFlags, TensorTable)
+from rosylnalive_amd.qwen import QWEN3_INV_FREQ_HD128
 
 pytestmark = pytest.mark.gpu
 
@@ -82,6 +83,19 @@ def test_once_only_rules_and_denormal_probe():
         assert (got == 2 * np.arange(16, dtype=np.float32)).all()
         with pytest.raises(GpuContractException):
             heap.upload(0, 0, np.zeros(4, np.uint8))  # slot 0 is the table
+        # a loop that submits and waits once per step holds bounded host memory: the last 1024 completions stay
+        # waitable, older ones are dropped with a clear error
+        fences = []
+        for _ in range(1030):
+            cl = b.begin()
+            cl.dispatch("scale_f32", ArgBlock.encode("scale_f32", x=1, y=1, n=16, a=1.0))
+            fences.append(b.submit(cl))
+            assert b.wait(fences[-1]).dispatches == 1
+        assert b.wait(fences[-1]).dispatches == 1 and b.wait(fences[-1024]).dispatches == 1
+        with pytest.raises(GpuContractException, match="dropped"):
+            b.wait(s1)
+        with pytest.raises(GpuContractException, match="never made"):
+            b.wait(fences[-1] + 1)
     finally:
         b.close()
 
@@ -249,5 +263,34 @@ def test_attention_gqa_causal(rows, past, qh, kvh, hd):
         r32 = cpuref.attention(q, k, v, qh, kvh, hd, past, scale)
         r64 = cpuref.attention(q.astype(np.float64), k, v, qh, kvh, hd, past, float(scale))
         check_relative(y, r32, r64, "attention")
+    finally:
+        s.close()
+
+
+def test_attention_gqa_causal_isolated_op_2048_fp32():
+    """The isolated GQA causal prefill attention at full size, fp32 leg: batch 1, seq 2048, 16 Q heads, 8 KV heads,
+    head_dim 128; Q, K, V ~ N(0, 1) from a seed, per-head RMSNorm (weights 1) and RoPE (theta 1e6, positions 0..2047)
+    applied to Q and K first; scale 1/sqrt(128), causal mask. Within KernelBounds of CpuRef F32 against F64."""
+    T, qh, kvh, hd = 2048, 16, 8, 128
+    r = rng(2048)
+    q = r.standard_normal((T, qh * hd)).astype(np.float32)
+    k = r.standard_normal((T, kvh * hd)).astype(np.float32)
+    v = r.standard_normal((T, kvh * hd)).astype(np.float32)
+    ones = np.full(hd, 0x3F80, np.uint16)
+    cos, sin = cpuref.rope_table(np.array(QWEN3_INV_FREQ_HD128, np.uint32), T)
+    q = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q.reshape(-1, hd), ones, 1e-6).reshape(T, -1), qh, 0)
+    k = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(k.reshape(-1, hd), ones, 1e-6).reshape(T, -1), kvh, 0)
+    scale = cpuref.attention_scale(hd, np.float32)
+    s = Session({"q": (F32, q.shape, 0, q), "k": (F32, k.shape, 0, k), "v": (F32, v.shape, 0, v),
+                 "y": (F32, q.shape, 0, None)})
+    try:
+        y = s.run("attention_gqa_causal", ["y"], q="q", k="k", v="v", y="y", rows=T, q_row0=0, past=0,
+                  q_heads=qh, kv_heads=kvh, head_dim=hd, scale=float(scale))["y"]
+        assert written_everywhere(y)
+        r32 = cpuref.attention(q, k, v, qh, kvh, hd, 0, scale)
+        r64 = cpuref.attention(q.astype(np.float64), k, v, qh, kvh, hd, 0, float(scale))
+        chk = check_relative(y, r32, r64, "attention 2048")
+        print(f"attention_gqa_causal T 2048 fp32: relL2 vs F64 {chk['measured']:.3g} (bound {chk['bound']:.3g})",
+              flush=True)
     finally:
         s.close()

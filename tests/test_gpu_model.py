@@ -341,3 +341,37 @@ def test_persistent_decode_aborts_past_its_wait_bound_and_recovers(fast_setup):
     ol = orc.forward(orc.new_cache(), 0, np.concatenate([prompt, [tok]]).astype(np.int32))[-1:]
     assert metrics.max_abs(lg, ol) <= 2e-2
     assert int(np.argmax(lg[0])) == int(np.argmax(ol[0])) == int(m.decode_ids(1)[0])
+
+
+def test_fast_hidden_1536_prefill_and_decode_match_oracle():
+    """A hidden size outside the add-and-norm pass's row widths (1536): the prefill residual GEMMs run unsplit with
+    a separate norm, and decode runs the per-stage list (the persistent step covers hidden 1024). Prefill logits and
+    teacher-forced decode steps against CpuRef F32."""
+    cfg = QwenConfig(2, 1536, 16, 8, 128, 4096, 4096, 256)
+    w = synthetic_weights(cfg, seed=15)
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), cfg.max_pos)
+    orc = cpuref.QwenOracle(cfg.oracle_dict(), w, cos, sin)
+    b = HipBackend(0)
+    m = QwenModel(b, cfg, mode="fast", max_tokens=128)
+    try:
+        m.load_weights(w)
+        assert not m.persistent_decode()
+        ids = synthetic_ids(15, "h1536/prompt", 100, cfg.vocab)
+        cont = synthetic_ids(15, "h1536/cont", 8, cfg.vocab)
+        ol = orc.forward(orc.new_cache(), 0, np.concatenate([ids, cont]).astype(np.int32))
+        lg, am = m.forward(ids, 0)
+        err = metrics.max_abs(lg, ol[:100])
+        assert err <= 2e-2 and metrics.top1_agreement(lg, ol[:100]) >= 0.99, err
+        assert am == int(np.argmax(lg[-1]))
+        worst = 0.0
+        for i, tok in enumerate(cont):
+            m.decode_set(int(tok), 100 + i)
+            m.decode_run(1)
+            d = m.read_logits(1)
+            worst = max(worst, metrics.max_abs(d, ol[100 + i:101 + i]))
+            assert int(m.decode_ids(1)[0]) == int(np.argmax(d[0]))
+        print(f"hidden 1536: prefill max-abs {err:.4g}, decode worst max-abs {worst:.4g}", flush=True)
+        assert worst <= 2e-2
+    finally:
+        m.close()
+        b.close()

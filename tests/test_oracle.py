@@ -415,3 +415,72 @@ def test_metrics_kernel_bound_vectors():
     assert chk["passed"] and chk["measured"] == 1.0
     chk = metrics.check_relative(np.array([0.5, 0.0]), np.array([1.0, 1e-39]), np.array([1.0, 1e-39]))
     assert not chk["passed"]
+
+
+# ---------------------------------------------------------------- softmax, logSumExp and KL (Rows.fs:84-135,275-292)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_softmax_logsumexp_kl_known_answers(dt):
+    """CpuRefTests.fs:168-180: softmax (0, 0) = (1/2, 1/2); logSumExp (0, 0) = log 2; a NaN spreads over the softmax
+    row; KL((0, 0) || (0, log 3)) = log(4/3) / 2."""
+    y = cpuref.softmax_rows(np.array([[0.0, 0.0]], dt))
+    assert y[0].tolist() == [0.5, 0.5]
+    assert cpuref.logsumexp_rows(np.array([[0.0, 0.0]], dt))[0] == dt(np.log(2.0))
+    assert np.isnan(cpuref.softmax_rows(np.array([[1.0, np.nan]], dt))).all()
+    kl = cpuref.kl_rows(np.array([[0.0, 0.0]], dt), np.array([[0.0, np.log(3.0)]], dt))[0]
+    tol = (1e-15, 1e-14) if dt == np.float64 else (1e-7, 1e-6)
+    assert abs(float(kl) - 0.5 * np.log(4.0 / 3.0)) <= tol[0] + tol[1] * 0.5 * np.log(4.0 / 3.0)
+
+
+def test_logsumexp_and_kl_with_infinite_logits():
+    """CpuRefTests.fs:182-211: an infinite row maximum is the answer; a NaN beats +inf; a logit masked in both rows
+    adds nothing to KL; P with mass where Q has none gives +inf; a NaN spreads."""
+    lse = lambda r, dt=np.float64: cpuref.logsumexp_rows(np.array([r], dt))[0]
+    assert lse([1.0, np.inf]) == np.inf
+    assert lse([-np.inf, -np.inf]) == -np.inf
+    assert lse([-np.inf, 0.0], np.float32) == 0.0
+    assert np.isnan(lse([np.inf, np.nan]))
+    assert np.isnan(lse([np.nan, -np.inf]))
+    kl = lambda p, q, dt=np.float64: cpuref.kl_rows(np.array([p], dt), np.array([q], dt))[0]
+    p, q = [1.0, -np.inf, 0.0], [1.0, -np.inf, 0.5]
+    finite = kl(p, q)
+    assert np.isfinite(finite) and finite > 0.0
+    assert finite == kl([1.0, 0.0], [1.0, 0.5])
+    # Metrics.klRow (candidate q, reference p): sum_i P_i (log P_i - log Q_i) over the unmasked entries, in float64
+    lp = np.array([1.0, 0.0]) - np.log(np.exp(1.0) + np.exp(0.0))
+    lq = np.array([1.0, 0.5]) - np.log(np.exp(1.0) + np.exp(0.5))
+    closed = float(np.sum(np.exp(lp) * (lp - lq)))
+    assert abs(finite - closed) <= 1e-15 + 1e-13 * closed
+    assert np.isfinite(kl(p, q, np.float32))
+    assert kl([0.0, 0.0], [0.0, -np.inf]) == np.inf
+    assert np.isnan(kl([0.0, np.nan], [0.0, 0.0]))
+
+
+def test_softmax_logsumexp_kl_against_float64_closed_forms():
+    """Random rows with a wide logit spread (a shifted maximum, large and small entries) against the textbook forms
+    in float64: softmax rows sum to 1 and equal exp(x - max) / sum; logSumExp equals scipy's; KL equals
+    sum p (log p - log q), is 0 for identical rows and changes under a swap of P and Q (the operand order is pinned)."""
+    from scipy.special import logsumexp
+
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((6, 300)) * 8.0 + 40.0
+    q = x + rng.standard_normal((6, 300))
+    for dt, tol in ((np.float64, 1e-13), (np.float32, 2e-5)):
+        xs, qs = x.astype(dt), q.astype(dt)
+        xd = xs.astype(np.float64)
+        ref = np.exp(xd - xd.max(axis=1, keepdims=True))
+        ref /= ref.sum(axis=1, keepdims=True)
+        sm = cpuref.softmax_rows(xs).astype(np.float64)
+        assert np.max(np.abs(sm - ref)) <= tol * ref.max()
+        assert np.allclose(sm.sum(axis=1), 1.0, atol=10 * tol)
+        assert np.allclose(cpuref.logsumexp_rows(xs), logsumexp(xd, axis=1), rtol=tol, atol=0)
+        qd = qs.astype(np.float64)
+        lp = xd - logsumexp(xd, axis=1, keepdims=True)
+        lq = qd - logsumexp(qd, axis=1, keepdims=True)
+        klr = np.sum(np.exp(lp) * (lp - lq), axis=1)
+        kl = cpuref.kl_rows(xs, qs).astype(np.float64)
+        assert np.allclose(kl, klr, rtol=50 * tol, atol=1e-12 if dt == np.float64 else 5e-5)
+        assert np.all(cpuref.kl_rows(xs, xs) == 0)
+        swapped = cpuref.kl_rows(qs, xs).astype(np.float64)
+        assert np.max(np.abs(swapped - kl)) > 1e-3
