@@ -120,6 +120,14 @@ int lrm_hip_dispatch(lrm_hip_list *l, uint32_t kernel, const uint32_t words[32])
  * each dispatch after the previous one): it runs on a second stream after everything recorded before it, and the next
  * lrm_hip_barrier, or the end of the list, waits for it. For read-only side work such as cache prefetch. */
 int lrm_hip_dispatch_overlapped(lrm_hip_list *l, uint32_t kernel, const uint32_t words[32]);
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc): records attention_decode_f16 followed by attention_combine (f32 output) with the
+ * split partials in the library's static scratch, a 4 MiB array each GPU holds from the library's load until the
+ * process ends, instead of a partials tensor of the caller's heap. words: the attention_decode_f16 argument block with
+ * its partials word 0; y: the combine's output token, f32 [batch, q_heads * 128]. Raises LRM_E_CONTRACT when
+ * batch * q_heads * splits * 130 * 4 bytes exceed the scratch. Records nothing that allocates; calls that overlap on one
+ * GPU (lists from two backends of that GPU) share the scratch and race. */
+int lrm_hip_dispatch_decode_attention_static(lrm_hip_list *l, const uint32_t words[32], uint32_t y);
 /* ICommandList.Barrier: joins the overlapped dispatches (the in-order dispatches need nothing). */
 int lrm_hip_barrier(lrm_hip_list *l);
 int lrm_hip_copy(lrm_hip_list *l, int src_slot, uint64_t src_offset, int dst_slot, uint64_t dst_offset, uint64_t bytes);

@@ -101,6 +101,7 @@ PROTOTYPES = {
     "lrm_hip_begin": (C.c_int, [P, C.c_int, C.POINTER(P)]),
     "lrm_hip_dispatch": (C.c_int, [P, C.c_uint32, U32P]),
     "lrm_hip_dispatch_overlapped": (C.c_int, [P, C.c_uint32, U32P]),
+    "lrm_hip_dispatch_decode_attention_static": (C.c_int, [P, U32P, C.c_uint32]),
     "lrm_hip_barrier": (C.c_int, [P]),
     "lrm_hip_copy": (C.c_int, [P, C.c_int, C.c_uint64, C.c_int, C.c_uint64, C.c_uint64]),
     "lrm_hip_begin_timer": (C.c_int, [P, C.c_char_p, C.POINTER(C.c_int)]),

@@ -337,6 +337,14 @@ int lrm_hip_dispatch_overlapped(lrm_hip_list* l, uint32_t kernel, const uint32_t
     });
 }
 
+int lrm_hip_dispatch_decode_attention_static(lrm_hip_list* l, const uint32_t words[32], uint32_t y) {
+    return guard([&] {
+        need_ptr(l, "list");
+        need_ptr(words, "words");
+        record_decode_attention_static(l->owner->d, l->l, words, y);
+    });
+}
+
 int lrm_hip_barrier(lrm_hip_list* l) {
     return guard([&] {
         need_ptr(l, "list");

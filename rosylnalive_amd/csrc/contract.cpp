@@ -498,7 +498,7 @@ static bool alias_lists(const char* alias, const char* name) {
     return false;
 }
 
-PreparedDispatch prepare(const SealedTableView& table, int kernel, const uint32_t* words) {
+static PreparedDispatch prepare_impl(const SealedTableView& table, int kernel, const uint32_t* words, int library) {
     auto& cat = catalog();
     if (kernel < 0 || kernel >= int(cat.size())) contract_fail("kernel id %d is not in the catalog", kernel);
     const KernelSpec& k = cat[size_t(kernel)];
@@ -512,6 +512,11 @@ PreparedDispatch prepare(const SealedTableView& table, int kernel, const uint32_
         const FieldSpec& f = k.fields[i];
         if (f.kind != FieldKind::Token) continue;
         uint32_t token = words[i + 1];
+        if (int(i) == library) {
+            if (token != 0) contract_fail("%s.%s: the library supplies this buffer; pass token 0", k.name, f.name);
+            counts[i] = 0xFFFFFFFFu;
+            continue;
+        }
         TensorRow row = table.row(token);
         if (f.access == Access::Meta) {
             if (token != 0 && row.is_zero()) contract_fail("%s.%s: token %u is not in the table", k.name, f.name, token);
@@ -552,6 +557,20 @@ PreparedDispatch prepare(const SealedTableView& table, int kernel, const uint32_
     std::memcpy(pd.words.data(), words, 128);
     pd.words[0] = pd.physical.x;
     return pd;
+}
+
+PreparedDispatch prepare(const SealedTableView& table, int kernel, const uint32_t* words) {
+    return prepare_impl(table, kernel, words, -1);
+}
+
+PreparedDispatch prepare_library_field(const SealedTableView& table, int kernel, const uint32_t* words,
+                                       int library_field) {
+    auto& cat = catalog();
+    if (kernel < 0 || kernel >= int(cat.size())) contract_fail("kernel id %d is not in the catalog", kernel);
+    const auto& fields = cat[size_t(kernel)].fields;
+    if (library_field < 0 || library_field >= int(fields.size()) || fields[size_t(library_field)].kind != FieldKind::Token)
+        contract_fail("%s: field %d is not a token field", cat[size_t(kernel)].name, library_field);
+    return prepare_impl(table, kernel, words, library_field);
 }
 
 void check_copy(const HeapLayout& layout, int ss, uint64_t so, int ds, uint64_t dof, uint64_t bytes) {

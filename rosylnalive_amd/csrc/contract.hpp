@@ -189,6 +189,11 @@ struct PreparedDispatch {
 // Dispatch.prepare (Dispatch.fs:149-173) plus the minimum element counts of kernel-abi.md, which this device checks
 // on the host before every launch so no kernel can touch memory outside its tensors.
 PreparedDispatch prepare(const SealedTableView& table, int kernel, const uint32_t* words);
+// The same checks for a dispatch one of whose token fields, `library_field`, is memory the library supplies rather
+// than a tensor of the heap: its word must be 0 and it takes no part in the token, aliasing and minimum-count rules
+// (the caller checks the bytes the launch touches against its own buffer).
+PreparedDispatch prepare_library_field(const SealedTableView& table, int kernel, const uint32_t* words,
+                                       int library_field);
 
 // Dispatch.checkCopy / checkTransfer
 void check_copy(const HeapLayout& layout, int src_slot, uint64_t src_off, int dst_slot, uint64_t dst_off, uint64_t bytes);

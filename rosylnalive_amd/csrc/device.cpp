@@ -80,6 +80,7 @@ Device::Device(int index, uint32_t flags) : index_(index), flags_(flags) {
     HIPC(hipEventCreateWithFlags(&join_ev_, hipEventDisableTiming));
     HIPC(hipEventCreate(&epoch_));
     HIPC(hipEventRecord(epoch_, stream_));
+    static_scratch_ = static_scratch_address(index);
 }
 
 Device::~Device() {
@@ -275,6 +276,28 @@ void CommandList::dispatch(int kernel, const uint32_t* words) {
         else
             c.ptr[size_t(u.field)] = dev_->resolve(u.token);
     }
+    cmds_.push_back(std::move(c));
+    ++dispatches_;
+}
+
+void CommandList::dispatch_library(int kernel, const uint32_t* words, int library_field, void* library_ptr) {
+    check_open();
+    if (exec_) contract_fail("a reusable list cannot be changed after its first submission");
+    if (!dev_->kernels_loaded()) contract_fail("Dispatch before LoadKernels");
+    if (!dev_->contains(kernel)) contract_fail("kernel %d is not in the loaded kernel set", kernel);
+    if (!library_ptr) contract_fail("no library buffer for field %d", library_field);
+    Cmd c{};
+    c.kind = Cmd::Launch;
+    c.pd = prepare_library_field(dev_->table(), kernel, words, library_field);
+    const KernelSpec& k = catalog()[size_t(kernel)];
+    c.ptr.assign(k.fields.size() + 1, nullptr);
+    for (const TokenUse& u : c.pd.tokens) {
+        if (u.access == Access::Meta)
+            c.ptr[size_t(u.field)] = static_cast<uint8_t*>(dev_->slot_ptr(0)) + size_t(u.token) * kRowBytes;
+        else
+            c.ptr[size_t(u.field)] = dev_->resolve(u.token);
+    }
+    c.ptr[size_t(library_field)] = library_ptr;
     cmds_.push_back(std::move(c));
     ++dispatches_;
 }

@@ -37,6 +37,14 @@ const LaunchFn* catalog_launchers();  // ids 0..13
 const LaunchFn* fast_launchers();     // ids 14..
 int fast_first_id();
 
+class Device;
+class CommandList;
+// The library's static scratch (scratch_static.hip): its size, this GPU's copy (hipGetSymbolAddress with `device`
+// current, looked up once per device), and the decode attention whose split partials live there.
+size_t static_scratch_bytes();
+void* static_scratch_address(int device);
+void record_decode_attention_static(Device& dev, CommandList* l, const uint32_t* words, uint32_t y);
+
 struct DeviceInfo {
     int index;
     char name[128];
@@ -70,6 +78,9 @@ class CommandList {
     // ordering rule: dispatches not separated by Barrier may overlap). It runs on the device's side stream, after
     // everything recorded before it; Barrier, and the end of the list, wait for it.
     void dispatch_overlapped(int kernel, const uint32_t* words);
+    // A dispatch whose token field `library_field` is device memory the library owns (`library_ptr`) rather than a
+    // tensor of the heap; its word is 0 (prepare_library_field). The caller has checked the bytes the launch touches.
+    void dispatch_library(int kernel, const uint32_t* words, int library_field, void* library_ptr);
     void barrier();
     void copy(int src_slot, uint64_t src_off, int dst_slot, uint64_t dst_off, uint64_t bytes);
     int begin_timer(const std::string& name);
@@ -138,6 +149,8 @@ class Device {
     void release(CommandList* list);  // frees a list; the caller releases every list it began
 
     hipStream_t stream() const { return stream_; }
+    // This device's copy of the library's static scratch array (its address from hipGetSymbolAddress at creation)
+    void* static_scratch() const { return static_scratch_; }
     void* slot_ptr(int slot) const;
     void* resolve(uint32_t token) const;  // device pointer of a token's first byte
 
@@ -155,6 +168,7 @@ class Device {
     hipStream_t side_ = nullptr;  // overlapped dispatches (default priority, like stream_)
     hipEvent_t fork_ev_ = nullptr, join_ev_ = nullptr;
     hipEvent_t epoch_ = nullptr;
+    void* static_scratch_ = nullptr;
     bool heap_created_ = false;
     HeapLayout layout_;
     std::vector<void*> pages_;  // slot i at pages_[i], slot 0 = the table buffer

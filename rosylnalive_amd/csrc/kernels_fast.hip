@@ -1832,6 +1832,9 @@ static uint32_t dec_splits(uint32_t max_pos, uint32_t chunks) {
 static uint32_t dec_grid_splits(uint32_t max_pos, uint32_t chunks, uint32_t splits) {
     return splits ? splits : dec_splits(max_pos, chunks);
 }
+uint32_t decode_attention_splits(uint32_t max_pos, uint32_t chunks, uint32_t splits) {
+    return dec_grid_splits(max_pos, chunks, splits);
+}
 
 static void l_attn_dec(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();

@@ -479,6 +479,11 @@ class HipCommandList:
         kid = Catalog.find(kernel).id if isinstance(kernel, str) else int(kernel)
         check(lib().lrm_hip_dispatch_overlapped(self._h, kid, args.as_c()))
 
+    def dispatch_decode_attention_static(self, args: ArgBlock, y: int) -> None:
+        """attention_decode_f16 (args, partials token 0) then attention_combine into the f32 tensor y, the split
+        partials in the library's static scratch: nothing is allocated (no counterpart in the reference)."""
+        check(lib().lrm_hip_dispatch_decode_attention_static(self._h, args.as_c(), int(y)))
+
     def barrier(self) -> None:
         check(lib().lrm_hip_barrier(self._h))
 
