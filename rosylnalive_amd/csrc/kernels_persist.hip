@@ -1,41 +1,46 @@
 // ================================================================ 38 decode_step_persistent
-// The one-sequence decode step (embed, every layer, lm_head, greedy argmax, state advance) as ONE launch: G
-// workgroups of 8 waves (G = 256 on MI355X, one per CU, all resident together) walk the layers stage by stage, each
-// taking a fixed share of every stage, and hand the stage outputs to each other through tagged exchange entries in
-// device memory instead of kernel boundaries. It computes what the multi-kernel step of the executor computes
-// (embed_dec, then per layer gemv_norm_dec, attention_decode_f16, attention_combine, gemv_residual_dec,
-// gemv_swiglu_dec, gemv_residual_dec, then lmhead_dec and argmax_dec) with the same per-lane arithmetic; only the
-// order of a few partial sums differs (the o_proj, SwiGLU and down rows are split over two waves, the split combine
-// runs one split per lane).
+// The one-sequence decode step (embed, every layer, lm_head, greedy argmax, state advance) as ONE launch: 256
+// workgroups of 8 waves (one per CU, all resident together) walk the layers stage by stage, each taking a fixed share
+// of every stage, and hand the stage outputs to each other through tagged exchange entries in device memory instead of
+// kernel boundaries. It computes what the multi-kernel step of the executor computes (embed_dec, then per layer
+// gemv_norm_dec, attention_decode_f16, attention_combine, gemv_residual_dec, gemv_swiglu_dec, gemv_residual_dec, then
+// lmhead_dec and argmax_dec) with the same per-lane products; the o_proj and down_proj sums run in another order (each
+// XCD's columns summed alone, then the eight sums added in XCD order), and the split combine runs one split per lane.
 //
 // Why: batch-1 decode of a 0.6B model moves ~1.2 GB per token, ~150 us at HBM speed, but as ~170 dependent kernels
-// it is bound by launch and ramp latency (4-6 us per kernel). Here each hand-off costs one store and one poll (about
-// 1 us between CUs), and every workgroup issues the weight loads of its next stage before it waits, so the weight
-// stream overlaps the hand-off latency.
+// it is bound by launch and ramp latency (4-6 us per kernel). Here each hand-off costs a store and a poll, and every
+// workgroup issues the weight loads of its next stage before it waits, so the weight stream overlaps the hand-offs.
+//
+// XCD mapping. An MI355X has 8 XCDs, each with its own L2; the dispatcher puts workgroup b on XCD (b + c) % 8, with c
+// fixed for a launch (it depends on the hardware queue), so each XCD holds 32 workgroups. A workgroup reads its XCD from
+// the hardware register XCC_ID and takes role j = b / 8 on it: every (XCD, j) is taken once. A device-scope store writes
+// through to memory
+// and a device-scope load from another XCD fetches it there: 0.7 us one way, about 2.2 us for an all-gather between all
+// 256 workgroups. A plain store stays in the writer's L2, where a device-scope load from the same XCD finds it: 0.3 us.
+// So KV head h is XCD h's: its q|k|v rows, its 32 attention splits, their combine, and the o_proj and down_proj
+// columns that read its outputs (o_proj columns 256 h .. + 255, SwiGLU outputs and down_proj columns 384 h .. + 383).
+// Four of a layer's six hand-offs stay inside one L2; the o_proj and down_proj outputs leave as per-XCD partial sums
+// [8][hidden] through memory, and every workgroup adds them to its own copy of the residual stream.
 //
 // Exchange entries carry their own ready mark, so a consumer polls the data itself. 8-byte entries (q|k|v, the
-// attention partials, the lm_head partials): (tag << 32) | value bits, written by one agent-scope 64-bit store and read
-// by agent-scope 64-bit loads (both coherent across the XCDs' L2s without cache maintenance); an entry is ready when
-// it carries this launch's tag, the launch epoch + 1 (header word 0, advanced by workgroup 0 at the end of every step),
-// so entries left by earlier steps never match. The vectors every workgroup reads (o, x after o_proj, the SwiGLU
-// output, x after down_proj) are 4-byte entries, the value with its lowest mantissa bit replaced by the tag's parity
-// (every such entry is written by every step, so the previous step's entries always carry the other parity; after an
-// aborted step the host zeroes the area), and are written in 8 copies, one per XCD, so each copy is polled by 32
-// workgroups instead of 256: halving the bytes and spreading the copies cut the polling traffic that bounds a
-// hand-off (all 256 workgroups polling one copy of 8-byte entries measured 1.7-2.8 us per hand-off).
+// attention partials, the lm_head partials): (tag << 32) | value bits; an entry is ready when it carries this launch's
+// tag, the launch epoch + 1 (header word 0, advanced by workgroup 0 at the end of every step), so entries left by
+// earlier steps never match. 4-byte entries (the combined o, the SwiGLU output, the o_proj and down_proj partial sums):
+// the value with its lowest mantissa bit replaced by the tag's parity; every such entry is written by every step, so
+// the previous step's entries always carry the other parity (after an aborted step the host zeroes the area).
 //
-// Stages of layer l (G = 256, Qwen3-0.6B: hidden 1024, 16/8 heads, intermediate 3072):
-//   A  q|k|v = W_qkv . RMSNorm(x): 2 rows per wave. Waits for x (all of it: the RMSNorm needs the whole row).
-//   B  attention: workgroup b takes KV head b / S (S = G / kv_heads = 32 splits) and the keys [s KPS, (s + 1) KPS)
-//      of split s = b % S (KPS a multiple of 64 chosen so the splits cover pos + 1 keys), both query heads, 64 keys
-//      at a time with an online softmax; the split holding pos also normalises, rotates and appends the new key and
-//      value. Its K/V loads are issued before it waits for q. Writes (max, sum, out[128]) per query head.
-//   B' combine: 8 output dims of one query head per workgroup, one split per lane.
-//   C  x += W_o . o: 4 rows per workgroup, each split over two waves.
-//   D  a = silu(W_g . h) * (W_u . h), h = RMSNorm(x): 12 gate/up pairs per workgroup.
-//   E  x += W_d . a: 4 rows per workgroup, each split over two waves.
-// Then every workgroup takes 1/G of the lm_head rows and writes its (max, lowest index); workgroup 0 merges them,
-// records the id and advances the state (position, id, step) for the next launch.
+// Stages of layer l (Qwen3-0.6B: hidden 1024, 16/8 heads, intermediate 3072), workgroup b on XCD h, j = b / 8:
+//   A  q|k|v of KV head h = W . RMSNorm(x): 2 of the XCD's 512 rows per wave. Waits for x, i.e. for the previous
+//      layer's down_proj partial sums of all XCDs (all of x: the RMSNorm needs the whole row).
+//   B  attention: split j of KV head h takes keys [j KPS, (j + 1) KPS) (KPS a multiple of 64 chosen so 32 splits cover
+//      pos + 1 keys), both query heads, 64 keys at a time with an online softmax; the split holding pos also
+//      normalises, rotates and appends the new key and value. Writes (max, sum, out[128]) per query head.
+//   B' combine: 8 output dims of one of the XCD's query heads per workgroup, one split per lane.
+//   C  p1[h] = W_o[:, 256 h .. + 255] . o_h: 32 rows per workgroup.
+//   D  a_h = silu(W_g . r) * (W_u . r), r = RMSNorm(x + sum_h p1[h]): 12 of the XCD's 384 gate/up pairs.
+//   E  p2[h] = W_d[:, 384 h .. + 383] . a_h: 32 rows per workgroup.
+// Then x += sum_h p2[h], every workgroup takes 1/256 of the lm_head rows and writes its (max, lowest index); workgroup
+// 0 merges them, records the id and advances the state (position, id, step) for the next launch.
 //
 // Every wait is bounded: a poll that waits longer than 0.2 s, or sees another workgroup's abort, sets the abort word
 // (header word 1) and the stage (word 2) and the workgroup returns; so every wave ends even if a workgroup were never
@@ -59,6 +64,21 @@ namespace {
 
 constexpr long long kWaitTicks = 20000000;  // 0.2 s of the 100 MHz constant clock: the default bound of a wait
 
+// The instantiated shape (persist::unsupported): Qwen3-0.6B on 256 workgroups.
+constexpr int kH = 1024, kQH = 16, kKVH = kXcds, kQPK = kQH / kKVH, kQC = kQH * 128, kKC = kKVH * 128, kI = 3072;
+constexpr int kG = 256;
+constexpr int kJN = kG / kXcds;                          // workgroups per XCD = attention splits per KV head
+constexpr int kNCH = kH / 512;                           // 512-wide chunks of the hidden vector per lane
+constexpr int kRA = (kQPK + 2) * 128 / (kJN * kWaves);  // q|k|v rows per wave
+constexpr int kCW = kQPK * 128, kEW = kI / kXcds;        // o_proj / down_proj columns of one XCD
+constexpr int kRowsG = kH / kJN, kRowsW = kRowsG / kWaves;  // o_proj / down_proj rows per workgroup, per wave
+constexpr int kNCC = kRowsW * (kCW / 8) / 64;            // 16-byte o_proj chunks per lane
+constexpr int kNCE = kRowsW * (kEW / 8) / 64;            // 16-byte down_proj chunks per lane
+constexpr int kPB = kEW / kJN;                           // SwiGLU outputs per workgroup
+constexpr int kUD = 2 * kPB * kNCH / kWaves;             // (gate/up row, chunk) units per wave
+static_assert(kRA == 2 && kNCC == 2 && kNCE == 3 && kPB == 12 && kUD == 6 && kRowsW == 4, "the 0.6B decode shape");
+static_assert(kRowsG <= 64 && kQPK * 16 == kJN, "one combine item and one row run per workgroup");
+
 struct PArgs {
     const uint16_t* embed;       // [V, H] bf16; also the tied lm_head
     const uint16_t* final_norm;  // [H]
@@ -78,23 +98,29 @@ struct PArgs {
     uint32_t* state;             // position, id, step
     uint32_t* out_ids;           // [max_steps]
     uint64_t* xch;               // exchange: header, then the entries
-    int layers, hidden, qh, kvh, inter, vocab, max_pos, max_steps, write_logits;
+    int layers, vocab, max_pos, max_steps, write_logits;
     float eps, scale_log2;
 };
 
-__device__ __forceinline__ uint64_t xload(const uint64_t* p) {
+__device__ __forceinline__ uint32_t word_load(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void xstore(uint64_t* p, float v, uint32_t tag) {
+// Device-wide entries (read by workgroups of every XCD): device-scope stores, written through to memory.
+__device__ __forceinline__ void gstore(uint64_t* p, float v, uint32_t tag) {
     __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // 4-byte entries: the value with its lowest mantissa bit replaced by the launch parity (a change of at most one unit
-// in the last place, which the readers of these vectors see; the writers keep their exact values)
-__device__ __forceinline__ void xstore32(uint32_t* p, float v, uint32_t parity) {
+// in the last place, which the readers of these vectors see)
+__device__ __forceinline__ void gstore32(uint32_t* p, float v, uint32_t parity) {
     __hip_atomic_store(p, (__float_as_uint(v) & ~1u) | parity, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint32_t word_load(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// XCD-local entries (read by the workgroups of the writer's XCD only): plain stores, which stay in the XCD's L2, where
+// the readers' device-scope loads find them.
+__device__ __forceinline__ void lstore(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+__device__ __forceinline__ void lstore32(uint32_t* p, float v, uint32_t parity) {
+    __hip_atomic_store(p, (__float_as_uint(v) & ~1u) | parity, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 __device__ __forceinline__ void abort_step(uint32_t* hdr, int stage) {
     __hip_atomic_store(hdr + 2, uint32_t(stage), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -111,22 +137,36 @@ __device__ __forceinline__ void unpack8bf(u32x4 v, float* f) {
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// Block-wide: waits until the entries at idx(i), i < n (1 <= n <= E * 512), are ready and writes their values to dst[i]
-// in LDS. Thread t polls entries t, t + 512, ..., re-reading only those not yet ready, back to back (a sleep between
-// polls measured slower: each 64 clocks of it added about 0.02 us per hand-off). When the step is
-// aborted (this wait timed out or another workgroup aborted) it sets `fail` (the workgroup's LDS flag), which the
-// caller reads after the barrier that ends the wait. `fail` must stay an LDS access: a generic (flat) read would also
-// wait for every global load in flight, the prefetched weights included.
-// READY(v) says whether a loaded entry is ready; VALUE(v) gives its value.
-template <int E, typename T, typename F, typename R, typename V>
-__device__ __forceinline__ void gather_entries(F idx, int n, R ready, V value, float* dst, uint32_t* hdr, int stage,
-                                               int& fail, long long limit) {
+// The bound of a wait: true (and the step aborted, `fail` set) when this poll has waited past `limit` ticks, or every
+// 16 polls, when another workgroup aborted.
+__device__ __forceinline__ bool wait_over(int it, long long& start, long long limit, uint32_t* hdr, int stage,
+                                          int& fail) {
+    if (it == 0) {
+        start = wall_clock64();
+        return false;
+    }
+    if (wall_clock64() - start > limit || ((it & 15) == 0 && word_load(hdr + 1) != 0u)) {
+        abort_step(hdr, stage);
+        fail = 1;
+        return true;
+    }
+    return false;
+}
+
+// Block-wide: waits until the 8-byte entries idx(i), i < n (1 <= n <= E * 512), carry `tag` and writes their values to
+// dst[i] in LDS. Thread t polls entries t, t + 512, ..., re-reading only those not yet ready, back to back. When the
+// step is aborted (this wait timed out or another workgroup aborted) it sets `fail` (the workgroup's LDS flag), which
+// the caller reads after the barrier that ends the wait. `fail` must stay an LDS access: a generic (flat) read would
+// also wait for every global load in flight, the prefetched weights included.
+template <int E, typename F>
+__device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, uint32_t* hdr, int stage, int& fail,
+                                       long long limit) {
     const int t = threadIdx.x;
     if (n <= 0) {
         lds_barrier();
         return;
     }
-    T v[E];
+    uint64_t v[E];
     bool pend[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) pend[e] = t + e * kThreads < n;
@@ -138,44 +178,54 @@ __device__ __forceinline__ void gather_entries(F idx, int n, R ready, V value, f
         bool any = false;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            pend[e] = pend[e] && !ready(v[e]);
+            pend[e] = pend[e] && uint32_t(v[e] >> 32) != tag;
             any |= pend[e];
         }
-        if (!any) break;
-        if (it == 0) {
-            start = wall_clock64();
-        } else if (wall_clock64() - start > limit || ((it & 15) == 0 && word_load(hdr + 1) != 0u)) {
-            abort_step(hdr, stage);
-            fail = 1;
-            break;
-        }
+        if (!any || wait_over(it, start, limit, hdr, stage, fail)) break;
     }
 #pragma unroll
     for (int e = 0; e < E; ++e)
-        if (t + e * kThreads < n) dst[t + e * kThreads] = value(v[e]);
+        if (t + e * kThreads < n) dst[t + e * kThreads] = __uint_as_float(uint32_t(v[e]));
     lds_barrier();
     // Nothing is in flight now (every poll waited for all older loads and stores); saying so lets the compiler's
     // wait counting start from zero after the loop instead of waiting for loads issued later.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 }
 
-// 8-byte entries carrying `tag`
-template <int E, typename F>
-__device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, uint32_t* hdr, int stage, int& fail,
-                                       long long limit) {
-    gather_entries<E, uint64_t>(
-        idx, n, [&](uint64_t v) __attribute__((always_inline)) { return uint32_t(v >> 32) == tag; },
-        [](uint64_t v) __attribute__((always_inline)) { return __uint_as_float(uint32_t(v)); }, dst, hdr, stage, fail,
-        limit);
-}
-
-// 4-byte entries of the launch parity
-template <int E, typename F>
-__device__ __forceinline__ void gather32(F idx, int n, uint32_t parity, float* dst, uint32_t* hdr, int stage,
-                                         int& fail, long long limit) {
-    gather_entries<E, uint32_t>(
-        idx, n, [&](uint32_t v) __attribute__((always_inline)) { return (v & 1u) == parity; },
-        [](uint32_t v) __attribute__((always_inline)) { return __uint_as_float(v); }, dst, hdr, stage, fail, limit);
+// Block-wide: waits until the 4-byte entries base[0 .. 4 nv) (nv <= E * 512) carry `parity` and writes their values
+// to dst (16-byte aligned, LDS). 16-byte device-scope loads, four entries each; otherwise as gather.
+template <int E>
+__device__ __forceinline__ void gather32x4(const uint32_t* base, int nv, uint32_t parity, float* dst, uint32_t* hdr,
+                                           int stage, int& fail, long long limit) {
+    const int t = threadIdx.x;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(base), (short)0, nv * 16, 0x00020000);
+    constexpr int kSc1 = 16;  // the buffer load's cache policy: device scope (sc1)
+    u32x4 v[E];
+    bool pend[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) pend[e] = t + e * kThreads < nv;
+    long long start = 0;
+    for (int it = 0;; ++it) {
+        asm volatile("" ::: "memory");  // every pass loads again
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            if (pend[e]) v[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, (t + e * kThreads) * 16, 0, kSc1);
+        bool any = false;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const uint32_t all = v[e][0] & v[e][1] & v[e][2] & v[e][3], some = v[e][0] | v[e][1] | v[e][2] | v[e][3];
+            const bool ready = parity ? (all & 1u) != 0u : (some & 1u) == 0u;
+            pend[e] = pend[e] && !ready;
+            any |= pend[e];
+        }
+        if (!any || wait_over(it, start, limit, hdr, stage, fail)) break;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+        if (t + e * kThreads < nv) *reinterpret_cast<u32x4*>(dst + 4 * (t + e * kThreads)) = v[e];
+    lds_barrier();
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), as in gather
 }
 
 // This lane's values k = 512 c + 8 lane + e of RMSNorm(vec) (vec in LDS, 512 NCH wide): every wave reads the whole
@@ -223,21 +273,45 @@ __device__ __forceinline__ float dot8_lds(u32x4 wv, const float* vec, int k0, fl
     return dot8(wv, v, acc);
 }
 
-template <int NCH, int RA, int NCC, int UD, int NCE, int KSX>
+// Rows q = c / CPR of this wave's kRowsW rows, the lane's chunks c = lane + 64 i (CPR 16-byte chunks per row) dotted
+// with the vector in LDS; the row sums go to red[w kRowsW + q].
+template <int NC, int CPR>
+__device__ __forceinline__ void rows_dot(const u32x4 (&wr)[NC], const float* vec, float* red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float acc[kRowsW];
+#pragma unroll
+    for (int q = 0; q < kRowsW; ++q) acc[q] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + 64 * i, q = c / CPR, kc = c - q * CPR;
+        const float d = dot8_lds(wr[i], vec, 8 * kc, 0.f);
+#pragma unroll
+        for (int qq = 0; qq < kRowsW; ++qq)
+            if (qq == q) acc[qq] += d;
+    }
+#pragma unroll
+    for (int q = 0; q < kRowsW; ++q) {
+        const float s = wave_sum(acc[q]);
+        if (lane == 0) red[w * kRowsW + q] = s;
+    }
+}
+
 __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     __shared__ __align__(16) float vec[kVecMax];
+    __shared__ __align__(16) float xres[kH];  // the residual stream: every workgroup holds all of it, the same bits
     __shared__ float red[64];
     __shared__ float qs[2][128];
     __shared__ float knew[128], vnew[128];
     __shared__ float ps[2][64];
     __shared__ float alpha_s[2];
-    __shared__ float xown[8];
     __shared__ float lmv[kWaves];
     __shared__ uint32_t lmi[kWaves];
     __shared__ int s_fail;
 
-    const int b = blockIdx.x, G = gridDim.x, t = threadIdx.x, lane = t & 63;
+    const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: row offsets stay scalar
+    // KV head xcd = this workgroup's XCD (hardware register XCC_ID); j = its index among the XCD's workgroups
+    const int xcd = __builtin_amdgcn_s_getreg((3 << 11) | 20) & (kXcds - 1), j = b / kXcds;
     uint32_t* hdr = reinterpret_cast<uint32_t*>(a.xch);
     const uint32_t pos = word_load(a.state), id = word_load(a.state + 1), step = word_load(a.state + 2);
     const uint32_t tag = word_load(hdr) + 1u;
@@ -247,17 +321,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     const long long wait_ticks = wait_word ? (long long)wait_word : kWaitTicks;
     if (t == 0) s_fail = 0;
 
-    const int H = a.hidden, QC = a.qh * 128, KC = a.kvh * 128, N1 = QC + 2 * KC, I = a.inter, MP = a.max_pos;
-    const int S = G / a.kvh, RB = kWaves / KSX, KS = KSX, PB = I / G;
-    const XLayout X(a.qh, a.kvh, H, I, G);
-    uint64_t* const lmp = a.xch + kHdrEntries + size_t(a.layers) * X.per_layer;  // lm_head partials
-    uint32_t* const x32 = reinterpret_cast<uint32_t*>(lmp + 2 * G);           // the 4-byte area
-    const int gw = b * kWaves + w, NWv = G * kWaves;
-    const int rr = b * RB + w / KS, ks = w % KS;  // stages C and E: this wave's row and its part of the row
-    const int rep = b % kReplicas;                // the copy of the shared vectors this workgroup polls
+    const int MP = a.max_pos, S = kJN;
+    const XLayout X(kQH, kKVH, kH, kI, kG);
+    uint64_t* const lmp = a.xch + kHdrEntries + size_t(a.layers) * X.per_layer64;  // lm_head partials
+    uint32_t* const x32 = reinterpret_cast<uint32_t*>(lmp + (2 * kG + 511) / 512 * 512);  // the 4-byte area
 
     // attention split of this workgroup (stage B): fixed for the step
-    const int hk = b / S, s = b % S;
+    const int hk = xcd, s = j;
     const int ntot = int(pos) + 1;
     const int KPS = ((ntot + S - 1) / S + 63) / 64 * 64;
     const int S_used = (ntot + KPS - 1) / KPS;
@@ -266,25 +336,39 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     const int k0 = s * KPS, nk = attn ? min(KPS, ntot - k0) : 0, nch = (nk + 63) / 64;
     const int jnew = int(pos) - k0;
 
-    u32x4 wa[RA][NCH], na[NCH];
+    // stage A: the XCD's q|k|v rows, local row lr = the XCD's query heads (0 .. 255), its key (256 ..), its value
+    u32x4 wa[kRA][kNCH], na[kNCH];
     auto issue_a = [&](int l) __attribute__((always_inline)) {
-        const uint16_t* W = a.qkv + size_t(l) * N1 * H;
+        const uint16_t* W = a.qkv + size_t(l) * (kQC + 2 * kKC) * kH;
 #pragma unroll
-        for (int r = 0; r < RA; ++r) {
-            const int row = min(gw + r * NWv, N1 - 1);
+        for (int r = 0; r < kRA; ++r) {
+            const int lr = j * kWaves + w + r * kJN * kWaves;
+            const int row = lr < kQPK * 128         ? kQPK * 128 * hk + lr
+                            : lr < (kQPK + 1) * 128 ? kQC + 128 * hk + lr - kQPK * 128
+                                                    : kQC + kKC + 128 * hk + lr - (kQPK + 1) * 128;
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) wa[r][c] = ld16(W + size_t(row) * H + 512 * c + 8 * lane);
+            for (int c = 0; c < kNCH; ++c) wa[r][c] = ld16(W + size_t(row) * kH + 512 * c + 8 * lane);
         }
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) na[c] = ld16(a.in_norm + size_t(l) * H + 512 * c + 8 * lane);
+        for (int c = 0; c < kNCH; ++c) na[c] = ld16(a.in_norm + size_t(l) * kH + 512 * c + 8 * lane);
     };
 
-    // x = widen(E[id]) (NaN for an id outside the vocabulary, as embed_dec); this workgroup keeps rows b RB .. + RB
+    // x = widen(E[id]) (NaN for an id outside the vocabulary, as embed_dec)
     issue_a(0);
-    for (int k = t; k < H; k += kThreads)
-        vec[k] = id < uint32_t(a.vocab) ? bf2f(a.embed[size_t(id) * H + k]) : __uint_as_float(0x7FC00000u);
+    for (int k = t; k < kH; k += kThreads)
+        xres[k] = id < uint32_t(a.vocab) ? bf2f(a.embed[size_t(id) * kH + k]) : __uint_as_float(0x7FC00000u);
     lds_barrier();
-    if (t < RB) xown[t] = vec[b * RB + t];
+
+    // x += the XCDs' partial sums gathered in vec ([8][hidden]), added in XCD order: the same bits in every workgroup
+    auto add_partials = [&]() __attribute__((always_inline)) {
+        for (int k = t; k < kH; k += kThreads) {
+            float sum = vec[k];
+#pragma unroll
+            for (int x = 1; x < kXcds; ++x) sum += vec[x * kH + k];
+            xres[k] += sum;
+        }
+        lds_barrier();
+    };
 
     // This split's first 64-key chunks of K and V^T (one when the split holds one, else two): they do not depend on
     // this step, so the chunks of layer l + 1 load at the end of layer l (layer 0's here), away from stage A, where
@@ -294,13 +378,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     u32x4 kr[2][2], vr[2][2];
     auto fetch = [&](auto set, int l, int c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set)::value;
-        const uint16_t* kb = a.kc + ((size_t(l) * a.kvh + hk) * MP + k0) * 128 + 8 * (t & 15);
-        const uint16_t* vb = a.vc + ((size_t(l) * a.kvh + hk) * 128 + (t >> 2)) * MP + k0 + 16 * (t & 3);
+        const uint16_t* kb = a.kc + ((size_t(l) * kKVH + hk) * MP + k0) * 128 + 8 * (t & 15);
+        const uint16_t* vb = a.vc + ((size_t(l) * kKVH + hk) * 128 + (t >> 2)) * MP + k0 + 16 * (t & 3);
         const int cc = min(c, nch - 1) * 64;
 #pragma unroll
         for (int i = 0; i < 2; ++i) kr[SET][i] = ld16(kb + size_t(cc + (t >> 4) + 32 * i) * 128);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) vr[SET][j] = ld16(vb + cc + 8 * j);
+        for (int jj = 0; jj < 2; ++jj) vr[SET][jj] = ld16(vb + cc + 8 * jj);
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
@@ -313,42 +397,38 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     prefetch_kv(0);
 
     for (int l = 0; l < a.layers; ++l) {
-        uint64_t* xl = a.xch + kHdrEntries + size_t(l) * X.per_layer;
-        uint32_t* xv32 = x32 + size_t(l) * X.per_layer32;
+        uint64_t* const q64 = a.xch + kHdrEntries + size_t(l) * X.per_layer64 + size_t(xcd) * X.blk64;  // XCD block
+        uint32_t* const l32 = x32 + size_t(l) * X.per_layer32;
+        uint32_t* const o32 = l32 + size_t(xcd) * X.blk32;  // this XCD's 4-byte block
         // ---------------------------------------------------------------- A: q|k|v = W_qkv . RMSNorm(x)
         if (l > 0) {
-            const uint32_t* src = xv32 - X.per_layer32 + X.x2 + rep * H;
-            gather32<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, par, vec, hdr, 1, s_fail,
-                          wait_ticks);
+            gather32x4<4>(l32 - X.per_layer32 + X.p2, kXcds * kH / 4, par, vec, hdr, 1, s_fail, wait_ticks);
             if (s_fail) return;
+            add_partials();
         }
-        u32x4 wc[NCC];
+        u32x4 wc[kNCC];
         {
-            float xv[NCH][8];
-            norm_lane<NCH>(vec, na, a.eps, xv);
+            float xv[kNCH][8];
+            norm_lane<kNCH>(xres, na, a.eps, xv);
 #pragma unroll
-            for (int r = 0; r < RA; ++r) {
-                const int row = gw + r * NWv;
+            for (int r = 0; r < kRA; ++r) {
                 float acc = 0.f;
 #pragma unroll
-                for (int c = 0; c < NCH; ++c) acc = dot8(wa[r][c], xv[c], acc);
+                for (int c = 0; c < kNCH; ++c) acc = dot8(wa[r][c], xv[c], acc);
                 acc = wave_sum(acc);
                 if (lane == 0) red[r * kWaves + w] = acc;
             }
         }
-        // one wave stores the workgroup's rows (runs of kWaves consecutive rows), so each run is one write of whole
-        // 8-byte entries from one instruction (partial lines written by several waves cost a read-modify-write each)
+        // one wave stores the workgroup's rows (runs of kWaves consecutive entries), so each run is one write of whole
+        // 8-byte entries from one instruction
         lds_barrier();
-        if (t < RA * kWaves) {
-            const int row = b * kWaves + (t % kWaves) + (t / kWaves) * NWv;
-            if (row < N1) xstore(xl + X.qkv + row, red[t], tag);
-        }
-        // stage C's o_proj weights (this wave's part of row rr), issued after the rows above have left: a load issue
-        // that waits for room in the memory queue would otherwise hold them back
-        {
-            const uint16_t* W = a.o_proj + (size_t(l) * H + rr) * QC + ks * (QC / KS) + 8 * lane;
+        if (t < kRA * kWaves) lstore(q64 + X.qkv + j * kWaves + (t % kWaves) + (t / kWaves) * kJN * kWaves, red[t], tag);
+        // stage C's o_proj weights (rows 32 j + 4 w + q, the XCD's 256 columns), issued after the rows above have
+        // left: a load issue that waits for room in the memory queue would otherwise hold them back
 #pragma unroll
-            for (int c = 0; c < NCC; ++c) wc[c] = ld16(W + 512 * c);
+        for (int i = 0; i < kNCC; ++i) {
+            const int c = lane + 64 * i, q = c / (kCW / 8), kc = c - q * (kCW / 8);
+            wc[i] = ld16(a.o_proj + (size_t(l) * kH + j * kRowsG + w * kRowsW + q) * kQC + kCW * hk + 8 * kc);
         }
 
         // ---------------------------------------------------------------- B: attention over this split
@@ -358,10 +438,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             const float cs = a.cos_t[size_t(pos) * 64 + (d & 63)], sn = a.sin_t[size_t(pos) * 64 + (d & 63)];
             const float nwt = bf2f(t < 256 ? a.q_norm[l * 128 + d] : a.k_norm[l * 128 + d]);
             const float nwp = bf2f(t < 256 ? a.q_norm[l * 128 + (d ^ 64)] : a.k_norm[l * 128 + (d ^ 64)]);
-            const uint64_t* src = xl + X.qkv;
-            const int qo = 2 * hk * 128, ko = QC + hk * 128, vo = QC + KC + hk * 128;
-            gather<1>([&](int i) { return src + (i < 256 ? qo + i : i < 384 ? ko + i - 256 : vo + i - 384); },
-                   has_pos ? 512 : 256, tag, vec, hdr, 2, s_fail, wait_ticks);
+            const uint64_t* src = q64 + X.qkv;  // the XCD's query heads, then its key and value
+            gather<1>([&](int i) { return src + i; }, has_pos ? 512 : 256, tag, vec, hdr, 2, s_fail, wait_ticks);
             if (s_fail) return;
             // per-head RMSNorm (q heads: threads 0-255, the new key: 256-383), then the rotation of (d, d + 64): each
             // thread normalises its partner element d ^ 64 too (the same expression as the partner's own thread, so the
@@ -380,11 +458,11 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             } else if (t < 384) {
                 const uint16_t kh = f2h(rot);
                 knew[d] = h2f(kh);
-                if (has_pos) a.kc[((size_t(l) * a.kvh + hk) * MP + pos) * 128 + d] = kh;
+                if (has_pos) a.kc[((size_t(l) * kKVH + hk) * MP + pos) * 128 + d] = kh;
             } else {
                 const uint16_t vh = f2h(val);
                 vnew[d] = h2f(vh);
-                if (has_pos) a.vc[((size_t(l) * a.kvh + hk) * 128 + d) * MP + pos] = vh;
+                if (has_pos) a.vc[((size_t(l) * kKVH + hk) * 128 + d) * MP + pos] = vh;
             }
             lds_barrier();
             // this thread's query dims and, for the split holding pos, its slices of the new key and value (read
@@ -443,20 +521,20 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 const int kg = 16 * (t & 3);
                 float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int jj = 0; jj < 2; ++jj) {
                     float vf[8];
-                    unpack8h(vr[SET][j], vf);
+                    unpack8h(vr[SET][jj], vf);
                     if constexpr (tail) {
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
-                            const int key = cb + kg + 8 * j + e;
+                            const int key = cb + kg + 8 * jj + e;
                             vf[e] = key >= nk ? 0.f : (has_pos && key == jnew ? vn : vf[e]);
                         }
                     }
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        a0 = fmaf(ps[0][kg + 8 * j + e], vf[e], a0);
-                        a1 = fmaf(ps[1][kg + 8 * j + e], vf[e], a1);
+                        a0 = fmaf(ps[0][kg + 8 * jj + e], vf[e], a0);
+                        a1 = fmaf(ps[1][kg + 8 * jj + e], vf[e], a1);
                     }
                 }
                 o0 = fmaf(o0, alpha_s[0], a0);
@@ -479,8 +557,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 chunk(C0{}, Tail{}, c);
             }
             // reduce the four key groups of each dim, then the partial rows of both heads, (max, sum, out[128]) and
-            // the padding, each written whole by one wave (wave hh: head 2 hk + hh) from LDS (qs and red are free
-            // after the chunks)
+            // the padding, each written whole by one wave (wave hh: the XCD's query head hh) from LDS (qs and red are
+            // free after the chunks)
             o0 = quad4_sum(o0);
             o1 = quad4_sum(o1);
             if ((t & 3) == 0) {
@@ -493,146 +571,99 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             }
             lds_barrier();
             if (w < 2) {
-                uint64_t* pr = xl + X.part + size_t((2 * hk + w) * S + s) * kPartStride;
+                uint64_t* pr = q64 + X.part + size_t(w * S + s) * kPartStride;
 #pragma unroll
                 for (int i = lane; i < kPartStride; i += 64)
-                    xstore(pr + i, i < 2 ? red[2 * w + i] : i < 130 ? qs[w][i - 2] : 0.f, tag);
+                    lstore(pr + i, i < 2 ? red[2 * w + i] : i < 130 ? qs[w][i - 2] : 0.f, tag);
             }
         }
 
         // ---------------------------------------------------------------- B': combine the splits
-        // item it = b + G j: query head it / 16, dims 8 (it % 16) .. + 7, the S_used splits one per lane
+        // query head hh = j / 16 of the XCD, dims 8 (j % 16) .. + 7, the S_used splits one per lane
         {
-            const int items = (a.qh * 16 - b + G - 1) / G;
-            const int per_item = S_used * 10;
-            const uint64_t* src = xl + X.part;
-            lds_barrier();  // vec may still be read by stage A's or B's waves
+            const int hh = j / 16, d8 = (j % 16) * 8;
+            const uint64_t* src = q64 + X.part;
+            lds_barrier();  // vec may still be read by stage B's waves
             gather<1>(
-               [&](int i) {
-                   const int j = i / per_item, r = i - j * per_item, sp = r / 10, k = r - sp * 10;
-                   const int it = b + G * j, hq = it >> 4, d8 = (it & 15) * 8;
-                   return src + size_t(hq * S + sp) * kPartStride + (k < 2 ? k : d8 + k);
-               },
-               items * per_item, tag, vec, hdr, 3, s_fail, wait_ticks);
+                [&](int i) {
+                    const int sp = i / 10, k = i - sp * 10;
+                    return src + size_t(hh * S + sp) * kPartStride + (k < 2 ? k : d8 + k);
+                },
+                S_used * 10, tag, vec, hdr, 3, s_fail, wait_ticks);
             if (s_fail) return;
-            for (int j = 0; j < items; ++j) {  // wave w: dim d8 + w of item j; every wave forms the split weights
-                const int it = b + G * j, hq = it >> 4, d8 = (it & 15) * 8;
+            {  // wave w: dim d8 + w; every wave forms the split weights
                 const bool ok = lane < S_used;
-                const float* v = vec + j * per_item + (ok ? lane : 0) * 10;
+                const float* v = vec + (ok ? lane : 0) * 10;
                 const float m = ok ? v[0] : -INFINITY;
                 const float M = wave_max(m);
                 const float e = ok ? exp2f(m - M) : 0.f;
                 const float L = wave_sum(ok ? v[1] * e : 0.f);
                 const float od = wave_sum(ok ? v[2 + w] * e : 0.f);
-                if (lane == 0) red[j * kWaves + w] = od / L;
+                if (lane == 0) red[w] = od / L;
             }
-            // one wave stores every copy of the workgroup's dims: 8 consecutive dims per copy from one instruction
             lds_barrier();
-            if (t < 64 * items) {
-                const int j = t / 64, it = b + G * j, hq = it >> 4, d8 = (it & 15) * 8, r = (t & 63) >> 3;
-                xstore32(xv32 + X.o + r * QC + hq * 128 + d8 + (t & 7), red[j * kWaves + (t & 7)], par);
-            }
+            if (t < kWaves) lstore32(o32 + X.o + hh * 128 + d8 + t, red[t], par);
         }
 
-        // ---------------------------------------------------------------- C: x += W_o . o
+        // ---------------------------------------------------------------- C: p1[xcd] = W_o[:, the XCD's columns] . o
         lds_barrier();  // the combine reads vec
-        {
-            const uint32_t* src = xv32 + X.o + rep * QC;
-            gather32<NCC * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, QC, par, vec, hdr, 4,
-                             s_fail, wait_ticks);
-            if (s_fail) return;
-        }
-        {
-            float acc = 0.f;
-            const int kb0 = ks * (QC / KS) + 8 * lane;
-#pragma unroll
-            for (int c = 0; c < NCC; ++c) acc = dot8_lds(wc[c], vec, kb0 + 512 * c, acc);
-            acc = wave_sum(acc);
-            if (lane == 0) red[w] = acc;
-        }
+        gather32x4<1>(o32 + X.o, kCW / 4, par, vec, hdr, 4, s_fail, wait_ticks);
+        if (s_fail) return;
+        rows_dot<kNCC, kCW / 8>(wc, vec, red);
         lds_barrier();
-        if (t < RB * kReplicas) {  // thread t: row t / 8 into copy t % 8 (one wave: every read precedes the write)
-            const int i = t / kReplicas, r = t % kReplicas;
-            float sum = 0.f;
-            for (int k = 0; k < KS; ++k) sum += red[i * KS + k];
-            const float xn = xown[i] + sum;
-            if (r == 0) xown[i] = xn;
-            xstore32(xv32 + X.x1 + r * H + b * RB + i, xn, par);
-        }
-        // stage D's gate/up weights, after the rows above: unit u = w UD + j is (row u / NCH of the workgroup's 2 PB, chunk j % NCH); rows
-        // 0 .. PB - 1 are gate rows b PB + r, the rest the matching up rows
-        u32x4 wd[UD], nd[NCH];
+        if (t < kRowsG) gstore32(l32 + X.p1 + xcd * kH + j * kRowsG + t, red[t], par);
+        // stage D's gate/up weights, after the rows above: unit u = w kUD + jj is (row u / kNCH of the workgroup's
+        // 2 kPB, chunk jj % kNCH); rows 0 .. kPB - 1 are gate rows 384 xcd + 12 j + r, the rest the matching up rows
+        u32x4 wd[kUD], nd[kNCH];
 #pragma unroll
-        for (int j = 0; j < UD; ++j) {
-            const int ri = (w * UD + j) / NCH, c = j % NCH;
-            const int grow = ri < PB ? b * PB + ri : I + b * PB + (ri - PB);
-            wd[j] = ld16(a.gate_up + (size_t(l) * 2 * I + grow) * H + 512 * c + 8 * lane);
+        for (int jj = 0; jj < kUD; ++jj) {
+            const int ri = (w * kUD + jj) / kNCH, c = jj % kNCH;
+            const int grow = ri < kPB ? kEW * hk + kPB * j + ri : kI + kEW * hk + kPB * j + (ri - kPB);
+            wd[jj] = ld16(a.gate_up + (size_t(l) * 2 * kI + grow) * kH + 512 * c + 8 * lane);
         }
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) nd[c] = ld16(a.post_norm + size_t(l) * H + 512 * c + 8 * lane);
+        for (int c = 0; c < kNCH; ++c) nd[c] = ld16(a.post_norm + size_t(l) * kH + 512 * c + 8 * lane);
 
         // ---------------------------------------------------------------- D: a = silu(W_g . h) * (W_u . h)
-        {
-            const uint32_t* src = xv32 + X.x1 + rep * H;
-            gather32<NCH>([&](int i) __attribute__((always_inline)) { return src + i; }, H, par, vec, hdr, 5, s_fail,
-                          wait_ticks);
-            if (s_fail) return;
-        }
-        // stage E's down_proj weights (this wave's part of row rr), before this stage computes: issued after its
-        // outputs they land only after the hand-off to stage E
-        u32x4 we[NCE];
-        {
-            const uint16_t* W = a.down + (size_t(l) * H + rr) * I + ks * (I / KS) + 8 * lane;
+        gather32x4<4>(l32 + X.p1, kXcds * kH / 4, par, vec, hdr, 5, s_fail, wait_ticks);
+        if (s_fail) return;
+        // stage E's down_proj weights (rows 32 j + 4 w + q, the XCD's 384 columns), before this stage computes:
+        // issued after its outputs they land only after the hand-off to stage E
+        u32x4 we[kNCE];
 #pragma unroll
-            for (int c = 0; c < NCE; ++c) we[c] = ld16(W + 512 * c);
+        for (int i = 0; i < kNCE; ++i) {
+            const int c = lane + 64 * i, q = c / (kEW / 8), kc = c - q * (kEW / 8);
+            we[i] = ld16(a.down + (size_t(l) * kH + j * kRowsG + w * kRowsW + q) * kI + kEW * hk + 8 * kc);
         }
+        add_partials();
         {
-            float xv[NCH][8];
-            norm_lane<NCH>(vec, nd, a.eps, xv);
+            float xv[kNCH][8];
+            norm_lane<kNCH>(xres, nd, a.eps, xv);
 #pragma unroll
-            for (int j = 0; j < UD; ++j) {
-                const int ri = (w * UD + j) / NCH, c = j % NCH;
-                float acc = dot8(wd[j], xv[c], 0.f);
+            for (int jj = 0; jj < kUD; ++jj) {
+                const int ri = (w * kUD + jj) / kNCH, c = jj % kNCH;
+                float acc = dot8(wd[jj], xv[c], 0.f);
                 acc = wave_sum(acc);
-                if (lane == 0) red[ri * NCH + c] = acc;
+                if (lane == 0) red[ri * kNCH + c] = acc;
             }
         }
         lds_barrier();
-        if (t < PB * kReplicas) {  // thread t: pair t / 8 into copy t % 8
-            const int j = t / kReplicas, r = t % kReplicas;
+        if (t < kPB) {
             float g = 0.f, u = 0.f;
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                g += red[j * NCH + c];
-                u += red[(PB + j) * NCH + c];
+            for (int c = 0; c < kNCH; ++c) {
+                g += red[t * kNCH + c];
+                u += red[(kPB + t) * kNCH + c];
             }
-            xstore32(xv32 + X.a + r * I + b * PB + j, g / (1.0f + __expf(-g)) * u, par);
+            lstore32(o32 + X.a + kPB * j + t, g / (1.0f + __expf(-g)) * u, par);
         }
 
-        // ---------------------------------------------------------------- E: x += W_d . a
-        {
-            const uint32_t* src = xv32 + X.a + rep * I;
-            gather32<NCE * KSX>([&](int i) __attribute__((always_inline)) { return src + i; }, I, par, vec, hdr, 6,
-                             s_fail, wait_ticks);
-            if (s_fail) return;
-        }
-        {
-            float acc = 0.f;
-            const int kb0 = ks * (I / KS) + 8 * lane;
-#pragma unroll
-            for (int c = 0; c < NCE; ++c) acc = dot8_lds(we[c], vec, kb0 + 512 * c, acc);
-            acc = wave_sum(acc);
-            if (lane == 0) red[w] = acc;
-        }
+        // ---------------------------------------------------------------- E: p2[xcd] = W_d[:, the XCD's columns] . a
+        gather32x4<1>(o32 + X.a, kEW / 4, par, vec, hdr, 6, s_fail, wait_ticks);
+        if (s_fail) return;
+        rows_dot<kNCE, kEW / 8>(we, vec, red);
         lds_barrier();
-        if (t < RB * kReplicas) {
-            const int i = t / kReplicas, r = t % kReplicas;
-            float sum = 0.f;
-            for (int k = 0; k < KS; ++k) sum += red[i * KS + k];
-            const float xn = xown[i] + sum;
-            if (r == 0) xown[i] = xn;
-            xstore32(xv32 + X.x2 + r * H + b * RB + i, xn, par);
-        }
+        if (t < kRowsG) gstore32(l32 + X.p2 + xcd * kH + j * kRowsG + t, red[t], par);
         // the next layer's q|k|v rows and K/V chunks, after the rows above (after the last layer: its q|k|v rows
         // again, never used; unconditional, so the compiler's wait counting has one path to follow)
         issue_a(min(l + 1, a.layers - 1));
@@ -640,14 +671,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     }
 
     // ---------------------------------------------------------------- lm_head over rows [r0, r1), then the argmax
-    const int V = a.vocab, per = (V + G - 1) / G, r0 = b * per, r1 = min(V, r0 + per);
-    u32x4 ra[4][NCH], rb4[4][NCH], rc4[4][NCH], nf[NCH];
-    auto load4 = [&](u32x4 (&dst)[4][NCH], int row) __attribute__((always_inline)) {
+    const int V = a.vocab, per = (V + kG - 1) / kG, r0 = b * per, r1 = min(V, r0 + per);
+    u32x4 ra[4][kNCH], rb4[4][kNCH], rc4[4][kNCH], nf[kNCH];
+    auto load4 = [&](u32x4 (&dst)[4][kNCH], int row) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint16_t* er = a.embed + size_t(min(row + r, V - 1)) * H + 8 * lane;
+            const uint16_t* er = a.embed + size_t(min(row + r, V - 1)) * kH + 8 * lane;
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) dst[r][c] = ld16(er + 512 * c);
+            for (int c = 0; c < kNCH; ++c) dst[r][c] = ld16(er + 512 * c);
         }
     };
     // wave w visits rows r0 + 4 w + 32 j, four at a time, through three register sets (the next two sets in flight
@@ -656,23 +687,22 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     load4(ra, r0 + 4 * w);
     load4(rb4, r0 + 4 * w + RS);
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) nf[c] = ld16(a.final_norm + 512 * c + 8 * lane);
-    {
-        const uint32_t* src = x32 + size_t(a.layers - 1) * X.per_layer32 + X.x2 + rep * H;
-        gather32<NCH>([&](int i) { return src + i; }, H, par, vec, hdr, 7, s_fail, wait_ticks);
-        if (s_fail) return;
-    }
-    float xv[NCH][8];
-    norm_lane<NCH>(vec, nf, a.eps, xv);
+    for (int c = 0; c < kNCH; ++c) nf[c] = ld16(a.final_norm + 512 * c + 8 * lane);
+    gather32x4<4>(x32 + size_t(a.layers - 1) * X.per_layer32 + X.p2, kXcds * kH / 4, par, vec, hdr, 7, s_fail,
+                  wait_ticks);
+    if (s_fail) return;
+    add_partials();
+    float xv[kNCH][8];
+    norm_lane<kNCH>(xres, nf, a.eps, xv);
     float best = -INFINITY;
     uint32_t besti = 0xFFFFFFFFu;
     bool nan = false;
-    auto proc = [&](const u32x4 (&src)[4][NCH], int row) __attribute__((always_inline)) {
+    auto proc = [&](const u32x4 (&src)[4][kNCH], int row) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             float acc = 0.f;
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) acc = dot8(src[r][c], xv[c], acc);
+            for (int c = 0; c < kNCH; ++c) acc = dot8(src[r][c], xv[c], acc);
             const float v = wave_sum(acc);
             if (row + r >= r1) continue;
             if (a.write_logits && lane == r) a.logits[row + r] = v;
@@ -709,25 +739,25 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 ix = lmi[i];
             }
         }
-        xstore(lmp + 2 * b, bv, tag);
-        xstore(lmp + 2 * b + 1, __uint_as_float(bn ? 0xFFFFFFFEu : ix), tag);
+        gstore(lmp + 2 * b, bv, tag);
+        gstore(lmp + 2 * b + 1, __uint_as_float(bn ? 0xFFFFFFFEu : ix), tag);
     }
     if (b != 0) return;
 
     // workgroup 0: the lowest index of the maximum over the workgroups' pairs (0xFFFFFFFF when a logit is NaN)
-    gather<1>([&](int i) { return lmp + i; }, 2 * G, tag, vec, hdr, 8, s_fail, wait_ticks);
+    gather<1>([&](int i) { return lmp + i; }, 2 * kG, tag, vec, hdr, 8, s_fail, wait_ticks);
     if (s_fail) return;
     float bv = 0.f;
     uint32_t bi = 0xFFFFFFFFu;
     bool bn = false;
-    for (int i = t; i < G; i += kThreads) {
+    for (int i = t; i < kG; i += kThreads) {
         const float v = vec[2 * i];
-        const uint32_t j = __float_as_uint(vec[2 * i + 1]);
-        if (j == 0xFFFFFFFEu)
+        const uint32_t jx = __float_as_uint(vec[2 * i + 1]);
+        if (jx == 0xFFFFFFFEu)
             bn = true;
-        else if (j != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || v > bv || (v == bv && j < bi))) {
+        else if (jx != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || v > bv || (v == bv && jx < bi))) {
             bv = v;
-            bi = j;
+            bi = jx;
         }
     }
     lds_barrier();  // vec is reused for the tree below
@@ -792,17 +822,13 @@ void launch_decode_persistent(const PreparedDispatch& pd, void* const* p, hipStr
     a.out_ids = (uint32_t*)p[16];
     a.xch = (uint64_t*)p[17];
     a.layers = int(w[19]);
-    a.hidden = int(w[20]);
-    a.qh = int(w[21]);
-    a.kvh = int(w[22]);
-    a.inter = int(w[23]);
     a.vocab = int(w[24]);
     a.max_pos = int(w[25]);
     a.max_steps = int(w[26]);
     a.write_logits = int(w[27]);
     a.eps = f32(w[28]);
     a.scale_log2 = f32(w[29]) * 1.4426950408889634f;
-    auto kern = k_decode_persist<kNCH, kRA, kNCC, kUD, kNCE, kKS>;
+    auto kern = k_decode_persist;
     // every workgroup must be resident at once (they wait for each other): at least one per CU, G <= CUs
     static int occupancy = -1;
     if (occupancy < 0) hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occupancy, kern, kThreads, 0), "occupancy");
@@ -811,6 +837,7 @@ void launch_decode_persistent(const PreparedDispatch& pd, void* const* p, hipStr
     hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "attribute");
     if (occupancy < 1 || int64_t(pd.physical.x) > int64_t(cus) * occupancy)
         throw HipError("decode_step_persistent: the grid does not fit on the device at once");
+    if (pd.physical.x != uint32_t(kG)) throw HipError("decode_step_persistent: the kernel runs 256 workgroups");
     hipLaunchKernelGGL(kern, dim3(pd.physical.x), dim3(kThreads), 0, s, a);
 }
 
