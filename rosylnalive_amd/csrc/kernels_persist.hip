@@ -5,7 +5,7 @@
 // kernel boundaries. It computes what the multi-kernel step of the executor computes (embed_dec, then per layer
 // gemv_norm_dec, attention_decode_f16, attention_combine, gemv_residual_dec, gemv_swiglu_dec, gemv_residual_dec, then
 // lmhead_dec and argmax_dec) with the same per-lane products; the o_proj and down_proj sums run in another order (each
-// XCD's columns summed alone, then the eight sums added in XCD order), and the split combine runs one split per lane.
+// XCD's columns summed alone, then the eight sums added in XCD order), and the split combine sums the splits in order.
 //
 // Why: batch-1 decode of a 0.6B model moves ~1.2 GB per token, ~150 us at HBM speed, but as ~170 dependent kernels
 // it is bound by launch and ramp latency (4-6 us per kernel). Here each hand-off costs a store and a poll, and every
@@ -17,26 +17,27 @@
 // through to memory
 // and a device-scope load from another XCD fetches it there: 0.7 us one way, about 2.2 us for an all-gather between all
 // 256 workgroups. A plain store stays in the writer's L2, where a device-scope load from the same XCD finds it: 0.3 us.
-// So KV head h is XCD h's: its q|k|v rows, its 32 attention splits, their combine, and the o_proj and down_proj
-// columns that read its outputs (o_proj columns 256 h .. + 255, SwiGLU outputs and down_proj columns 384 h .. + 383).
-// Four of a layer's six hand-offs stay inside one L2; the o_proj and down_proj outputs leave as per-XCD partial sums
-// [8][hidden] through memory, and every workgroup adds them to its own copy of the residual stream.
+// So KV head h is XCD h's: its q|k|v rows, its 32 attention splits, and the o_proj and down_proj columns that read its
+// outputs (o_proj columns 256 h .. + 255, SwiGLU outputs and down_proj columns 384 h .. + 383). Three of a layer's five
+// hand-offs stay inside one L2; the o_proj and down_proj outputs leave as per-XCD partial sums [8][hidden] through
+// memory, and every workgroup adds them to its own copy of the residual stream as it gathers them.
 //
-// Exchange entries carry their own ready mark, so a consumer polls the data itself. 8-byte entries (q|k|v, the
-// attention partials, the lm_head partials): (tag << 32) | value bits; an entry is ready when it carries this launch's
-// tag, the launch epoch + 1 (header word 0, advanced by workgroup 0 at the end of every step), so entries left by
-// earlier steps never match. 4-byte entries (the combined o, the SwiGLU output, the o_proj and down_proj partial sums):
-// the value with its lowest mantissa bit replaced by the tag's parity; every such entry is written by every step, so
-// the previous step's entries always carry the other parity (after an aborted step the host zeroes the area).
+// Exchange entries carry their own ready mark, so a consumer polls the data itself. 8-byte entries (q|k|v, the lm_head
+// partials): (tag << 32) | value bits; an entry is ready when it carries this launch's tag, the launch epoch + 1 (header
+// word 0, advanced by workgroup 0 at the end of every step), so entries left by earlier steps never match. 4-byte
+// entries (the attention partials, the SwiGLU output, the o_proj and down_proj partial sums): the value with its lowest
+// mantissa bit replaced by the tag's parity; every entry that is read is written by every step (an attention split
+// that holds no keys writes an empty partial), so the previous step's entries always carry the other parity (after an
+// aborted step the host zeroes the area).
 //
 // Stages of layer l (Qwen3-0.6B: hidden 1024, 16/8 heads, intermediate 3072), workgroup b on XCD h, j = b / 8:
 //   A  q|k|v of KV head h = W . RMSNorm(x): 2 of the XCD's 512 rows per wave. Waits for x, i.e. for the previous
 //      layer's down_proj partial sums of all XCDs (all of x: the RMSNorm needs the whole row).
 //   B  attention: split j of KV head h takes keys [j KPS, (j + 1) KPS) (KPS a multiple of 64 chosen so 32 splits cover
 //      pos + 1 keys), both query heads, 64 keys at a time with an online softmax; the split holding pos also
-//      normalises, rotates and appends the new key and value. Writes (max, sum, out[128]) per query head.
-//   B' combine: 8 output dims of one of the XCD's query heads per workgroup, one split per lane.
-//   C  p1[h] = W_o[:, 256 h .. + 255] . o_h: 32 rows per workgroup.
+//      normalises, rotates and appends the new key and value. Writes (out[128], max, sum) per query head.
+//   C  o_h = the combine of the splits (every workgroup of the XCD forms all 256 dims), then
+//      p1[h] = W_o[:, 256 h .. + 255] . o_h: 32 rows per workgroup.
 //   D  a_h = silu(W_g . r) * (W_u . r), r = RMSNorm(x + sum_h p1[h]): 12 of the XCD's 384 gate/up pairs.
 //   E  p2[h] = W_d[:, 384 h .. + 383] . a_h: 32 rows per workgroup.
 // Then x += sum_h p2[h], every workgroup takes 1/256 of the lm_head rows and writes its (max, lowest index); workgroup
@@ -192,25 +193,30 @@ __device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, u
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 }
 
-// Block-wide: waits until the 4-byte entries base[0 .. 4 nv) (nv <= E * 512) carry `parity` and writes their values
-// to dst (16-byte aligned, LDS). 16-byte device-scope loads, four entries each; otherwise as gather.
-template <int E>
-__device__ __forceinline__ void gather32x4(const uint32_t* base, int nv, uint32_t parity, float* dst, uint32_t* hdr,
-                                           int stage, int& fail, long long limit) {
+// Block-wide: waits until the 4-byte entries of the 16-byte vectors at byte offsets voff(v) from base, v < nv
+// (nv <= E * 512, every offset below `bytes`), carry `parity` and writes vector v to dst[4 v .. 4 v + 3] (LDS, 16-byte
+// aligned). 16-byte device-scope loads, four entries each; otherwise as gather.
+template <int E, typename F>
+__device__ __forceinline__ void gather32x4(const uint32_t* base, int bytes, F voff, int nv, uint32_t parity,
+                                           float* dst, uint32_t* hdr, int stage, int& fail, long long limit) {
     const int t = threadIdx.x;
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(base), (short)0, nv * 16, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(base), (short)0, bytes, 0x00020000);
     constexpr int kSc1 = 16;  // the buffer load's cache policy: device scope (sc1)
     u32x4 v[E];
+    int off[E];
     bool pend[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) pend[e] = t + e * kThreads < nv;
+    for (int e = 0; e < E; ++e) {
+        pend[e] = t + e * kThreads < nv;
+        off[e] = pend[e] ? voff(t + e * kThreads) : 0;
+    }
     long long start = 0;
     for (int it = 0;; ++it) {
         asm volatile("" ::: "memory");  // every pass loads again
 #pragma unroll
         for (int e = 0; e < E; ++e)
-            if (pend[e]) v[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, (t + e * kThreads) * 16, 0, kSc1);
+            if (pend[e]) v[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[e], 0, kSc1);
         bool any = false;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -224,6 +230,57 @@ __device__ __forceinline__ void gather32x4(const uint32_t* base, int nv, uint32_
 #pragma unroll
     for (int e = 0; e < E; ++e)
         if (t + e * kThreads < nv) *reinterpret_cast<u32x4*>(dst + 4 * (t + e * kThreads)) = v[e];
+    lds_barrier();
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), as in gather
+}
+
+// Block-wide: waits for the per-XCD partial sums [kXcds][kH] at base (4-byte parity entries) and adds them to the
+// residual stream xres: thread t polls rows 4 (t % 256) .. + 3 of XCDs 4 (t / 256) .. + 3 and sums them in XCD order in
+// registers; the upper half's sums go through LDS (sc) to the lower half, which adds lower + upper to x. The same
+// order in every workgroup, so the same bits. As gather otherwise.
+__device__ __forceinline__ void gather_sum8(const uint32_t* base, uint32_t parity, float* xres, float* sc,
+                                            uint32_t* hdr, int stage, int& fail, long long limit) {
+    const int t = threadIdx.x, r4 = t & (kH / 4 - 1), x0 = (t / (kH / 4)) * 4;
+    static_assert(kThreads == 2 * (kH / 4) && kXcds == 8, "two threads per 4 rows, four XCDs each");
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(base), (short)0, kXcds * kH * 4, 0x00020000);
+    constexpr int kSc1 = 16;
+    u32x4 v[4];
+    bool pend[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) pend[x] = true;
+    long long start = 0;
+    for (int it = 0;; ++it) {
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+            if (pend[x]) v[x] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((x0 + x) * kH + 4 * r4) * 4, 0, kSc1);
+        bool any = false;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            const uint32_t all = v[x][0] & v[x][1] & v[x][2] & v[x][3], some = v[x][0] | v[x][1] | v[x][2] | v[x][3];
+            const bool ready = parity ? (all & 1u) != 0u : (some & 1u) == 0u;
+            pend[x] = pend[x] && !ready;
+            any |= pend[x];
+        }
+        if (!any || wait_over(it, start, limit, hdr, stage, fail)) break;
+    }
+    float4 sum;
+    sum.x = __uint_as_float(v[0][0]), sum.y = __uint_as_float(v[0][1]);
+    sum.z = __uint_as_float(v[0][2]), sum.w = __uint_as_float(v[0][3]);
+#pragma unroll
+    for (int x = 1; x < 4; ++x) {
+        sum.x += __uint_as_float(v[x][0]), sum.y += __uint_as_float(v[x][1]);
+        sum.z += __uint_as_float(v[x][2]), sum.w += __uint_as_float(v[x][3]);
+    }
+    if (x0) *reinterpret_cast<float4*>(sc + 4 * r4) = sum;
+    lds_barrier();
+    if (!x0) {
+        const float4 hi = *reinterpret_cast<const float4*>(sc + 4 * r4);
+        float4 xr = *reinterpret_cast<const float4*>(xres + 4 * r4);
+        xr.x += sum.x + hi.x, xr.y += sum.y + hi.y, xr.z += sum.z + hi.z, xr.w += sum.w + hi.w;
+        *reinterpret_cast<float4*>(xres + 4 * r4) = xr;
+    }
     lds_barrier();
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), as in gather
 }
@@ -300,7 +357,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     __shared__ __align__(16) float vec[kVecMax];
     __shared__ __align__(16) float xres[kH];  // the residual stream: every workgroup holds all of it, the same bits
     __shared__ float red[64];
-    __shared__ float qs[2][128];
+    __shared__ __align__(16) float qs[2][128];
     __shared__ float knew[128], vnew[128];
     __shared__ float ps[2][64];
     __shared__ float alpha_s[2];
@@ -359,17 +416,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         xres[k] = id < uint32_t(a.vocab) ? bf2f(a.embed[size_t(id) * kH + k]) : __uint_as_float(0x7FC00000u);
     lds_barrier();
 
-    // x += the XCDs' partial sums gathered in vec ([8][hidden]), added in XCD order: the same bits in every workgroup
-    auto add_partials = [&]() __attribute__((always_inline)) {
-        for (int k = t; k < kH; k += kThreads) {
-            float sum = vec[k];
-#pragma unroll
-            for (int x = 1; x < kXcds; ++x) sum += vec[x * kH + k];
-            xres[k] += sum;
-        }
-        lds_barrier();
-    };
-
     // This split's first 64-key chunks of K and V^T (one when the split holds one, else two): they do not depend on
     // this step, so the chunks of layer l + 1 load at the end of layer l (layer 0's here), away from stage A, where
     // loads in flight would hold back this workgroup's q|k|v rows. K: thread t holds key slots t / 16 and t / 16 + 32
@@ -402,9 +448,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         uint32_t* const o32 = l32 + size_t(xcd) * X.blk32;  // this XCD's 4-byte block
         // ---------------------------------------------------------------- A: q|k|v = W_qkv . RMSNorm(x)
         if (l > 0) {
-            gather32x4<4>(l32 - X.per_layer32 + X.p2, kXcds * kH / 4, par, vec, hdr, 1, s_fail, wait_ticks);
+            gather_sum8(l32 - X.per_layer32 + X.p2, par, xres, vec, hdr, 1, s_fail, wait_ticks);
             if (s_fail) return;
-            add_partials();
         }
         u32x4 wc[kNCC];
         {
@@ -556,9 +601,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             } else {
                 chunk(C0{}, Tail{}, c);
             }
-            // reduce the four key groups of each dim, then the partial rows of both heads, (max, sum, out[128]) and
-            // the padding, each written whole by one wave (wave hh: the XCD's query head hh) from LDS (qs and red are
-            // free after the chunks)
+            // reduce the four key groups of each dim, then the partial rows of both heads, (out[128], max, sum) and
+            // two pad entries, each written whole by one wave (wave hh: the XCD's query head hh) from LDS (qs and red
+            // are free after the chunks)
             o0 = quad4_sum(o0);
             o1 = quad4_sum(o1);
             if ((t & 3) == 0) {
@@ -571,45 +616,58 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             }
             lds_barrier();
             if (w < 2) {
-                uint64_t* pr = q64 + X.part + size_t(w * S + s) * kPartStride;
+                uint32_t* pr = o32 + X.part + size_t(w * S + s) * kPartStride;
 #pragma unroll
-                for (int i = lane; i < kPartStride; i += 64)
-                    lstore(pr + i, i < 2 ? red[2 * w + i] : i < 130 ? qs[w][i - 2] : 0.f, tag);
+                for (int i = lane; i < 4 * kPartVecs; i += 64)
+                    lstore32(pr + i, i < 128 ? qs[w][i] : i < 130 ? red[2 * w + i - 128] : 0.f, par);
             }
-        }
-
-        // ---------------------------------------------------------------- B': combine the splits
-        // query head hh = j / 16 of the XCD, dims 8 (j % 16) .. + 7, the S_used splits one per lane
-        {
-            const int hh = j / 16, d8 = (j % 16) * 8;
-            const uint64_t* src = q64 + X.part;
-            lds_barrier();  // vec may still be read by stage B's waves
-            gather<1>(
-                [&](int i) {
-                    const int sp = i / 10, k = i - sp * 10;
-                    return src + size_t(hh * S + sp) * kPartStride + (k < 2 ? k : d8 + k);
-                },
-                S_used * 10, tag, vec, hdr, 3, s_fail, wait_ticks);
-            if (s_fail) return;
-            {  // wave w: dim d8 + w; every wave forms the split weights
-                const bool ok = lane < S_used;
-                const float* v = vec + (ok ? lane : 0) * 10;
-                const float m = ok ? v[0] : -INFINITY;
-                const float M = wave_max(m);
-                const float e = ok ? exp2f(m - M) : 0.f;
-                const float L = wave_sum(ok ? v[1] * e : 0.f);
-                const float od = wave_sum(ok ? v[2 + w] * e : 0.f);
-                if (lane == 0) red[w] = od / L;
-            }
-            lds_barrier();
-            if (t < kWaves) lstore32(o32 + X.o + hh * 128 + d8 + t, red[t], par);
+        } else if (w < 2) {  // no keys in this split: its rows are not read, but every step writes them (parity)
+            uint32_t* pr = o32 + X.part + size_t(w * S + s) * kPartStride;
+#pragma unroll
+            for (int i = lane; i < 4 * kPartVecs; i += 64) lstore32(pr + i, 0.f, par);
         }
 
         // ---------------------------------------------------------------- C: p1[xcd] = W_o[:, the XCD's columns] . o
-        lds_barrier();  // the combine reads vec
-        gather32x4<1>(o32 + X.o, kCW / 4, par, vec, hdr, 4, s_fail, wait_ticks);
-        if (s_fail) return;
-        rows_dot<kNCC, kCW / 8>(wc, vec, red);
+        // o of the XCD's two query heads, formed by every workgroup from the splits' partial rows (row r = hh S_used
+        // + sp of the gathered rows at vec[132 r ..]): the split weights 2^(m_sp - M), summed in split order
+        lds_barrier();  // vec may still be read by stage B's waves
+        {
+            // up to 3 vectors per thread at once (more would spill registers); at long contexts the rest follow
+            constexpr int kV1 = 3 * kThreads;
+            auto voff = [&](int v) {
+                const int r = v / kPartVecs, c = v - r * kPartVecs, hh = r / S_used, sp = r - hh * S_used;
+                return ((hh * S + sp) * kPartStride + 4 * c) * 4;
+            };
+            const int nv = 2 * S_used * kPartVecs;
+            gather32x4<3>(o32 + X.part, 2 * S * kPartStride * 4, voff, min(nv, kV1), par, vec, hdr, 4, s_fail,
+                          wait_ticks);
+            if (s_fail) return;
+            if (nv > kV1) {
+                static_assert(2 * kJN * kPartVecs <= kV1 + 2 * kThreads, "the partial rows in two passes");
+                gather32x4<2>(o32 + X.part, 2 * S * kPartStride * 4, [&](int v) { return voff(v + kV1); }, nv - kV1,
+                              par, vec + 4 * kV1, hdr, 4, s_fail, wait_ticks);
+                if (s_fail) return;
+            }
+        }
+        if (w < 2) {  // wave hh: the split weights 2^(m_sp - M) / sum_sp 2^(m_sp - M) l_sp of query head hh, a split per lane
+            const bool ok = lane < S_used;
+            const float* r = vec + (w * S_used + (ok ? lane : 0)) * 4 * kPartVecs;
+            const float m = ok ? r[128] : -INFINITY;
+            const float M = wave_max(m);
+            const float e = ok ? exp2f(m - M) : 0.f;
+            const float L = wave_sum(ok ? r[129] * e : 0.f);
+            ps[w][lane] = e / L;
+        }
+        lds_barrier();
+        if (t < kCW) {
+            const int hh = t >> 7, d = t & 127;
+            const float* rows = vec + hh * S_used * 4 * kPartVecs + d;
+            float O = 0.f;
+            for (int sp = 0; sp < S_used; ++sp) O = fmaf(ps[hh][sp], rows[sp * 4 * kPartVecs], O);
+            qs[hh][d] = O;
+        }
+        lds_barrier();
+        rows_dot<kNCC, kCW / 8>(wc, &qs[0][0], red);
         lds_barrier();
         if (t < kRowsG) gstore32(l32 + X.p1 + xcd * kH + j * kRowsG + t, red[t], par);
         // stage D's gate/up weights, after the rows above: unit u = w kUD + jj is (row u / kNCH of the workgroup's
@@ -625,7 +683,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         for (int c = 0; c < kNCH; ++c) nd[c] = ld16(a.post_norm + size_t(l) * kH + 512 * c + 8 * lane);
 
         // ---------------------------------------------------------------- D: a = silu(W_g . h) * (W_u . h)
-        gather32x4<4>(l32 + X.p1, kXcds * kH / 4, par, vec, hdr, 5, s_fail, wait_ticks);
+        gather_sum8(l32 + X.p1, par, xres, vec, hdr, 5, s_fail, wait_ticks);
         if (s_fail) return;
         // stage E's down_proj weights (rows 32 j + 4 w + q, the XCD's 384 columns), before this stage computes:
         // issued after its outputs they land only after the hand-off to stage E
@@ -635,7 +693,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             const int c = lane + 64 * i, q = c / (kEW / 8), kc = c - q * (kEW / 8);
             we[i] = ld16(a.down + (size_t(l) * kH + j * kRowsG + w * kRowsW + q) * kI + kEW * hk + 8 * kc);
         }
-        add_partials();
         {
             float xv[kNCH][8];
             norm_lane<kNCH>(xres, nd, a.eps, xv);
@@ -659,7 +716,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         }
 
         // ---------------------------------------------------------------- E: p2[xcd] = W_d[:, the XCD's columns] . a
-        gather32x4<1>(o32 + X.a, kEW / 4, par, vec, hdr, 6, s_fail, wait_ticks);
+        gather32x4<1>(o32 + X.a, kEW * 4, [](int v) { return 16 * v; }, kEW / 4, par, vec, hdr, 6, s_fail, wait_ticks);
         if (s_fail) return;
         rows_dot<kNCE, kEW / 8>(we, vec, red);
         lds_barrier();
@@ -688,10 +745,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     load4(rb4, r0 + 4 * w + RS);
 #pragma unroll
     for (int c = 0; c < kNCH; ++c) nf[c] = ld16(a.final_norm + 512 * c + 8 * lane);
-    gather32x4<4>(x32 + size_t(a.layers - 1) * X.per_layer32 + X.p2, kXcds * kH / 4, par, vec, hdr, 7, s_fail,
-                  wait_ticks);
+    gather_sum8(x32 + size_t(a.layers - 1) * X.per_layer32 + X.p2, par, xres, vec, hdr, 7, s_fail, wait_ticks);
     if (s_fail) return;
-    add_partials();
     float xv[kNCH][8];
     norm_lane<kNCH>(xres, nf, a.eps, xv);
     float best = -INFINITY;

@@ -11,14 +11,15 @@ constexpr int kWaves = 8, kThreads = 512;
 // 256-byte header before the entries: u32 word 0 = launch epoch, 1 = abort, 2 = the stage that aborted, 3 = the bound
 // of every wait in 100 MHz constant-clock ticks (0: 0.2 s)
 constexpr int kHdrEntries = 32;
-constexpr int kVecMax = 8192;  // floats of the LDS vector a stage gathers its input into
-// The accelerator complex dies (XCDs) of an MI355X, each with its own L2: workgroup b of a launch runs on XCD b % 8.
-// KV head h lives on XCD h: its q|k|v rows, attention splits and split combine, and the o_proj / down_proj columns
-// that read them, so four of the six hand-offs of a layer stay inside one L2.
+constexpr int kVecMax = 8704;  // floats of the LDS vector a stage gathers its input into
+// The accelerator complex dies (XCDs) of an MI355X, each with its own L2. KV head h lives on XCD h: its q|k|v rows,
+// attention splits, and the o_proj / down_proj columns that read them, so three of a layer's five hand-offs stay
+// inside one L2.
 constexpr int kXcds = 8;
-// 8-byte entries per (query head, split) attention partial row: (max, sum, out[128]) padded to whole 128-byte lines, so
-// one wave writes every line of a row whole (lines written in part by several waves cost a read-modify-write each)
-constexpr int kPartStride = 144;
+// 4-byte entries per (query head, split) attention partial row: out[128], max, sum, padded to whole 128-byte lines, so
+// one wave writes every line of a row whole (lines written in part by several waves cost a read-modify-write each).
+// The first kPartVecs 16-byte vectors (out, max, sum, two pad entries) are what the readers poll.
+constexpr int kPartStride = 160, kPartVecs = 33;
 
 struct Shape {
     int hidden, heads, kv_heads, head_dim, inter, max_pos, blocks;
@@ -26,26 +27,25 @@ struct Shape {
 
 // The exchange area, per layer:
 //   8-byte entries (tag << 32) | value bits, one block per XCD (4 KB aligned, so no cache line is written by two
-//   XCDs): the XCD's q|k|v rows (its query heads, key, value: 128 each), then its attention partials per (query head,
-//   split) in rows of kPartStride entries;
+//   XCDs): the XCD's q|k|v rows (its query heads, key, value: 128 each);
 //   4-byte entries, the value with its lowest mantissa bit replaced by the launch parity: one block per XCD holding
-//   its combined attention output o (query heads x 128) and its slice of the SwiGLU output (inter / kXcds), then the
-//   device-wide partial sums [kXcds][hidden] of o_proj (p1) and of down_proj (p2), each XCD's columns summed alone.
+//   its attention partials per (query head, split) in rows of kPartStride entries and its slice of the SwiGLU output
+//   (inter / kXcds), then the device-wide partial sums [kXcds][hidden] of o_proj (p1) and of down_proj (p2), each XCD's
+//   columns summed alone.
 // The XCD blocks are written and read by one XCD only; p1, p2, the lm_head partials and the header by all.
 struct XLayout {
-    int qkv, part, blk64, per_layer64;       // 8-byte entries
-    int o, a, blk32, p1, p2, per_layer32;    // 4-byte entries
+    int qkv, blk64, per_layer64;             // 8-byte entries
+    int part, a, blk32, p1, p2, per_layer32;  // 4-byte entries
 #if defined(__HIPCC__)
     __host__ __device__
 #endif
     XLayout(int qh, int kvh, int hidden, int inter, int blocks) {
         const int S = blocks / kXcds, qpk = qh / kvh;
         qkv = 0;
-        part = (qpk + 2) * 128;
-        blk64 = (part + qpk * S * kPartStride + 511) / 512 * 512;
+        blk64 = ((qpk + 2) * 128 + 511) / 512 * 512;
         per_layer64 = kXcds * blk64;
-        o = 0;
-        a = qpk * 128;
+        part = 0;
+        a = qpk * S * kPartStride;
         blk32 = (a + inter / kXcds + 1023) / 1024 * 1024;
         p1 = kXcds * blk32;
         p2 = p1 + kXcds * hidden;
