@@ -126,6 +126,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["prefill_2048", "prefill_512"],
+                    help="run only this workload (for profiling runs) and print its figures as the JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -154,6 +156,24 @@ def main():
 
     def kv_bytes(ctx):
         return 2 * L * KVH * ctx * HD * 2
+
+    def prefill(T, rows, name):
+        """The forward of T synthetic tokens, logits of the last `rows` rows: the best of three warm runs."""
+        ids = synthetic_ids(args.seed, name, T, V)
+        model.forward(ids, 0, logits_rows=rows)
+        best = min((model.forward(ids, 0, logits_rows=rows), model.last_ms())[1] for _ in range(3))
+        fl = 2 * T * L * lin_params_layer + 2 * rows * V * H + L * QH * (T * (T + 1) // 2) * (4 * HD + 3)
+        return {"ms": round(best, 3), "tok_s": round(T / (best / 1e3), 1), "tflops": round(fl / (best / 1e3) / 1e12, 1),
+                "mfma_frac": round(fl / (best / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flop": fl}
+
+    if args.only:
+        T, rows = (2048, 1) if args.only == "prefill_2048" else (512, 512)
+        res = prefill(T, rows, "bench/" + args.only.replace("_", ""))
+        log(args.only, res)
+        print(json.dumps({"workload": args.only, **res}), flush=True)
+        model.close()
+        backend.close()
+        return
 
     # ---------------------------------------------------------------- headline: decode, context 128 + ...
     prompt = synthetic_ids(args.seed, "bench/prompt", 128, V)
@@ -297,23 +317,10 @@ def main():
     e_sample = None
     if not args.no_extras:
         # 512-token prefill with every logit row (all 512 x 151936 logits)
-        ids = synthetic_ids(args.seed, "bench/prefill512", 512, V)
-        model.forward(ids, 0, logits_rows=512)
-        best = min((model.forward(ids, 0, logits_rows=512), model.last_ms())[1] for _ in range(3))
-        fl = 2 * 512 * L * lin_params_layer + 2 * 512 * V * H + L * QH * (512 * 513 // 2) * (4 * HD + 3)
-        out["prefill_512_all_logits"] = {"ms": round(best, 3), "tok_s": round(512 / (best / 1e3), 1),
-                                         "tflops": round(fl / (best / 1e3) / 1e12, 1),
-                                         "mfma_frac": round(fl / (best / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                                         "flop": fl}
+        out["prefill_512_all_logits"] = prefill(512, 512, "bench/prefill512")
         log("prefill 512:", out["prefill_512_all_logits"])
         # 2048-token prefill, last-row logits
-        ids = synthetic_ids(args.seed, "bench/prefill2048", 2048, V)
-        model.forward(ids, 0, logits_rows=1)
-        best = min((model.forward(ids, 0, logits_rows=1), model.last_ms())[1] for _ in range(3))
-        fl = 2 * 2048 * L * lin_params_layer + 2 * V * H + L * QH * (2048 * 2049 // 2) * (4 * HD + 3)
-        out["prefill_2048"] = {"ms": round(best, 3), "tok_s": round(2048 / (best / 1e3), 1),
-                               "tflops": round(fl / (best / 1e3) / 1e12, 1),
-                               "mfma_frac": round(fl / (best / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flop": fl}
+        out["prefill_2048"] = prefill(2048, 1, "bench/prefill2048")
         log("prefill 2048:", out["prefill_2048"])
         # the isolated GQA prefill attention at T = 2048 on the caches the prefill just wrote (layer 0)
         cl = backend.begin()

@@ -198,8 +198,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     const uint16_t* const pa = p.a + kz;
     const uint16_t* const pw = p.w + kz;
     constexpr int WN = BN / 2, JT = WN / 16;    // columns per wave, MFMA tiles per wave
-    constexpr int GLD = GBK + 8;                // register path: LDS row stride (halves), padded against bank conflicts
-    constexpr int STAGE = DMA ? (GBM + BN) * GBK : (GBM + BN) * GLD;  // halves: the A tile then the W tile
+    // both paths: unpadded LDS rows of GBK halves, the 16-byte chunks XOR-swizzled (row r, position q holds k chunk
+    // q ^ (r % 8)), so a fragment read (16 rows, one chunk) spreads over the banks (padded 144-byte rows measured
+    // 14 % of the register path's cycles stalled on bank conflicts)
+    constexpr int STAGE = (GBM + BN) * GBK;  // halves: the A tile then the W tile
     // the two stages, or what the QKV epilogue needs after them (x32 32 KiB + the V^T tile 128 x 136 halves)
     constexpr int LDS_HALVES = EPI == EPI_QKV ? (2 * STAGE > 33792 ? 2 * STAGE : 33792) : 2 * STAGE;
     __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALVES];
@@ -338,16 +340,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         auto sstore = [&](auto set, int buf) __attribute__((always_inline)) {
             constexpr int S = decltype(set)::value;
             uint16_t* As = lds + buf * STAGE;
-            uint16_t* Bs = As + GBM * GLD;
+            uint16_t* Bs = As + GBM * GBK;
     #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int c = t + 256 * i;
-                *reinterpret_cast<u32x4*>(As + (c >> 3) * GLD + (c & 7) * 8) = ra[S][i];
+                const int c = t + 256 * i, r = c >> 3;
+                *reinterpret_cast<u32x4*>(As + r * GBK + (((c & 7) ^ (r & 7)) * 8)) = ra[S][i];
             }
     #pragma unroll
             for (int i = 0; i < BCH; ++i) {
-                const int c = t + 256 * i;
-                *reinterpret_cast<u32x4*>(Bs + (c >> 3) * GLD + (c & 7) * 8) = rb[S][i];
+                const int c = t + 256 * i, r = c >> 3;
+                *reinterpret_cast<u32x4*>(Bs + r * GBK + (((c & 7) ^ (r & 7)) * 8)) = rb[S][i];
             }
         };
 
@@ -358,14 +360,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         auto read_frags = [&](auto ksc, int buf) __attribute__((always_inline)) {
             constexpr int KS = decltype(ksc)::value;
             const uint16_t* As = lds + buf * STAGE;
-            const uint16_t* Bs = As + GBM * GLD;
-            const int kof = KS * 32 + 8 * g;
+            const uint16_t* Bs = As + GBM * GBK;
     #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                fa[KS][i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + (wm * 64 + i * 16 + c16) * GLD + kof));
+            for (int i = 0; i < 4; ++i) {
+                const int r = wm * 64 + i * 16 + c16;
+                fa[KS][i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + r * GBK + (((KS * 4 + g) ^ (r & 7)) * 8)));
+            }
     #pragma unroll
-            for (int j = 0; j < JT; ++j)
-                fb[KS][j] = as_f16x8(*reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 16 + c16) * GLD + kof));
+            for (int j = 0; j < JT; ++j) {
+                const int r = wn * WN + j * 16 + c16;
+                fb[KS][j] = as_f16x8(*reinterpret_cast<const u32x4*>(Bs + r * GBK + (((KS * 4 + g) ^ (r & 7)) * 8)));
+            }
         };
         auto mfma_half = [&](auto ksc) __attribute__((always_inline)) {
             constexpr int KS = decltype(ksc)::value;
