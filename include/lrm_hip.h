@@ -22,6 +22,7 @@ extern "C" {
 #define LRM_E_HIP 2      /* device lost, HIP API failure */
 #define LRM_E_ARG 3      /* invalid argument to the executor or a helper */
 #define LRM_E_INTERNAL 4
+#define LRM_E_RANGE 5 /* a value the fast path stores as fp16 (activation, K/V cache entry) became inf or NaN */
 
 #define LRM_ABI_VERSION 1
 

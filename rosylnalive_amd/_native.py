@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblrm_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "lrm_hip.h")
 
-LRM_OK, LRM_E_CONTRACT, LRM_E_HIP, LRM_E_ARG, LRM_E_INTERNAL = 0, 1, 2, 3, 4
+LRM_OK, LRM_E_CONTRACT, LRM_E_HIP, LRM_E_ARG, LRM_E_INTERNAL, LRM_E_RANGE = 0, 1, 2, 3, 4, 5
 
 
 class LrmError(RuntimeError):
@@ -28,6 +28,12 @@ class GpuContractException(LrmError):
 
 class HipDeviceError(LrmError):
     """A device or HIP API failure."""
+
+
+class Fp16RangeError(LrmError):
+    """A value the fast path stores as fp16 (normed hidden rows, q, the K/V cache, the attention or SwiGLU output)
+    became inf or NaN where the float32 reference stays finite: the call's results are not usable. The message names
+    the sites."""
 
 
 class DeviceInfo(C.Structure):
@@ -163,6 +169,8 @@ def check(rc: int) -> None:
         raise GpuContractException(rc, msg)
     if rc == LRM_E_HIP:
         raise HipDeviceError(rc, msg)
+    if rc == LRM_E_RANGE:
+        raise Fp16RangeError(rc, msg)
     if rc == LRM_E_ARG:
         raise LrmError(rc, "invalid argument: " + msg)
     raise LrmError(rc, msg)

@@ -24,6 +24,9 @@ static int guard(F&& f) {
     } catch (const HipError& e) {
         g_err = e.what();
         return LRM_E_HIP;
+    } catch (const RangeError& e) {
+        g_err = e.what();
+        return LRM_E_RANGE;
     } catch (const std::invalid_argument& e) {
         g_err = e.what();
         return LRM_E_ARG;

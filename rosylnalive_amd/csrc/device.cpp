@@ -81,6 +81,34 @@ Device::Device(int index, uint32_t flags) : index_(index), flags_(flags) {
     HIPC(hipEventCreate(&epoch_));
     HIPC(hipEventRecord(epoch_, stream_));
     static_scratch_ = static_scratch_address(index);
+    f16_range_[0] = f16_range_word_fast();
+    f16_range_[1] = f16_range_word_persist();
+}
+
+uint32_t Device::take_f16_range() {
+    HIPC(hipSetDevice(index_));
+    uint32_t bits = 0;
+    for (void* w : f16_range_) {
+        uint32_t v = 0;
+        HIPC(hipMemcpyAsync(&v, w, 4, hipMemcpyDeviceToHost, stream_));
+        HIPC(hipStreamSynchronize(stream_));
+        if (v) {
+            const uint32_t zero = 0;
+            HIPC(hipMemcpyAsync(w, &zero, 4, hipMemcpyHostToDevice, stream_));
+            HIPC(hipStreamSynchronize(stream_));
+        }
+        bits |= v;
+    }
+    return bits;
+}
+
+std::string f16_range_sites(uint32_t bits) {
+    static const char* names[] = {"normed hidden rows (h)", "query (q)", "K/V cache", "attention output (o)",
+                                  "SwiGLU output (a)"};
+    std::string out;
+    for (int i = 0; i < 5; ++i)
+        if (bits & (1u << i)) out += (out.empty() ? "" : ", ") + std::string(names[i]);
+    return out;
 }
 
 Device::~Device() {

@@ -28,6 +28,12 @@ struct HipError : std::runtime_error {
     using std::runtime_error::runtime_error;
 };
 
+// A value the fast path stores as fp16 (an activation or a K/V cache entry) became inf or NaN: the call's results
+// are not usable.
+struct RangeError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
 void hip_check(hipError_t e, const char* what);
 
 // The launch function of one catalog kernel: pointers per field (nullptr for non-token fields), the prepared words.
@@ -44,6 +50,13 @@ class CommandList;
 size_t static_scratch_bytes();
 void* static_scratch_address(int device);
 void record_decode_attention_static(Device& dev, CommandList* l, const uint32_t* words, uint32_t y);
+// The fp16 range words of the fast-path and persistent-decode code objects on the current GPU (hipGetSymbolAddress):
+// sticky bits of the sites where a kernel stored an inf or NaN half (1 normed hidden rows, 2 q, 4 K/V cache, 8 attention
+// output, 16 SwiGLU output).
+void* f16_range_word_fast();
+void* f16_range_word_persist();
+// The site names of a set of those bits, comma-separated.
+std::string f16_range_sites(uint32_t bits);
 
 struct DeviceInfo {
     int index;
@@ -151,6 +164,9 @@ class Device {
     hipStream_t stream() const { return stream_; }
     // This device's copy of the library's static scratch array (its address from hipGetSymbolAddress at creation)
     void* static_scratch() const { return static_scratch_; }
+    // The fp16 range sites (bits as f16_range_word_fast) that kernels on this GPU flagged since the last call, then
+    // cleared. The words are per GPU, shared by every backend on it; call after the work in question has completed.
+    uint32_t take_f16_range();
     void* slot_ptr(int slot) const;
     void* resolve(uint32_t token) const;  // device pointer of a token's first byte
 
@@ -169,6 +185,7 @@ class Device {
     hipEvent_t fork_ev_ = nullptr, join_ev_ = nullptr;
     hipEvent_t epoch_ = nullptr;
     void* static_scratch_ = nullptr;
+    void* f16_range_[2] = {nullptr, nullptr};
     bool heap_created_ = false;
     HeapLayout layout_;
     std::vector<void*> pages_;  // slot i at pages_[i], slot 0 = the table buffer

@@ -127,5 +127,32 @@ __device__ __forceinline__ float wave_sum(float v) { return cross_rows_sum(row_s
 
 __device__ __forceinline__ float wave_max(float v) { return cross_rows_max(row_max16(v)); }
 
+// ---------------------------------------------------------------- the fp16 range monitor
+// The fast path narrows some activations and the K/V cache to fp16, whose range ends at 65,504: a value the float32
+// reference keeps (a SwiGLU outlier, a large projection) becomes inf there. Every kernel that stores such a value ORs
+// the bit of its site into a sticky device word when a half it stores is inf or NaN; the executor reads and clears the
+// word after each forward and decode run and fails the call with the sites named, instead of passing the inf on. The
+// word starts at zero (static storage) and each code object including this header holds its own, one per GPU.
+enum F16Site : uint32_t {
+    kF16Hidden = 1u,  // RMSNorm output rows (the GEMM input h)
+    kF16Query = 2u,   // q after its norm and RoPE
+    kF16Cache = 4u,   // K or V cache entries
+    kF16Attn = 8u,    // the attention output o
+    kF16Swiglu = 16u  // the SwiGLU output a
+};
+static __device__ uint32_t f16_range_word;
+
+// 1 when a half of the pair is inf or NaN (exponent field all ones)
+__device__ __forceinline__ uint32_t f16_bad2(uint32_t p) {
+    return uint32_t((p & 0x7C00u) == 0x7C00u) | uint32_t((p & 0x7C000000u) == 0x7C000000u);
+}
+__device__ __forceinline__ uint32_t f16_bad8(u32x4 v) {
+    return f16_bad2(v[0]) | f16_bad2(v[1]) | f16_bad2(v[2]) | f16_bad2(v[3]);
+}
+// A vector atomic, issued only by the lanes that saw a bad value (none, on finite data).
+__device__ __forceinline__ void f16_note(uint32_t bad, uint32_t site) {
+    if (bad) __hip_atomic_fetch_or(&f16_range_word, site, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace fast
 }  // namespace lrm

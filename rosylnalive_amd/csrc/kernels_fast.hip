@@ -51,7 +51,13 @@ __global__ __launch_bounds__(256) void k_rmsnorm_f16(const float* x, const uint1
     ss = (red[0] + red[1]) + (red[2] + red[3]);
     float rr = 1.0f / sqrtf(ss / float(cols) + eps);
     uint16_t* yr = y + size_t(r) * cols;
-    for (uint32_t c = threadIdx.x; c < cols; c += 256u) yr[c] = f2h(bf2f(w[c]) * (xr[c] * rr));
+    uint32_t bad = 0;
+    for (uint32_t c = threadIdx.x; c < cols; c += 256u) {
+        const uint16_t h = f2h(bf2f(w[c]) * (xr[c] * rr));
+        bad |= f16_bad2(h);
+        yr[c] = h;
+    }
+    f16_note(bad, kF16Hidden);
 }
 
 // The same for cols = 256 NC (the model widths): one wave per row, four rows per block. Each lane loads its NC float4
@@ -77,12 +83,16 @@ __global__ __launch_bounds__(256) void k_rmsnorm_f16_wave(const float* x, const 
     ss = wave_sum(ss);
     const float rr = 1.0f / sqrtf(ss / float(cols) + eps);
     uint2* yr = reinterpret_cast<uint2*>(y + size_t(r) * cols) + lane;
+    uint32_t bad = 0;
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
         const float w0 = __uint_as_float(wv[j].x << 16), w1 = __uint_as_float(wv[j].x & 0xFFFF0000u);
         const float w2 = __uint_as_float(wv[j].y << 16), w3 = __uint_as_float(wv[j].y & 0xFFFF0000u);
-        yr[64 * j] = make_uint2(pack2h(w0 * (v[j].x * rr), w1 * (v[j].y * rr)), pack2h(w2 * (v[j].z * rr), w3 * (v[j].w * rr)));
+        const uint2 h = make_uint2(pack2h(w0 * (v[j].x * rr), w1 * (v[j].y * rr)), pack2h(w2 * (v[j].z * rr), w3 * (v[j].w * rr)));
+        bad |= f16_bad2(h.x) | f16_bad2(h.y);
+        yr[64 * j] = h;
     }
+    f16_note(bad, kF16Hidden);
 }
 
 // ================================================================ 40 residual_add_norm
@@ -132,12 +142,16 @@ __global__ __launch_bounds__(256) void k_resid_add_norm(float* x, const float* p
     ss = wave_sum(ss);
     const float rr = 1.0f / sqrtf(ss / float(cols) + eps);
     uint2* yr = reinterpret_cast<uint2*>(y + size_t(r) * cols) + lane;
+    uint32_t bad = 0;
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
         const float w0 = __uint_as_float(wv[j].x << 16), w1 = __uint_as_float(wv[j].x & 0xFFFF0000u);
         const float w2 = __uint_as_float(wv[j].y << 16), w3 = __uint_as_float(wv[j].y & 0xFFFF0000u);
-        yr[64 * j] = make_uint2(pack2h(w0 * (v[j].x * rr), w1 * (v[j].y * rr)), pack2h(w2 * (v[j].z * rr), w3 * (v[j].w * rr)));
+        const uint2 h = make_uint2(pack2h(w0 * (v[j].x * rr), w1 * (v[j].y * rr)), pack2h(w2 * (v[j].z * rr), w3 * (v[j].w * rr)));
+        bad |= f16_bad2(h.x) | f16_bad2(h.y);
+        yr[64 * j] = h;
     }
+    f16_note(bad, kF16Hidden);
 }
 
 // ================================================================ GEMM (ids 15, 17, 18, 19)
@@ -501,6 +515,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             uint16_t* out = is_q ? p.q_out + size_t(m) * (p.qh * 128) + head * 128
                                  : p.kc + (size_t(head - p.qh) * p.max_pos + pos) * 128;
             out += hf * 32;
+            uint32_t bad = 0;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {  // 8 dims d = 32 hf + 8 u + e and their partners d + 64
                 const u32x4 wl = *reinterpret_cast<const u32x4*>(nw + 8 * u);
@@ -525,10 +540,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                     }
                     lo[e2] = uint32_t(f2h(rl[0])) | (uint32_t(f2h(rl[1])) << 16);
                     hi[e2] = uint32_t(f2h(rh[0])) | (uint32_t(f2h(rh[1])) << 16);
+                    bad |= f16_bad2(lo[e2]) | f16_bad2(hi[e2]);
                 }
                 *reinterpret_cast<u32x4*>(out + 8 * u) = u32x4{lo[0], lo[1], lo[2], lo[3]};
                 *reinterpret_cast<u32x4*>(out + 64 + 8 * u) = u32x4{hi[0], hi[1], hi[2], hi[3]};
             }
+            f16_note(bad, is_q ? kF16Query : kF16Cache);
             return;
         }
     }
@@ -574,6 +591,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             }
         }
         __syncthreads();
+        uint32_t bad = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int q = t + 256 * k, row = q >> 3, ch = q & 7, m = m0 + row, col = tx * 64 + ch * 8;
@@ -581,11 +599,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             const u32x4 v = *reinterpret_cast<const u32x4*>(As + row * 72 + ch * 8);
             uint16_t* dst = p.y16 + size_t(m) * p.inter + col;
             if (col + 8 <= p.inter && (p.inter & 7) == 0) {
+                bad |= f16_bad8(v);
                 *reinterpret_cast<u32x4*>(dst) = v;
             } else {
-                for (int e = 0; e < 8 && col + e < p.inter; ++e) dst[e] = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+                for (int e = 0; e < 8 && col + e < p.inter; ++e) {
+                    const uint16_t h = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+                    bad |= f16_bad2(h);
+                    dst[e] = h;
+                }
             }
         }
+        f16_note(bad, kF16Swiglu);
         return;
     }
 
@@ -612,6 +636,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         const int p0 = p.pos0 + m0;
         const bool whole = (p0 & 7) == 0 && m0 + GBM <= p.M;  // 16-byte aligned, every row of the tile present
         const int ch = t & 15;
+        uint32_t bad = 0;
         uint16_t* vbase = p.vc + size_t(head - p.qh - p.kvh) * 128 * p.max_pos + p0 + ch * 8;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -619,13 +644,19 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             const u32x4 v = *reinterpret_cast<const u32x4*>(Vs + d * 136 + ch * 8);
             uint16_t* dst = vbase + size_t(d) * p.max_pos;
             if (whole) {
+                bad |= f16_bad8(v);
                 *reinterpret_cast<u32x4*>(dst) = v;
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    if (m0 + ch * 8 + e < p.M) dst[e] = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+                    if (m0 + ch * 8 + e < p.M) {
+                        const uint16_t h = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+                        bad |= f16_bad2(h);
+                        dst[e] = h;
+                    }
             }
         }
+        f16_note(bad, kF16Cache);
         return;
     }
 }
@@ -849,6 +880,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
         const float inv = 1.0f / (l_run * e0 + l1 * e1);
         const float f0 = e0 * inv, f1 = e1 * inv;
         uint16_t* yr = y + size_t(row) * QC + head * 128;
+        uint32_t bad = 0;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -857,9 +889,11 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
                 uint2 v;
                 v.x = pack2h(o[dt][4 * r4] * f0 + b[0] * f1, o[dt][4 * r4 + 1] * f0 + b[1] * f1);
                 v.y = pack2h(o[dt][4 * r4 + 2] * f0 + b[2] * f1, o[dt][4 * r4 + 3] * f0 + b[3] * f1);
+                bad |= f16_bad2(v.x) | f16_bad2(v.y);
                 // register r of tile dt: dim 32 dt + 8 (r / 4) + 4 h + r % 4
                 *reinterpret_cast<uint2*>(yr + 32 * dt + 8 * r4 + 4 * h) = v;
             }
+        f16_note(bad, kF16Attn);
     }
 }
 
@@ -1056,10 +1090,12 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
                 const uint16_t kh = f2h(krot);
                 knew[d] = h2f(kh);
                 kc[(size_t(kvhead) * max_pos + pos) * 128 + d] = kh;
+                f16_note(f16_bad2(kh), kF16Cache);
             } else {
                 const uint16_t vh = f2h(kvv);
                 vnew[d] = h2f(vh);
                 vc[(size_t(kvhead) * 128 + d) * max_pos + pos] = vh;
+                f16_note(f16_bad2(vh), kF16Cache);
             }
         }
     }
@@ -1239,10 +1275,13 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* part, OUT* y,
     if (par == 0) {
         const float v = (o + o_hi[d]) / L;
         OUT* yo = y + (size_t(b) * gridDim.x + h) * 128 + d;
-        if constexpr (sizeof(OUT) == 4)
+        if constexpr (sizeof(OUT) == 4) {
             *yo = v;
-        else
-            *yo = f2h(v);
+        } else {
+            const uint16_t hv = f2h(v);
+            f16_note(f16_bad2(hv), kF16Attn);
+            *yo = hv;
+        }
     }
 }
 
@@ -1606,7 +1645,11 @@ __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const ui
             gv += red[i][0][t];
             uv += red[i][NT - 1][t];
         }
-        if (row < M && col < inter) y16[size_t(row) * inter + col] = f2h(gv / (1.0f + __expf(-gv)) * uv);
+        if (row < M && col < inter) {
+            const uint16_t hv = f2h(gv / (1.0f + __expf(-gv)) * uv);
+            f16_note(f16_bad2(hv), kF16Swiglu);
+            y16[size_t(row) * inter + col] = hv;
+        }
         return;
     }
     if (t >= 256 * NT) return;
@@ -1837,6 +1880,13 @@ static uint32_t dec_splits(uint32_t max_pos, uint32_t chunks) {
 static uint32_t dec_grid_splits(uint32_t max_pos, uint32_t chunks, uint32_t splits) {
     return splits ? splits : dec_splits(max_pos, chunks);
 }
+void* f16_range_word_fast() {
+    void* p = nullptr;
+    hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(fast::f16_range_word)), "hipGetSymbolAddress(f16_range_word)");
+    if (!p) throw HipError("hipGetSymbolAddress(f16_range_word) returned a null address");
+    return p;
+}
+
 uint32_t decode_attention_splits(uint32_t max_pos, uint32_t chunks, uint32_t splits) {
     return dec_grid_splits(max_pos, chunks, splits);
 }

@@ -503,11 +503,17 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             } else if (t < 384) {
                 const uint16_t kh = f2h(rot);
                 knew[d] = h2f(kh);
-                if (has_pos) a.kc[((size_t(l) * kKVH + hk) * MP + pos) * 128 + d] = kh;
+                if (has_pos) {
+                    a.kc[((size_t(l) * kKVH + hk) * MP + pos) * 128 + d] = kh;
+                    f16_note(f16_bad2(kh), kF16Cache);
+                }
             } else {
                 const uint16_t vh = f2h(val);
                 vnew[d] = h2f(vh);
-                if (has_pos) a.vc[((size_t(l) * kKVH + hk) * 128 + d) * MP + pos] = vh;
+                if (has_pos) {
+                    a.vc[((size_t(l) * kKVH + hk) * 128 + d) * MP + pos] = vh;
+                    f16_note(f16_bad2(vh), kF16Cache);
+                }
             }
             lds_barrier();
             // this thread's query dims and, for the split holding pos, its slices of the new key and value (read
@@ -850,6 +856,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
 // fields: embed, final_norm, in_norm, qkv, q_norm, k_norm, o_proj, post_norm, gate_up, down, k_cache, v_cache, cos,
 // sin, logits, state, out_ids, exchange, layers, hidden, q_heads, kv_heads, inter, vocab, max_pos, max_steps,
 // write_logits, eps, scale, blocks
+void* f16_range_word_persist() {
+    void* p = nullptr;
+    hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(fast::f16_range_word)), "hipGetSymbolAddress(f16_range_word)");
+    if (!p) throw HipError("hipGetSymbolAddress(f16_range_word) returned a null address");
+    return p;
+}
+
 void launch_decode_persistent(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     auto f32 = [](uint32_t u) {

@@ -499,7 +499,15 @@ uint32_t QwenExec::forward(int seq, int pos0, const int32_t* ids, int t_, float*
             am = forward_fp32(pos0 + c0, n, lg, std::max(want, 1));
     }
     last_t_ = t_;
+    if (c.mode == 1) check_f16_range("forward");
     return am;
+}
+
+void QwenExec::check_f16_range(const char* what) {
+    const uint32_t bits = dev_.take_f16_range();
+    if (bits)
+        throw RangeError(std::string(what) + ": a value stored as fp16 left the fp16 range (|x| > 65504, or NaN) at: " +
+                         f16_range_sites(bits) + "; the results of this call are not usable");
 }
 
 uint32_t QwenExec::forward_fp32(int pos0, int T, float* logits, int lr) {
@@ -862,6 +870,7 @@ void QwenExec::run_decode_steps(int steps) {
             throw std::runtime_error("decode_step_persistent: a workgroup waited past its bound at stage " +
                                      std::to_string(hdr[2]) + "; the decode state did not advance from there");
     }
+    check_f16_range("decode");
 }
 
 void QwenExec::read_decode_ids(int32_t* out, int count) {

@@ -84,6 +84,8 @@ class QwenExec {
     void upload_rope(const uint32_t* inv_freq_bits);
     uint32_t forward_fp32(int pos0, int t, float* logits, int logits_rows);
     uint32_t forward_fast(int seq, int pos0, int t, float* logits, int logits_rows);
+    // Fast mode: fails the call (RangeError) when a kernel flagged an fp16 value out of range since the last check.
+    void check_f16_range(const char* what);
     void record_decode_fast();
     void record_decode_batch(CommandList* l);
     void sync_f16();  // refreshes the fp16 copies of the matrices written since the last forward

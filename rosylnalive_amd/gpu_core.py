@@ -15,10 +15,10 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import numpy as np
 
 from . import _native as N
-from ._native import GpuContractException, HipDeviceError, LrmError, check, lib, u32s, u64s
+from ._native import Fp16RangeError, GpuContractException, HipDeviceError, LrmError, check, lib, u32s, u64s
 
 __all__ = [
-    "GpuContractException", "HipDeviceError", "LrmError", "Heap", "DType", "Arena", "TensorFlags", "Catalog",
+    "Fp16RangeError", "GpuContractException", "HipDeviceError", "LrmError", "Heap", "DType", "Arena", "TensorFlags", "Catalog",
     "KernelSpec", "ArgBlock", "HeapLayout", "HeapPlanner", "TensorTable", "SealedTable", "HipBackendProvider",
     "HipBackend", "HipHeap", "HipCommandList", "Submission", "Completion", "TimerResult", "prepare", "grid_physical",
 ]
