@@ -23,6 +23,8 @@ extern "C" {
 #define LRM_E_ARG 3      /* invalid argument to the executor or a helper */
 #define LRM_E_INTERNAL 4
 #define LRM_E_RANGE 5 /* a value the fast path stores as fp16 (activation, K/V cache entry) became inf or NaN */
+#define LRM_E_FORMAT 6    /* SafetensorsFormatException (src/Lrm.Tensor/Safetensors.fs:15-17) */
+#define LRM_E_INTEGRITY 7 /* IntegrityException (Safetensors.fs:20-34): size or SHA-256 differs from the pinned one */
 
 #define LRM_ABI_VERSION 1
 
@@ -162,6 +164,13 @@ int lrm_qwen_destroy(lrm_qwen *q);
 /* Weights by Hugging Face name, bf16 bits (TinyModel.fs:79-101 names; tied lm_head = model.embed_tokens.weight). */
 int lrm_qwen_set_weight(lrm_qwen *q, const char *name, const uint16_t *data, uint64_t elems);
 int lrm_qwen_read_weight(lrm_qwen *q, const char *name, uint16_t *out, uint64_t elems);
+/* Every weight from a Qwen3 checkpoint (model.safetensors) through the validating reader below: each weight of the
+ * configuration present as BF16 with its exact shape, no other tensor but an optional lm_head.weight that must equal
+ * model.embed_tokens.weight byte for byte (Qwen3 ties them; the Qwen3-0.6B file stores both: 311 entries,
+ * tests/Lrm.Tensor.Tests/ModelTests.fs:16-29). Uploads straight from the mapped file in pieces of at most 64 MiB
+ * (UploadFrom, src/Lrm.Gpu.Core/Backend.fs:119-120). LRM_E_FORMAT for a malformed file, LRM_E_ARG for a file of
+ * another layout. */
+int lrm_qwen_load_safetensors(lrm_qwen *q, const char *path);
 /* TinyModel.forward (TinyModel.fs:144-204): ids at positions pos0 .. pos0 + t - 1; writes the cache; the last
  * logits_rows rows of logits (f32 [logits_rows, vocab]) when logits != NULL; *argmax = argmax of the last row
  * (0xFFFFFFFF for a row holding a NaN, argmaxRows semantics). */
@@ -202,6 +211,31 @@ uint64_t lrm_stream_of(const char *name);
 int lrm_synth_normal_f32(uint64_t seed, uint64_t stream, uint64_t n, float std, float *out);
 int lrm_synth_normal_bf16(uint64_t seed, uint64_t stream, uint64_t n, float std, uint16_t *out);
 int lrm_rope_table(const uint32_t *inv_freq_bits, int half, int max_pos, float *cos_out, float *sin_out);
+
+/* ---- safetensors: the validating reader (SafetensorsFile, src/Lrm.Tensor/Safetensors.fs:504-727) ----
+ * Open maps the file read-only and checks the 8-byte header length (at most 100,000,000), that the header is UTF-8
+ * JSON (nesting at most 8) whose keys are unique, that every entry has exactly dtype (F32, BF16, F16, I32, U32, U8,
+ * F64, I64), shape (non-negative integers) and data_offsets (a pair) with a byte count that matches, that metadata is
+ * an object of strings, and that the tensors tile the data section exactly (SafetensorsParse.header, :401-498).
+ * Entries and metadata come back in code point order of their names. Names are UTF-8 and may hold any character, so
+ * they are returned as (bytes, length), not NUL-terminated. */
+typedef struct lrm_st lrm_st;
+int lrm_st_open(const char *path, lrm_st **out);                                   /* SafetensorsFile.Open */
+int lrm_st_open_verified(const char *path, int64_t bytes, const char *sha256_hex, lrm_st **out); /* .OpenVerified */
+int lrm_st_validate(const uint8_t *bytes, uint64_t n, lrm_st **out);               /* SafetensorsFile.Validate */
+/* HeaderLength, DataOffset, Entries.Length, Metadata.Length, IsAligned, Length */
+int lrm_st_info(const lrm_st *f, int64_t *header_length, int64_t *data_offset, int32_t *entries, int32_t *metadata,
+                int32_t *aligned, uint64_t *length);
+/* Entry i: up to name_cap bytes of its name (*name_len = the full length), dtype code, rank and up to dims_cap dims,
+ * data offsets [begin, end) from the start of the data section. */
+int lrm_st_entry(const lrm_st *f, int i, char *name, int name_cap, int32_t *name_len, uint32_t *dtype, int32_t *rank,
+                 int64_t *dims, int dims_cap, int64_t *begin, int64_t *end);
+int lrm_st_metadata(const lrm_st *f, int i, char *key, int key_cap, int32_t *key_len, char *value, int value_cap,
+                    int32_t *value_len);
+/* A pointer to entry i's bytes in the mapping, valid until lrm_st_close (SafetensorsFile.Span); i = -1: the file's
+ * first byte (HeaderBytes). */
+int lrm_st_data(const lrm_st *f, int i, const void **data);
+int lrm_st_close(lrm_st *f);
 
 #ifdef __cplusplus
 }

@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(HERE, "liblrm_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "lrm_hip.h")
 
 LRM_OK, LRM_E_CONTRACT, LRM_E_HIP, LRM_E_ARG, LRM_E_INTERNAL, LRM_E_RANGE = 0, 1, 2, 3, 4, 5
+LRM_E_FORMAT, LRM_E_INTEGRITY = 6, 7
 
 
 class LrmError(RuntimeError):
@@ -28,6 +29,15 @@ class GpuContractException(LrmError):
 
 class HipDeviceError(LrmError):
     """A device or HIP API failure."""
+
+
+class SafetensorsFormatError(LrmError):
+    """SafetensorsFormatException (src/Lrm.Tensor/Safetensors.fs:15-17): the file breaks a format rule; the message
+    names the file and the rule."""
+
+
+class IntegrityError(LrmError):
+    """IntegrityException (Safetensors.fs:20-34): the file's size or SHA-256 differs from the pinned one."""
 
 
 class Fp16RangeError(LrmError):
@@ -120,6 +130,18 @@ PROTOTYPES = {
     "lrm_qwen_destroy": (C.c_int, [P]),
     "lrm_qwen_set_weight": (C.c_int, [P, C.c_char_p, P, C.c_uint64]),
     "lrm_qwen_read_weight": (C.c_int, [P, C.c_char_p, P, C.c_uint64]),
+    "lrm_qwen_load_safetensors": (C.c_int, [P, C.c_char_p]),
+    "lrm_st_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+    "lrm_st_open_verified": (C.c_int, [C.c_char_p, C.c_int64, C.c_char_p, C.POINTER(P)]),
+    "lrm_st_validate": (C.c_int, [P, C.c_uint64, C.POINTER(P)]),
+    "lrm_st_info": (C.c_int, [P, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.POINTER(C.c_int32),
+                              C.POINTER(C.c_int32), C.POINTER(C.c_int32), U64P]),
+    "lrm_st_entry": (C.c_int, [P, C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_int32), U32P, C.POINTER(C.c_int32),
+                               C.POINTER(C.c_int64), C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    "lrm_st_metadata": (C.c_int, [P, C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_int32), C.c_char_p, C.c_int,
+                                  C.POINTER(C.c_int32)]),
+    "lrm_st_data": (C.c_int, [P, C.c_int, C.POINTER(P)]),
+    "lrm_st_close": (C.c_int, [P]),
     "lrm_qwen_forward": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, P, C.c_int, U32P]),
     "lrm_qwen_greedy": (C.c_int, [P, P, C.c_int, C.c_int, P]),
     "lrm_qwen_decode_set": (C.c_int, [P, P, P]),
@@ -171,6 +193,10 @@ def check(rc: int) -> None:
         raise HipDeviceError(rc, msg)
     if rc == LRM_E_RANGE:
         raise Fp16RangeError(rc, msg)
+    if rc == LRM_E_FORMAT:
+        raise SafetensorsFormatError(rc, msg)
+    if rc == LRM_E_INTEGRITY:
+        raise IntegrityError(rc, msg)
     if rc == LRM_E_ARG:
         raise LrmError(rc, "invalid argument: " + msg)
     raise LrmError(rc, msg)

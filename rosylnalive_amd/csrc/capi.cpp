@@ -1,13 +1,17 @@
 // extern "C" entry points of liblrm_hip.so (include/lrm_hip.h): thin wrappers that map C++ exceptions to status codes
 // and a thread-local message.
+#include <algorithm>
+#include <cctype>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <string>
 
 #include "../../include/lrm_hip.h"
 #include "contract.hpp"
 #include "device.hpp"
 #include "qwen_exec.hpp"
+#include "safetensors.hpp"
 
 using namespace lrm;
 
@@ -27,6 +31,12 @@ static int guard(F&& f) {
     } catch (const RangeError& e) {
         g_err = e.what();
         return LRM_E_RANGE;
+    } catch (const FormatError& e) {
+        g_err = e.what();
+        return LRM_E_FORMAT;
+    } catch (const IntegrityError& e) {
+        g_err = e.what();
+        return LRM_E_INTEGRITY;
     } catch (const std::invalid_argument& e) {
         g_err = e.what();
         return LRM_E_ARG;
@@ -598,6 +608,114 @@ int lrm_rope_table(const uint32_t* inv, int half, int max_pos, float* c, float* 
         need_ptr(c, "cos");
         need_ptr(s, "sin");
         rope_table(inv, half, max_pos, c, s);
+    });
+}
+
+// ---------------------------------------------------------------- safetensors
+
+struct lrm_st {
+    std::unique_ptr<StFile> f;
+};
+
+static void copy_bytes(char* dst, int cap, int32_t* len, const std::string& s) {
+    if (len) *len = int32_t(s.size());
+    if (dst && cap > 0) std::memcpy(dst, s.data(), std::min(size_t(cap), s.size()));
+}
+
+int lrm_st_open(const char* path, lrm_st** out) {
+    return guard([&] {
+        need_ptr(path, "path");
+        need_ptr(out, "out");
+        *out = new lrm_st{StFile::open(path)};
+    });
+}
+
+int lrm_st_open_verified(const char* path, int64_t bytes, const char* sha256_hex, lrm_st** out) {
+    return guard([&] {
+        need_ptr(path, "path");
+        need_ptr(sha256_hex, "sha256");
+        need_ptr(out, "out");
+        std::string h(sha256_hex);
+        for (char& ch : h) ch = char(std::tolower(uint8_t(ch)));
+        if (h.size() != 64 || h.find_first_not_of("0123456789abcdef") != std::string::npos)
+            throw std::invalid_argument("sha256 must be 64 hex digits");
+        if (bytes < 0) throw std::invalid_argument("the pinned size is negative");
+        *out = new lrm_st{StFile::open(path, bytes, h.c_str())};
+    });
+}
+
+int lrm_st_validate(const uint8_t* bytes, uint64_t n, lrm_st** out) {
+    return guard([&] {
+        if (n) need_ptr(bytes, "bytes");
+        need_ptr(out, "out");
+        static const uint8_t none = 0;
+        *out = new lrm_st{StFile::from_memory(n ? bytes : &none, n)};
+    });
+}
+
+int lrm_st_info(const lrm_st* f, int64_t* header_length, int64_t* data_offset, int32_t* entries, int32_t* metadata,
+                int32_t* aligned, uint64_t* length) {
+    return guard([&] {
+        need_ptr(f, "file");
+        if (header_length) *header_length = f->f->header_length();
+        if (data_offset) *data_offset = f->f->data_offset();
+        if (entries) *entries = int32_t(f->f->entries().size());
+        if (metadata) *metadata = int32_t(f->f->metadata().size());
+        if (aligned) *aligned = f->f->aligned() ? 1 : 0;
+        if (length) *length = f->f->length();
+    });
+}
+
+int lrm_st_entry(const lrm_st* f, int i, char* name, int name_cap, int32_t* name_len, uint32_t* dtype, int32_t* rank,
+                 int64_t* dims, int dims_cap, int64_t* begin, int64_t* end) {
+    return guard([&] {
+        need_ptr(f, "file");
+        const auto& es = f->f->entries();
+        if (i < 0 || size_t(i) >= es.size()) throw std::invalid_argument("entry " + std::to_string(i) + " of " + std::to_string(es.size()));
+        const StEntry& e = es[size_t(i)];
+        copy_bytes(name, name_cap, name_len, e.name);
+        if (dtype) *dtype = e.dtype;
+        if (rank) *rank = int32_t(e.shape.size());
+        for (size_t k = 0; dims && k < e.shape.size() && int(k) < dims_cap; ++k) dims[k] = e.shape[k];
+        if (begin) *begin = e.begin;
+        if (end) *end = e.end;
+    });
+}
+
+int lrm_st_metadata(const lrm_st* f, int i, char* key, int key_cap, int32_t* key_len, char* value, int value_cap,
+                    int32_t* value_len) {
+    return guard([&] {
+        need_ptr(f, "file");
+        const auto& m = f->f->metadata();
+        if (i < 0 || size_t(i) >= m.size()) throw std::invalid_argument("metadata " + std::to_string(i) + " of " + std::to_string(m.size()));
+        copy_bytes(key, key_cap, key_len, m[size_t(i)].first);
+        copy_bytes(value, value_cap, value_len, m[size_t(i)].second);
+    });
+}
+
+int lrm_st_data(const lrm_st* f, int i, const void** data) {
+    return guard([&] {
+        need_ptr(f, "file");
+        need_ptr(data, "data");
+        const auto& es = f->f->entries();
+        if (i == -1) {
+            *data = f->f->bytes();
+            return;
+        }
+        if (i < 0 || size_t(i) >= es.size()) throw std::invalid_argument("entry " + std::to_string(i));
+        *data = f->f->data(es[size_t(i)]);
+    });
+}
+
+int lrm_st_close(lrm_st* f) {
+    return guard([&] { delete f; });
+}
+
+int lrm_qwen_load_safetensors(lrm_qwen* q, const char* path) {
+    return guard([&] {
+        need_ptr(q, "model");
+        need_ptr(path, "path");
+        q->q.load_safetensors(path);
     });
 }
 

@@ -1,5 +1,6 @@
 // The Qwen3 executor (see qwen_exec.hpp).
 #include "qwen_exec.hpp"
+#include "safetensors.hpp"
 
 #include "persist.hpp"
 
@@ -414,6 +415,12 @@ void QwenExec::upload_rope(const uint32_t* inv) {
 std::vector<std::string> QwenExec::weight_names() const { return weight_names_; }
 
 void QwenExec::set_weight(const std::string& name, const uint16_t* data, uint64_t elems) {
+    set_weight_bytes(name, reinterpret_cast<const uint8_t*>(data), elems);
+}
+
+// The bf16 elements as little-endian byte pairs (a mapped file need not align them), uploaded in pieces of at most
+// 64 MiB.
+void QwenExec::set_weight_bytes(const std::string& name, const uint8_t* data, uint64_t elems) {
     const Tensor& tt = t(name);
     uint64_t n = 1;
     for (uint32_t d : tt.dims) n *= d;
@@ -422,14 +429,49 @@ void QwenExec::set_weight(const std::string& name, const uint16_t* data, uint64_
     if (f16_copy_.count(base)) {
         // the fp16 copy must hold the same values: |w| >= 65536 has no fp16 counterpart
         for (uint64_t i = 0; i < elems; ++i) {
-            uint16_t a = data[i] & 0x7FFFu;
+            const uint16_t w = uint16_t(data[2 * i] | (uint16_t(data[2 * i + 1]) << 8)), a = w & 0x7FFFu;
             if (a >= 0x4780u && a < 0x7F80u)
                 arg_fail("weight %s element %llu (bf16 %04x) is outside the fp16 range the fast path computes in",
-                         name.c_str(), (unsigned long long)i, data[i]);
+                         name.c_str(), (unsigned long long)i, w);
         }
         f16_dirty_.insert(base);
     }
-    upload_tensor(name, data, elems * 2);
+    constexpr uint64_t kPiece = uint64_t(64) << 20;
+    for (uint64_t off = 0; off < elems * 2; off += kPiece)
+        upload_tensor(name, data + off, std::min(kPiece, elems * 2 - off), off);
+}
+
+void QwenExec::load_safetensors(const std::string& path) {
+    std::unique_ptr<StFile> f = StFile::open(path);
+    const char* p = f->path().c_str();
+    const std::set<std::string> expected(weight_names_.begin(), weight_names_.end());
+    for (const StEntry& e : f->entries())
+        if (e.name != "lm_head.weight" && !expected.count(e.name))
+            arg_fail("%s: tensor %s is not a weight of this Qwen3 configuration", p, e.name.c_str());
+    auto check = [&](const StEntry* e, const std::string& name, const std::vector<uint32_t>& dims) {
+        if (!e) arg_fail("%s: no tensor %s", p, name.c_str());
+        if (e->dtype != BF16) arg_fail("%s: %s is %s, not bf16", p, name.c_str(), dtype_name(e->dtype));
+        bool same = e->shape.size() == dims.size();
+        for (size_t k = 0; same && k < dims.size(); ++k) same = e->shape[k] == int64_t(dims[k]);
+        if (!same) {
+            std::string got, want;
+            for (int64_t d : e->shape) got += (got.empty() ? "" : ", ") + std::to_string(d);
+            for (uint32_t d : dims) want += (want.empty() ? "" : ", ") + std::to_string(d);
+            arg_fail("%s: %s has shape [%s], not [%s]", p, name.c_str(), got.c_str(), want.c_str());
+        }
+    };
+    for (const std::string& n : weight_names_) check(f->find(n), n, t(n).dims);
+    // Qwen3 ties the output projection to the embedding: a stored lm_head must be a byte-exact copy of it
+    const StEntry* emb = f->find("model.embed_tokens.weight");
+    if (const StEntry* lm = f->find("lm_head.weight")) {
+        check(lm, "lm_head.weight", t("model.embed_tokens.weight").dims);
+        if (std::memcmp(f->data(*lm), f->data(*emb), size_t(emb->bytes())) != 0)
+            arg_fail("%s: lm_head.weight differs from model.embed_tokens.weight; this executor ties them", p);
+    }
+    for (const std::string& n : weight_names_) {
+        const StEntry* e = f->find(n);
+        set_weight_bytes(n, f->data(*e), uint64_t(e->bytes() / 2));
+    }
 }
 
 void QwenExec::sync_f16() {

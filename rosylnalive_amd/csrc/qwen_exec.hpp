@@ -42,6 +42,10 @@ class QwenExec {
 
     // Weights by their Hugging Face names (bf16 bits).
     void set_weight(const std::string& name, const uint16_t* data, uint64_t elems);
+    // Every weight from a Qwen3 checkpoint in safetensors form (the validating reader): each weight of this
+    // configuration present as bf16 with its exact shape, nothing else but an optional lm_head.weight identical to
+    // the tied embedding.
+    void load_safetensors(const std::string& path);
     std::vector<std::string> weight_names() const;
     void read_weight(const std::string& name, uint16_t* out, uint64_t elems);
 
@@ -84,6 +88,7 @@ class QwenExec {
     void upload_rope(const uint32_t* inv_freq_bits);
     uint32_t forward_fp32(int pos0, int t, float* logits, int logits_rows);
     uint32_t forward_fast(int seq, int pos0, int t, float* logits, int logits_rows);
+    void set_weight_bytes(const std::string& name, const uint8_t* data, uint64_t elems);
     // Fast mode: fails the call (RangeError) when a kernel flagged an fp16 value out of range since the last check.
     void check_f16_range(const char* what);
     void record_decode_fast();

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 import json
+import os
 from dataclasses import asdict, dataclass
 from typing import Dict, List, Optional, Sequence
 
@@ -177,6 +178,12 @@ class QwenModel:
     def set_weight(self, name: str, bits: np.ndarray) -> None:
         a = np.ascontiguousarray(bits, dtype=np.uint16)
         check(lib().lrm_qwen_set_weight(self._h, name.encode(), a.ctypes.data, a.size))
+
+    def load_safetensors(self, path: str) -> None:
+        """Every weight from a Qwen3 checkpoint through the library's validating reader: each weight of this
+        configuration as BF16 with its exact shape, nothing else but an optional lm_head.weight equal to the tied
+        embedding byte for byte."""
+        check(lib().lrm_qwen_load_safetensors(self._h, os.fsencode(path)))
 
     def load_weights(self, weights: Dict[str, np.ndarray]) -> None:
         for name in self.cfg.weight_shapes():
