@@ -25,6 +25,7 @@ extern "C" {
 #define LRM_E_RANGE 5 /* a value the fast path stores as fp16 (activation, K/V cache entry) became inf or NaN */
 #define LRM_E_FORMAT 6    /* SafetensorsFormatException (src/Lrm.Tensor/Safetensors.fs:15-17) */
 #define LRM_E_INTEGRITY 7 /* IntegrityException (Safetensors.fs:20-34): size or SHA-256 differs from the pinned one */
+#define LRM_E_DATA 8      /* InvalidDataException (src/Lrm.Tokenizer/TokenizerJson.fs:24-25): tokenizer.json refused */
 
 #define LRM_ABI_VERSION 1
 
@@ -236,6 +237,38 @@ int lrm_st_metadata(const lrm_st *f, int i, char *key, int key_cap, int32_t *key
  * first byte (HeaderBytes). */
 int lrm_st_data(const lrm_st *f, int i, const void **data);
 int lrm_st_close(lrm_st *f);
+
+/* ---- tokenizer: the Qwen3 byte-level BPE tokenizer (QwenTokenizer, src/Lrm.Tokenizer/QwenTokenizer.fs) ----
+ * Encode: added tokens on the raw text (leftmost-longest), then for each stretch between them the oracle's NFC, the
+ * Split pre-tokenizer and byte-level BPE; no BOS or EOS. Output arrays follow one rule: when the buffer is NULL or
+ * `cap` is smaller than the result, nothing is written; *count (*len) is the result's size either way. */
+typedef struct lrm_tok lrm_tok;
+/* QwenTokenizer.parse: tokenizer.json bytes with the loader's checks (TokenizerJson.parse, TokenizerJson.fs:227-250):
+ * LRM_E_DATA for any configuration other than Qwen3's. */
+int lrm_tok_parse(const uint8_t *json, uint64_t n, lrm_tok **out);
+int lrm_tok_destroy(lrm_tok *t);
+int lrm_tok_info(const lrm_tok *t, int32_t *vocab_size, int32_t *merges, int32_t *added); /* VocabSize, MergeCount */
+int lrm_tok_added(const lrm_tok *t, int i, int32_t *id, char *content, int cap, int32_t *len, int32_t *special);
+/* Encode (UTF-8 text; LRM_E_ARG for ill-formed UTF-8, the reference's refusal of a lone surrogate) and EncodeBytes
+ * (each maximal ill-formed subpart becomes U+FFFD first). */
+int lrm_tok_encode(const lrm_tok *t, const uint8_t *utf8, uint64_t n, int32_t *ids, uint64_t cap, uint64_t *count);
+int lrm_tok_encode_bytes(const lrm_tok *t, const uint8_t *bytes, uint64_t n, int32_t *ids, uint64_t cap,
+                         uint64_t *count);
+/* DecodeBytes: LRM_E_ARG for an id outside [0, 151936); ids from VocabSize up to 151936 give no bytes. */
+int lrm_tok_decode_bytes(const lrm_tok *t, const int32_t *ids, uint64_t n, uint8_t *out, uint64_t cap, uint64_t *len);
+int lrm_tok_id_of(const lrm_tok *t, const uint8_t *token, uint64_t n, int32_t *id); /* IdOf; -1 for none */
+int lrm_tok_token_of(const lrm_tok *t, int32_t id, char *out, int cap, int32_t *len); /* TokenOf; *len -1: none */
+/* The stages alone, for their tests: PreTokenizer.split (piece start byte offsets, then the text's length), Nfc.normalize,
+ * and per scalar 0 .. 0x10FFFF the Split class (0 letter, 1 number, 2 space, 3 other), the contraction letter (0 for
+ * none) and whether NFC splits there (each array 0x110000 bytes, NULL to skip), and the byte map. */
+int lrm_tok_pre_split(const uint8_t *utf8, uint64_t n, uint64_t *bounds, uint64_t cap, uint64_t *count);
+int lrm_tok_nfc(const uint8_t *utf8, uint64_t n, uint8_t *out, uint64_t cap, uint64_t *len);
+/* Nfc.normalize of many strings at once: string i is text[offsets[i] .. offsets[i + 1]) (count + 1 offsets); the
+ * results are concatenated in out, string i at out_offsets[i] .. out_offsets[i + 1]. */
+int lrm_tok_nfc_many(const uint8_t *text, const uint64_t *offsets, uint64_t count, uint8_t *out, uint64_t cap,
+                     uint64_t *out_offsets, uint64_t *len);
+int lrm_tok_scalar_tables(uint8_t *classes, uint8_t *contraction, uint8_t *nfc_split);
+int lrm_tok_byte_char(int b, uint32_t *c);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ LIB_PATH = os.path.join(HERE, "liblrm_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "lrm_hip.h")
 
 LRM_OK, LRM_E_CONTRACT, LRM_E_HIP, LRM_E_ARG, LRM_E_INTERNAL, LRM_E_RANGE = 0, 1, 2, 3, 4, 5
-LRM_E_FORMAT, LRM_E_INTEGRITY = 6, 7
+LRM_E_FORMAT, LRM_E_INTEGRITY, LRM_E_DATA = 6, 7, 8
 
 
 class LrmError(RuntimeError):
@@ -38,6 +38,11 @@ class SafetensorsFormatError(LrmError):
 
 class IntegrityError(LrmError):
     """IntegrityException (Safetensors.fs:20-34): the file's size or SHA-256 differs from the pinned one."""
+
+
+class TokenizerDataError(LrmError):
+    """InvalidDataException of the tokenizer loader (src/Lrm.Tokenizer/TokenizerJson.fs:24-25): tokenizer.json holds
+    a configuration this tokenizer does not run."""
 
 
 class Fp16RangeError(LrmError):
@@ -142,6 +147,21 @@ PROTOTYPES = {
                                   C.POINTER(C.c_int32)]),
     "lrm_st_data": (C.c_int, [P, C.c_int, C.POINTER(P)]),
     "lrm_st_close": (C.c_int, [P]),
+    "lrm_tok_parse": (C.c_int, [P, C.c_uint64, C.POINTER(P)]),
+    "lrm_tok_destroy": (C.c_int, [P]),
+    "lrm_tok_info": (C.c_int, [P, C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    "lrm_tok_added": (C.c_int, [P, C.c_int, C.POINTER(C.c_int32), C.c_char_p, C.c_int, C.POINTER(C.c_int32),
+                                C.POINTER(C.c_int32)]),
+    "lrm_tok_encode": (C.c_int, [P, P, C.c_uint64, P, C.c_uint64, U64P]),
+    "lrm_tok_encode_bytes": (C.c_int, [P, P, C.c_uint64, P, C.c_uint64, U64P]),
+    "lrm_tok_decode_bytes": (C.c_int, [P, P, C.c_uint64, P, C.c_uint64, U64P]),
+    "lrm_tok_id_of": (C.c_int, [P, P, C.c_uint64, C.POINTER(C.c_int32)]),
+    "lrm_tok_token_of": (C.c_int, [P, C.c_int32, C.c_char_p, C.c_int, C.POINTER(C.c_int32)]),
+    "lrm_tok_pre_split": (C.c_int, [P, C.c_uint64, P, C.c_uint64, U64P]),
+    "lrm_tok_nfc": (C.c_int, [P, C.c_uint64, P, C.c_uint64, U64P]),
+    "lrm_tok_nfc_many": (C.c_int, [P, P, C.c_uint64, P, C.c_uint64, P, U64P]),
+    "lrm_tok_scalar_tables": (C.c_int, [P, P, P]),
+    "lrm_tok_byte_char": (C.c_int, [C.c_int, U32P]),
     "lrm_qwen_forward": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, P, C.c_int, U32P]),
     "lrm_qwen_greedy": (C.c_int, [P, P, C.c_int, C.c_int, P]),
     "lrm_qwen_decode_set": (C.c_int, [P, P, P]),
@@ -197,6 +217,8 @@ def check(rc: int) -> None:
         raise SafetensorsFormatError(rc, msg)
     if rc == LRM_E_INTEGRITY:
         raise IntegrityError(rc, msg)
+    if rc == LRM_E_DATA:
+        raise TokenizerDataError(rc, msg)
     if rc == LRM_E_ARG:
         raise LrmError(rc, "invalid argument: " + msg)
     raise LrmError(rc, msg)

@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "liblrm_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIP_SOURCES = ["kernels_catalog.hip", "kernels_fast.hip", "kernels_persist.hip", "scratch_static.hip"]
-HOST_SOURCES = ["contract.cpp", "device.cpp", "qwen_exec.cpp", "safetensors.cpp", "capi.cpp"]
+HOST_SOURCES = ["contract.cpp", "device.cpp", "qwen_exec.cpp", "safetensors.cpp", "tokenizer.cpp", "capi.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

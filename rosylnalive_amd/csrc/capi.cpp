@@ -12,6 +12,7 @@
 #include "device.hpp"
 #include "qwen_exec.hpp"
 #include "safetensors.hpp"
+#include "tokenizer.hpp"
 
 using namespace lrm;
 
@@ -37,6 +38,12 @@ static int guard(F&& f) {
     } catch (const IntegrityError& e) {
         g_err = e.what();
         return LRM_E_INTEGRITY;
+    } catch (const tok::DataError& e) {
+        g_err = e.what();
+        return LRM_E_DATA;
+    } catch (const std::out_of_range& e) {
+        g_err = e.what();
+        return LRM_E_ARG;
     } catch (const std::invalid_argument& e) {
         g_err = e.what();
         return LRM_E_ARG;
@@ -84,6 +91,14 @@ struct lrm_qwen {
     lrm_hip_device* dev;
     lrm_qwen(lrm_hip_device* d, const QwenConfig& c, const uint32_t* inv) : q(d->d, c, inv), dev(d) {}
 };
+
+// Copies `n` items to `out` when they fit in `cap` (nothing otherwise); *count = n either way.
+template <class T>
+static void fill_out(const T* src, size_t n, T* out, uint64_t cap, uint64_t* count) {
+    need_ptr(count, "count");
+    *count = n;
+    if (out && cap >= n && n) std::memcpy(out, src, n * sizeof(T));
+}
 
 extern "C" {
 
@@ -716,6 +731,174 @@ int lrm_qwen_load_safetensors(lrm_qwen* q, const char* path) {
         need_ptr(q, "model");
         need_ptr(path, "path");
         q->q.load_safetensors(path);
+    });
+}
+
+// ---------------------------------------------------------------- tokenizer
+
+struct lrm_tok {
+    std::unique_ptr<tok::Tokenizer> t;
+};
+
+int lrm_tok_parse(const uint8_t* json, uint64_t n, lrm_tok** out) {
+    return guard([&] {
+        if (n) need_ptr(json, "json");
+        need_ptr(out, "out");
+        *out = new lrm_tok{tok::Tokenizer::parse(json, n)};
+    });
+}
+
+int lrm_tok_destroy(lrm_tok* t) {
+    return guard([&] { delete t; });
+}
+
+int lrm_tok_info(const lrm_tok* t, int32_t* vocab_size, int32_t* merges, int32_t* added) {
+    return guard([&] {
+        need_ptr(t, "tokenizer");
+        if (vocab_size) *vocab_size = t->t->vocab_size();
+        if (merges) *merges = t->t->merge_count();
+        if (added) *added = int32_t(t->t->added().size());
+    });
+}
+
+int lrm_tok_added(const lrm_tok* t, int i, int32_t* id, char* content, int cap, int32_t* len, int32_t* special) {
+    return guard([&] {
+        need_ptr(t, "tokenizer");
+        const auto& a = t->t->added();
+        if (i < 0 || size_t(i) >= a.size()) throw std::invalid_argument("added token " + std::to_string(i));
+        if (id) *id = a[size_t(i)].id;
+        if (special) *special = a[size_t(i)].special ? 1 : 0;
+        copy_bytes(content, cap, len, tok::utf8_encode(a[size_t(i)].content));
+    });
+}
+
+int lrm_tok_encode(const lrm_tok* t, const uint8_t* utf8, uint64_t n, int32_t* ids, uint64_t cap, uint64_t* count) {
+    return guard([&] {
+        need_ptr(t, "tokenizer");
+        if (n) need_ptr(utf8, "text");
+        const std::vector<int32_t> v = t->t->encode(utf8, n);
+        fill_out(v.data(), v.size(), ids, cap, count);
+    });
+}
+
+int lrm_tok_encode_bytes(const lrm_tok* t, const uint8_t* bytes, uint64_t n, int32_t* ids, uint64_t cap,
+                         uint64_t* count) {
+    return guard([&] {
+        need_ptr(t, "tokenizer");
+        if (n) need_ptr(bytes, "bytes");
+        const std::vector<int32_t> v = t->t->encode_bytes(bytes, n);
+        fill_out(v.data(), v.size(), ids, cap, count);
+    });
+}
+
+int lrm_tok_decode_bytes(const lrm_tok* t, const int32_t* ids, uint64_t n, uint8_t* out, uint64_t cap,
+                         uint64_t* len) {
+    return guard([&] {
+        need_ptr(t, "tokenizer");
+        if (n) need_ptr(ids, "ids");
+        const std::string b = t->t->decode_bytes(ids, n);
+        fill_out(reinterpret_cast<const uint8_t*>(b.data()), b.size(), out, cap, len);
+    });
+}
+
+int lrm_tok_id_of(const lrm_tok* t, const uint8_t* token, uint64_t n, int32_t* id) {
+    return guard([&] {
+        need_ptr(t, "tokenizer");
+        need_ptr(id, "id");
+        *id = t->t->id_of(std::string(reinterpret_cast<const char*>(token), n));
+    });
+}
+
+int lrm_tok_token_of(const lrm_tok* t, int32_t id, char* out, int cap, int32_t* len) {
+    return guard([&] {
+        need_ptr(t, "tokenizer");
+        need_ptr(len, "len");
+        std::string s;
+        if (!t->t->token_of(id, s)) {
+            *len = -1;
+            return;
+        }
+        copy_bytes(out, cap, len, s);
+    });
+}
+
+int lrm_tok_pre_split(const uint8_t* utf8, uint64_t n, uint64_t* bounds, uint64_t cap, uint64_t* count) {
+    return guard([&] {
+        if (n) need_ptr(utf8, "text");
+        std::u32string s;
+        size_t bad = 0;
+        if (!tok::utf8_decode(utf8, n, s, &bad)) throw std::invalid_argument("not valid UTF-8 at byte " + std::to_string(bad));
+        const std::vector<size_t> b = tok::pre_split(s);
+        // scalar boundaries -> byte offsets
+        std::vector<uint64_t> off;
+        off.reserve(b.size());
+        uint64_t at = 0;
+        size_t k = 0;
+        for (size_t i = 0; i <= s.size(); ++i) {
+            while (k < b.size() && b[k] == i) {
+                off.push_back(at);
+                ++k;
+            }
+            if (i < s.size()) {
+                const uint32_t c = uint32_t(s[i]);
+                at += c < 0x80 ? 1 : c < 0x800 ? 2 : c < 0x10000 ? 3 : 4;
+            }
+        }
+        fill_out(off.data(), off.size(), bounds, cap, count);
+    });
+}
+
+int lrm_tok_nfc(const uint8_t* utf8, uint64_t n, uint8_t* out, uint64_t cap, uint64_t* len) {
+    return guard([&] {
+        if (n) need_ptr(utf8, "text");
+        std::u32string s;
+        size_t bad = 0;
+        if (!tok::utf8_decode(utf8, n, s, &bad)) throw std::invalid_argument("not valid UTF-8 at byte " + std::to_string(bad));
+        const std::string r = tok::utf8_encode(tok::nfc(s));
+        fill_out(reinterpret_cast<const uint8_t*>(r.data()), r.size(), out, cap, len);
+    });
+}
+
+int lrm_tok_nfc_many(const uint8_t* text, const uint64_t* offsets, uint64_t count, uint8_t* out, uint64_t cap,
+                     uint64_t* out_offsets, uint64_t* len) {
+    return guard([&] {
+        need_ptr(offsets, "offsets");
+        need_ptr(len, "len");
+        std::string all;
+        std::vector<uint64_t> offs{0};
+        for (uint64_t i = 0; i < count; ++i) {
+            const uint64_t b = offsets[i], e = offsets[i + 1];
+            if (e < b) throw std::invalid_argument("offsets decrease at " + std::to_string(i));
+            std::u32string s;
+            size_t bad = 0;
+            if (!tok::utf8_decode(text + b, size_t(e - b), s, &bad))
+                throw std::invalid_argument("string " + std::to_string(i) + " is not valid UTF-8");
+            all += tok::utf8_encode(tok::nfc(s));
+            offs.push_back(all.size());
+        }
+        *len = all.size();
+        if (out && cap >= all.size()) {
+            if (!all.empty()) std::memcpy(out, all.data(), all.size());
+            if (out_offsets) std::memcpy(out_offsets, offs.data(), offs.size() * sizeof(uint64_t));
+        }
+    });
+}
+
+int lrm_tok_scalar_tables(uint8_t* classes, uint8_t* contraction, uint8_t* nfc_split) {
+    return guard([&] {
+        for (uint32_t c = 0; c < 0x110000; ++c) {
+            if (classes) classes[c] = uint8_t(tok::char_class(c));
+            if (contraction) contraction[c] = uint8_t(tok::contraction_letter(c));
+            if (nfc_split) nfc_split[c] = tok::nfc_split_point(c) ? 1 : 0;
+        }
+    });
+}
+
+int lrm_tok_byte_char(int b, uint32_t* c) {
+    return guard([&] {
+        need_ptr(c, "c");
+        if (b < 0 || b > 255) throw std::invalid_argument("byte " + std::to_string(b));
+        *c = tok::byte_char(uint8_t(b));
     });
 }
 
