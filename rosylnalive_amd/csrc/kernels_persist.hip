@@ -741,7 +741,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         for (int r = 0; r < 4; ++r) {
             const uint16_t* er = a.embed + size_t(min(row + r, V - 1)) * kH + 8 * lane;
 #pragma unroll
-            for (int c = 0; c < kNCH; ++c) dst[r][c] = ld16(er + 512 * c);
+            for (int c = 0; c < kNCH; ++c) dst[r][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(er + 512 * c));
         }
     };
     // wave w visits rows r0 + 4 w + 32 j, four at a time, through three register sets (the next two sets in flight
