@@ -8,7 +8,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liblrm_hip.so")
+# LRM_HIP_LIB selects another build of the library (the stage-timing variant of rosylnalive_amd/persist_stages.py)
+LIB_PATH = os.environ.get("LRM_HIP_LIB") or os.path.join(HERE, "liblrm_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "lrm_hip.h")
 
 LRM_OK, LRM_E_CONTRACT, LRM_E_HIP, LRM_E_ARG, LRM_E_INTERNAL, LRM_E_RANGE = 0, 1, 2, 3, 4, 5

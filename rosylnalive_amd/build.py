@@ -53,26 +53,35 @@ def _run(cmd):
     return r.stderr
 
 
-def build(verbose: bool = False) -> str:
+# The stage-timing variant of the library (the persistent decode step records constant-clock stamps at its stage
+# boundaries; rosylnalive_amd/persist_stages.py reads them): same sources, built apart with LRM_PERSIST_STAMPS.
+STAMPS_DIR = os.path.join(HERE, "stamps")
+STAMPS_LIB = os.path.join(STAMPS_DIR, "liblrm_hip.so")
+
+
+def build(verbose: bool = False, stamps: bool = False) -> str:
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
     cxx = shutil.which("g++") or "g++"
-    os.makedirs(BUILD, exist_ok=True)
+    build_dir = os.path.join(STAMPS_DIR, "_build") if stamps else BUILD
+    lib_path = STAMPS_LIB if stamps else LIB
+    extra = ["-DLRM_PERSIST_STAMPS"] if stamps else []
+    os.makedirs(build_dir, exist_ok=True)
     jobs = []
     for s in HIP_SOURCES:
-        jobs.append([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, s), "-o", os.path.join(BUILD, s + ".o")])
+        jobs.append([hipcc, *HIPCC_FLAGS, *extra, "-c", os.path.join(CSRC, s), "-o", os.path.join(build_dir, s + ".o")])
     for s in HOST_SOURCES:
-        jobs.append([cxx, *CXX_FLAGS, "-c", os.path.join(CSRC, s), "-o", os.path.join(BUILD, s + ".o")])
+        jobs.append([cxx, *CXX_FLAGS, *extra, "-c", os.path.join(CSRC, s), "-o", os.path.join(build_dir, s + ".o")])
     with ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
         for err in ex.map(_run, jobs):
             if verbose and err.strip():
                 print(err, file=sys.stderr)
-    objs = [os.path.join(BUILD, s + ".o") for s in HIP_SOURCES + HOST_SOURCES]
-    tmp = LIB + ".tmp"
+    objs = [os.path.join(build_dir, s + ".o") for s in HIP_SOURCES + HOST_SOURCES]
+    tmp = lib_path + ".tmp"
     _run([cxx, "-shared", "-o", tmp, *objs, "-L" + os.path.join(ROCM, "lib"), "-Wl,-rpath," + os.path.join(ROCM, "lib"),
           "-lamdhip64", "-fopenmp", "-lquadmath"])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib_path)
+    return lib_path
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, stamps="--stamps" in sys.argv[1:]))

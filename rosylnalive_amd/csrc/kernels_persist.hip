@@ -353,6 +353,25 @@ __device__ __forceinline__ void rows_dot(const u32x4 (&wr)[NC], const float* vec
     }
 }
 
+// Stage stamps of the timing build (persist.hpp, LRM_PERSIST_STAMPS); nothing in the shipped build.
+#if defined(LRM_PERSIST_STAMPS)
+#define PSTAMP(k)                                                                                    \
+    do {                                                                                             \
+        if (t == 0 && (l == kStampLayer || l == kStampLayer + 1)) stamps[(k) + 16 * (l - kStampLayer)] = wall_clock64(); \
+    } while (0)
+#define PSTAMP_AT(k)                            \
+    do {                                        \
+        if (t == 0) stamps[k] = wall_clock64(); \
+    } while (0)
+#else
+#define PSTAMP(k) \
+    do {          \
+    } while (0)
+#define PSTAMP_AT(k) \
+    do {             \
+    } while (0)
+#endif
+
 __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     __shared__ __align__(16) float vec[kVecMax];
     __shared__ __align__(16) float xres[kH];  // the residual stream: every workgroup holds all of it, the same bits
@@ -382,6 +401,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     const XLayout X(kQH, kKVH, kH, kI, kG);
     uint64_t* const lmp = a.xch + kHdrEntries + size_t(a.layers) * X.per_layer64;  // lm_head partials
     uint32_t* const x32 = reinterpret_cast<uint32_t*>(lmp + (2 * kG + 511) / 512 * 512);  // the 4-byte area
+#if defined(LRM_PERSIST_STAMPS)
+    uint64_t* const stamps = reinterpret_cast<uint64_t*>(x32 + size_t(a.layers) * X.per_layer32) + size_t(b) * kStampWords;
+#endif
+    PSTAMP_AT(40);
 
     // attention split of this workgroup (stage B): fixed for the step
     const int hk = xcd, s = j;
@@ -447,10 +470,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         uint32_t* const l32 = x32 + size_t(l) * X.per_layer32;
         uint32_t* const o32 = l32 + size_t(xcd) * X.blk32;  // this XCD's 4-byte block
         // ---------------------------------------------------------------- A: q|k|v = W_qkv . RMSNorm(x)
+        PSTAMP(0);
         if (l > 0) {
             gather_sum8(l32 - X.per_layer32 + X.p2, par, xres, vec, hdr, 1, s_fail, wait_ticks);
             if (s_fail) return;
         }
+        PSTAMP(1);
         u32x4 wc[kNCC];
         {
             float xv[kNCH][8];
@@ -467,6 +492,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         // one wave stores the workgroup's rows (runs of kWaves consecutive entries), so each run is one write of whole
         // 8-byte entries from one instruction
         lds_barrier();
+        PSTAMP(2);
         if (t < kRA * kWaves) lstore(q64 + X.qkv + j * kWaves + (t % kWaves) + (t / kWaves) * kJN * kWaves, red[t], tag);
         // stage C's o_proj weights (rows 32 j + 4 w + q, the XCD's 256 columns), issued after the rows above have
         // left: a load issue that waits for room in the memory queue would otherwise hold them back
@@ -486,6 +512,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             const uint64_t* src = q64 + X.qkv;  // the XCD's query heads, then its key and value
             gather<1>([&](int i) { return src + i; }, has_pos ? 512 : 256, tag, vec, hdr, 2, s_fail, wait_ticks);
             if (s_fail) return;
+            PSTAMP(3);
             // per-head RMSNorm (q heads: threads 0-255, the new key: 256-383), then the rotation of (d, d + 64): each
             // thread normalises its partner element d ^ 64 too (the same expression as the partner's own thread, so the
             // same bits) instead of exchanging it through LDS; the split holding pos appends the rotated key and the
@@ -621,6 +648,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 red[2 * w + 1] = l_run;
             }
             lds_barrier();
+            PSTAMP(4);
             if (w < 2) {
                 uint32_t* pr = o32 + X.part + size_t(w * S + s) * kPartStride;
 #pragma unroll
@@ -634,6 +662,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         }
 
         // ---------------------------------------------------------------- C: p1[xcd] = W_o[:, the XCD's columns] . o
+        PSTAMP(5);
         // o of the XCD's two query heads, formed by every workgroup from the splits' partial rows (row r = hh S_used
         // + sp of the gathered rows at vec[132 r ..]): the split weights 2^(m_sp - M), summed in split order
         lds_barrier();  // vec may still be read by stage B's waves
@@ -665,6 +694,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             ps[w][lane] = e / L;
         }
         lds_barrier();
+        PSTAMP(6);
         if (t < kCW) {
             const int hh = t >> 7, d = t & 127;
             const float* rows = vec + hh * S_used * 4 * kPartVecs + d;
@@ -675,6 +705,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         lds_barrier();
         rows_dot<kNCC, kCW / 8>(wc, &qs[0][0], red);
         lds_barrier();
+        PSTAMP(8);
         if (t < kRowsG) gstore32(l32 + X.p1 + xcd * kH + j * kRowsG + t, red[t], par);
         // stage D's gate/up weights, after the rows above: unit u = w kUD + jj is (row u / kNCH of the workgroup's
         // 2 kPB, chunk jj % kNCH); rows 0 .. kPB - 1 are gate rows 384 xcd + 12 j + r, the rest the matching up rows
@@ -691,6 +722,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         // ---------------------------------------------------------------- D: a = silu(W_g . h) * (W_u . h)
         gather_sum8(l32 + X.p1, par, xres, vec, hdr, 5, s_fail, wait_ticks);
         if (s_fail) return;
+        PSTAMP(9);
         // stage E's down_proj weights (rows 32 j + 4 w + q, the XCD's 384 columns), before this stage computes:
         // issued after its outputs they land only after the hand-off to stage E
         u32x4 we[kNCE];
@@ -711,6 +743,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             }
         }
         lds_barrier();
+        PSTAMP(10);
         if (t < kPB) {
             float g = 0.f, u = 0.f;
 #pragma unroll
@@ -724,8 +757,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         // ---------------------------------------------------------------- E: p2[xcd] = W_d[:, the XCD's columns] . a
         gather32x4<1>(o32 + X.a, kEW * 4, [](int v) { return 16 * v; }, kEW / 4, par, vec, hdr, 6, s_fail, wait_ticks);
         if (s_fail) return;
+        PSTAMP(11);
         rows_dot<kNCE, kEW / 8>(we, vec, red);
         lds_barrier();
+        PSTAMP(12);
         if (t < kRowsG) gstore32(l32 + X.p2 + xcd * kH + j * kRowsG + t, red[t], par);
         // the next layer's q|k|v rows and K/V chunks, after the rows above (after the last layer: its q|k|v rows
         // again, never used; unconditional, so the compiler's wait counting has one path to follow)
@@ -733,6 +768,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         if (l + 1 < a.layers) prefetch_kv(l + 1);
     }
 
+    PSTAMP_AT(41);
     // ---------------------------------------------------------------- lm_head over rows [r0, r1), then the argmax
     const int V = a.vocab, per = (V + kG - 1) / kG, r0 = b * per, r1 = min(V, r0 + per);
     u32x4 ra[4][kNCH], rb4[4][kNCH], rc4[4][kNCH], nf[kNCH];
@@ -753,6 +789,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     for (int c = 0; c < kNCH; ++c) nf[c] = ld16(a.final_norm + 512 * c + 8 * lane);
     gather_sum8(x32 + size_t(a.layers - 1) * X.per_layer32 + X.p2, par, xres, vec, hdr, 7, s_fail, wait_ticks);
     if (s_fail) return;
+    PSTAMP_AT(42);
     float xv[kNCH][8];
     norm_lane<kNCH>(xres, nf, a.eps, xv);
     float best = -INFINITY;
@@ -803,6 +840,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         gstore(lmp + 2 * b, bv, tag);
         gstore(lmp + 2 * b + 1, __uint_as_float(bn ? 0xFFFFFFFEu : ix), tag);
     }
+    PSTAMP_AT(43);
     if (b != 0) return;
 
     // workgroup 0: the lowest index of the maximum over the workgroups' pairs (0xFFFFFFFF when a logit is NaN)
@@ -847,6 +885,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         a.state[0] = pos + 1u;
         a.state[2] = step + 1u;
         __hip_atomic_store(hdr, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // the next launch's epoch
+#if defined(LRM_PERSIST_STAMPS)
+        stamps[44] = wall_clock64();
+#endif
     }
 }
 

@@ -59,10 +59,21 @@ inline uint64_t exchange_entries64(int layers, const Shape& s) {
     return uint64_t(kHdrEntries) + uint64_t(layers) * uint64_t(X.per_layer64) + (2ull * s.blocks + 511) / 512 * 512;
 }
 
+// The stage-timing build (compiled with LRM_PERSIST_STAMPS): per workgroup 64 constant-clock stamps after the
+// exchange entries. Stamps k < 16 and 16 + k: stage boundary k of layers kStampLayer and kStampLayer + 1; 40 the
+// launch start, 41 the end of the layers, 42 the lm_head's x gathered, 43 the lm_head done, 44 (workgroup 0) the step's
+// end.
+constexpr int kStampLayer = 14, kStampWords = 64;
+#if defined(LRM_PERSIST_STAMPS)
+constexpr uint64_t kStampEntries = 256ull * kStampWords;
+#else
+constexpr uint64_t kStampEntries = 0;
+#endif
+
 // The whole exchange buffer in 8-byte units.
 inline uint64_t exchange_entries(int layers, const Shape& s) {
     const XLayout X(s.heads, s.kv_heads, s.hidden, s.inter, s.blocks);
-    return exchange_entries64(layers, s) + (uint64_t(layers) * uint64_t(X.per_layer32) + 1) / 2;
+    return exchange_entries64(layers, s) + (uint64_t(layers) * uint64_t(X.per_layer32) + 1) / 2 + kStampEntries;
 }
 
 // nullptr when the instantiated kernel covers the shape, else the reason it does not. The kernel is written for the
