@@ -158,21 +158,23 @@ __device__ __forceinline__ bool wait_over(int it, long long& start, long long li
 // dst[i] in LDS. Thread t polls entries t, t + 512, ..., re-reading only those not yet ready, back to back. When the
 // step is aborted (this wait timed out or another workgroup aborted) it sets `fail` (the workgroup's LDS flag), which
 // the caller reads after the barrier that ends the wait. `fail` must stay an LDS access: a generic (flat) read would
-// also wait for every global load in flight, the prefetched weights included.
+// also wait for every global load in flight, the prefetched weights included. Returns the number of passes this thread
+// made (the stage-timing build records it).
 template <int E, typename F>
-__device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, uint32_t* hdr, int stage, int& fail,
-                                       long long limit) {
+__device__ __forceinline__ int gather(F idx, int n, uint32_t tag, float* dst, uint32_t* hdr, int stage, int& fail,
+                                      long long limit) {
     const int t = threadIdx.x;
     if (n <= 0) {
         lds_barrier();
-        return;
+        return 0;
     }
     uint64_t v[E];
     bool pend[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) pend[e] = t + e * kThreads < n;
     long long start = 0;
-    for (int it = 0;; ++it) {
+    int it = 0;
+    for (;; ++it) {
 #pragma unroll
         for (int e = 0; e < E; ++e)
             if (pend[e]) v[e] = __hip_atomic_load(idx(t + e * kThreads), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -191,13 +193,14 @@ __device__ __forceinline__ void gather(F idx, int n, uint32_t tag, float* dst, u
     // Nothing is in flight now (every poll waited for all older loads and stores); saying so lets the compiler's
     // wait counting start from zero after the loop instead of waiting for loads issued later.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    return it + 1;
 }
 
 // Block-wide: waits until the 4-byte entries of the 16-byte vectors at byte offsets voff(v) from base, v < nv
 // (nv <= E * 512, every offset below `bytes`), carry `parity` and writes vector v to dst[4 v .. 4 v + 3] (LDS, 16-byte
 // aligned). 16-byte device-scope loads, four entries each; otherwise as gather.
 template <int E, typename F>
-__device__ __forceinline__ void gather32x4(const uint32_t* base, int bytes, F voff, int nv, uint32_t parity,
+__device__ __forceinline__ int gather32x4(const uint32_t* base, int bytes, F voff, int nv, uint32_t parity,
                                            float* dst, uint32_t* hdr, int stage, int& fail, long long limit) {
     const int t = threadIdx.x;
     const __amdgpu_buffer_rsrc_t rs =
@@ -212,7 +215,8 @@ __device__ __forceinline__ void gather32x4(const uint32_t* base, int bytes, F vo
         off[e] = pend[e] ? voff(t + e * kThreads) : 0;
     }
     long long start = 0;
-    for (int it = 0;; ++it) {
+    int it = 0;
+    for (;; ++it) {
         asm volatile("" ::: "memory");  // every pass loads again
 #pragma unroll
         for (int e = 0; e < E; ++e)
@@ -232,13 +236,14 @@ __device__ __forceinline__ void gather32x4(const uint32_t* base, int bytes, F vo
         if (t + e * kThreads < nv) *reinterpret_cast<u32x4*>(dst + 4 * (t + e * kThreads)) = v[e];
     lds_barrier();
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), as in gather
+    return it + 1;
 }
 
 // Block-wide: waits for the per-XCD partial sums [kXcds][kH] at base (4-byte parity entries) and adds them to the
 // residual stream xres: thread t polls rows 4 (t % 256) .. + 3 of XCDs 4 (t / 256) .. + 3 and sums them in XCD order in
 // registers; the upper half's sums go through LDS (sc) to the lower half, which adds lower + upper to x. The same
 // order in every workgroup, so the same bits. As gather otherwise.
-__device__ __forceinline__ void gather_sum8(const uint32_t* base, uint32_t parity, float* xres, float* sc,
+__device__ __forceinline__ int gather_sum8(const uint32_t* base, uint32_t parity, float* xres, float* sc,
                                             uint32_t* hdr, int stage, int& fail, long long limit) {
     const int t = threadIdx.x, r4 = t & (kH / 4 - 1), x0 = (t / (kH / 4)) * 4;
     static_assert(kThreads == 2 * (kH / 4) && kXcds == 8, "two threads per 4 rows, four XCDs each");
@@ -250,7 +255,8 @@ __device__ __forceinline__ void gather_sum8(const uint32_t* base, uint32_t parit
 #pragma unroll
     for (int x = 0; x < 4; ++x) pend[x] = true;
     long long start = 0;
-    for (int it = 0;; ++it) {
+    int it = 0;
+    for (;; ++it) {
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int x = 0; x < 4; ++x)
@@ -283,6 +289,7 @@ __device__ __forceinline__ void gather_sum8(const uint32_t* base, uint32_t parit
     }
     lds_barrier();
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), as in gather
+    return it + 1;
 }
 
 // This lane's values k = 512 c + 8 lane + e of RMSNorm(vec) (vec in LDS, 512 NCH wide): every wave reads the whole
@@ -363,12 +370,21 @@ __device__ __forceinline__ void rows_dot(const u32x4 (&wr)[NC], const float* vec
     do {                                        \
         if (t == 0) stamps[k] = wall_clock64(); \
     } while (0)
+#define PITER(k, n)                                                     \
+    do {                                                                \
+        const int n_ = (n);                                             \
+        if (t == 0 && l == kStampLayer) stamps[32 + (k)] = uint64_t(n_); \
+    } while (0)
 #else
 #define PSTAMP(k) \
     do {          \
     } while (0)
 #define PSTAMP_AT(k) \
     do {             \
+    } while (0)
+#define PITER(k, n) \
+    do {            \
+        (void)(n);  \
     } while (0)
 #endif
 
@@ -440,8 +456,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     lds_barrier();
 
     // This split's first 64-key chunks of K and V^T (one when the split holds one, else two): they do not depend on
-    // this step, so the chunks of layer l + 1 load at the end of layer l (layer 0's here), away from stage A, where
-    // loads in flight would hold back this workgroup's q|k|v rows. K: thread t holds key slots t / 16 and t / 16 + 32
+    // this step, so layer l + 1's load during layer l (layer 0's here): the first after stage C's wait, the second at
+    // the end of the layer, so neither wait for x holds back much behind them. K: thread t holds key slots t / 16 and t / 16 + 32
     // of a chunk, dims 8 (t % 16) .. + 7; V^T: dim t / 4, keys 16 (t % 4) .. + 15. Past the last chunk: re-read it
     // (never used).
     u32x4 kr[2][2], vr[2][2];
@@ -457,13 +473,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
-    auto prefetch_kv = [&](int l) __attribute__((always_inline)) {
-        if (attn) {
-            fetch(C0{}, l, 0);
-            if (nch > 1) fetch(C1{}, l, 1);
-        }
-    };
-    prefetch_kv(0);
+    if (attn) {
+        fetch(C0{}, 0, 0);
+        if (nch > 1) fetch(C1{}, 0, 1);
+    }
 
     for (int l = 0; l < a.layers; ++l) {
         uint64_t* const q64 = a.xch + kHdrEntries + size_t(l) * X.per_layer64 + size_t(xcd) * X.blk64;  // XCD block
@@ -472,7 +485,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         // ---------------------------------------------------------------- A: q|k|v = W_qkv . RMSNorm(x)
         PSTAMP(0);
         if (l > 0) {
-            gather_sum8(l32 - X.per_layer32 + X.p2, par, xres, vec, hdr, 1, s_fail, wait_ticks);
+            PITER(0, gather_sum8(l32 - X.per_layer32 + X.p2, par, xres, vec, hdr, 1, s_fail, wait_ticks));
             if (s_fail) return;
         }
         PSTAMP(1);
@@ -510,7 +523,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             const float nwt = bf2f(t < 256 ? a.q_norm[l * 128 + d] : a.k_norm[l * 128 + d]);
             const float nwp = bf2f(t < 256 ? a.q_norm[l * 128 + (d ^ 64)] : a.k_norm[l * 128 + (d ^ 64)]);
             const uint64_t* src = q64 + X.qkv;  // the XCD's query heads, then its key and value
-            gather<1>([&](int i) { return src + i; }, has_pos ? 512 : 256, tag, vec, hdr, 2, s_fail, wait_ticks);
+            PITER(1, gather<1>([&](int i) { return src + i; }, has_pos ? 512 : 256, tag, vec, hdr, 2, s_fail, wait_ticks));
             if (s_fail) return;
             PSTAMP(3);
             // per-head RMSNorm (q heads: threads 0-255, the new key: 256-383), then the rotation of (d, d + 64): each
@@ -674,16 +687,19 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 return ((hh * S + sp) * kPartStride + 4 * c) * 4;
             };
             const int nv = 2 * S_used * kPartVecs;
-            gather32x4<3>(o32 + X.part, 2 * S * kPartStride * 4, voff, min(nv, kV1), par, vec, hdr, 4, s_fail,
-                          wait_ticks);
+            PITER(2, gather32x4<3>(o32 + X.part, 2 * S * kPartStride * 4, voff, min(nv, kV1), par, vec, hdr, 4, s_fail,
+                                   wait_ticks));
             if (s_fail) return;
             if (nv > kV1) {
                 static_assert(2 * kJN * kPartVecs <= kV1 + 2 * kThreads, "the partial rows in two passes");
-                gather32x4<2>(o32 + X.part, 2 * S * kPartStride * 4, [&](int v) { return voff(v + kV1); }, nv - kV1,
-                              par, vec + 4 * kV1, hdr, 4, s_fail, wait_ticks);
+                PITER(3, gather32x4<2>(o32 + X.part, 2 * S * kPartStride * 4, [&](int v) { return voff(v + kV1); },
+                                       nv - kV1, par, vec + 4 * kV1, hdr, 4, s_fail, wait_ticks));
                 if (s_fail) return;
             }
         }
+        // the next layer's first K/V chunk (its registers are free once this layer's attention is done): in flight
+        // through this stage's compute and the wait for the o_proj sums, away from the next layer's first wait
+        if (attn) fetch(C0{}, min(l + 1, a.layers - 1), 0);
         if (w < 2) {  // wave hh: the split weights 2^(m_sp - M) / sum_sp 2^(m_sp - M) l_sp of query head hh, a split per lane
             const bool ok = lane < S_used;
             const float* r = vec + (w * S_used + (ok ? lane : 0)) * 4 * kPartVecs;
@@ -720,7 +736,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         for (int c = 0; c < kNCH; ++c) nd[c] = ld16(a.post_norm + size_t(l) * kH + 512 * c + 8 * lane);
 
         // ---------------------------------------------------------------- D: a = silu(W_g . h) * (W_u . h)
-        gather_sum8(l32 + X.p1, par, xres, vec, hdr, 5, s_fail, wait_ticks);
+        PITER(4, gather_sum8(l32 + X.p1, par, xres, vec, hdr, 5, s_fail, wait_ticks));
         if (s_fail) return;
         PSTAMP(9);
         // stage E's down_proj weights (rows 32 j + 4 w + q, the XCD's 384 columns), before this stage computes:
@@ -755,17 +771,18 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         }
 
         // ---------------------------------------------------------------- E: p2[xcd] = W_d[:, the XCD's columns] . a
-        gather32x4<1>(o32 + X.a, kEW * 4, [](int v) { return 16 * v; }, kEW / 4, par, vec, hdr, 6, s_fail, wait_ticks);
+        PITER(5, gather32x4<1>(o32 + X.a, kEW * 4, [](int v) { return 16 * v; }, kEW / 4, par, vec, hdr, 6, s_fail,
+                               wait_ticks));
         if (s_fail) return;
         PSTAMP(11);
         rows_dot<kNCE, kEW / 8>(we, vec, red);
         lds_barrier();
         PSTAMP(12);
         if (t < kRowsG) gstore32(l32 + X.p2 + xcd * kH + j * kRowsG + t, red[t], par);
-        // the next layer's q|k|v rows and K/V chunks, after the rows above (after the last layer: its q|k|v rows
+        // the next layer's q|k|v rows and second K/V chunk, after the rows above (after the last layer: its q|k|v rows
         // again, never used; unconditional, so the compiler's wait counting has one path to follow)
         issue_a(min(l + 1, a.layers - 1));
-        if (l + 1 < a.layers) prefetch_kv(l + 1);
+        if (l + 1 < a.layers && attn && nch > 1) fetch(C1{}, l + 1, 1);
     }
 
     PSTAMP_AT(41);

@@ -28,6 +28,12 @@ STAGES = [  # name, first stamp, last stamp, attention workgroups only
     ("E compute", 11, 12, False)]
 
 
+def S_used(pos):
+    """Attention splits holding keys at position pos (32 splits of a whole number of 64-key chunks)."""
+    kps = ((pos + 1 + 31) // 32 + 63) // 64 * 64
+    return (pos + 1 + kps - 1) // kps
+
+
 def main(argv):
     contexts = [int(c) for c in (argv[0] if argv else "392,4000").split(",")]
     if not os.path.exists(STAMPS_LIB):
@@ -74,7 +80,14 @@ def main(argv):
             sel = attn if only_attn else slice(None)
             d = us(L[sel, k1] - L[sel, k0])
             print(f"  {name:28s} {np.median(d):7.2f} {d.max():7.2f} {d.min():7.2f} {us(L[sel, k1].max() - lay0):12.2f}")
-        print(f"  layer (first start to last end) {us(L[:, 12].max() - lay0):.2f} us", flush=True)
+        print(f"  layer (first start to last end) {us(L[:, 12].max() - lay0):.2f} us")
+        P = st[:, 32:38]
+        passes = [("A", P[:, 0]), ("B", P[attn, 1]), ("C", P[:, 2])]
+        if 2 * S_used(ctx + 8) * 33 > 3 * 512:  # the partial rows took a second gather
+            passes.append(("C, second part", P[:, 3]))
+        passes += [("D", P[:, 4]), ("E", P[:, 5])]
+        print("  poll passes of thread 0 (median / max): " +
+              "; ".join(f"{n} {np.median(v):.0f} / {v.max()}" for n, v in passes), flush=True)
     m.close()
     b.close()
 
