@@ -360,20 +360,31 @@ __device__ __forceinline__ void rows_dot(const u32x4 (&wr)[NC], const float* vec
     }
 }
 
-// Stage stamps of the timing build (persist.hpp, LRM_PERSIST_STAMPS); nothing in the shipped build.
+// Stage stamps of the timing build (persist.hpp, LRM_PERSIST_STAMPS); nothing in the shipped build. Thread 0 keeps
+// them in LDS (st_lds) and copies them to memory when the workgroup is done, so no store of theirs is in flight while
+// the step runs (a wait for the loads in flight would also wait for it).
 #if defined(LRM_PERSIST_STAMPS)
-#define PSTAMP(k)                                                                                    \
-    do {                                                                                             \
-        if (t == 0 && (l == kStampLayer || l == kStampLayer + 1)) stamps[(k) + 16 * (l - kStampLayer)] = wall_clock64(); \
+#define PSTAMP(k)                                                                                      \
+    do {                                                                                               \
+        if (t == 0 && (l == kStampLayer || l == kStampLayer + 1)) st_lds[(k) + 16 * (l - kStampLayer)] = wall_clock64(); \
     } while (0)
 #define PSTAMP_AT(k)                            \
     do {                                        \
-        if (t == 0) stamps[k] = wall_clock64(); \
+        if (t == 0) st_lds[k] = wall_clock64(); \
     } while (0)
-#define PITER(k, n)                                                     \
-    do {                                                                \
-        const int n_ = (n);                                             \
-        if (t == 0 && l == kStampLayer) stamps[32 + (k)] = uint64_t(n_); \
+#define PITER(k, n)                                                      \
+    do {                                                                 \
+        const int n_ = (n);                                              \
+        if (t == 0 && l == kStampLayer) st_lds[32 + (k)] = uint64_t(n_); \
+    } while (0)
+#define PSUB(k)                                                           \
+    do {                                                                  \
+        if (t == 0 && l == kStampLayer) st_lds[48 + (k)] = wall_clock64(); \
+    } while (0)
+#define PFLUSH()                                                           \
+    do {                                                                   \
+        if (t == 0)                                                        \
+            for (int k_ = 0; k_ < kStampWords; ++k_) stamps[k_] = st_lds[k_]; \
     } while (0)
 #else
 #define PSTAMP(k) \
@@ -385,6 +396,12 @@ __device__ __forceinline__ void rows_dot(const u32x4 (&wr)[NC], const float* vec
 #define PITER(k, n) \
     do {            \
         (void)(n);  \
+    } while (0)
+#define PSUB(k) \
+    do {        \
+    } while (0)
+#define PFLUSH() \
+    do {         \
     } while (0)
 #endif
 
@@ -419,6 +436,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     uint32_t* const x32 = reinterpret_cast<uint32_t*>(lmp + (2 * kG + 511) / 512 * 512);  // the 4-byte area
 #if defined(LRM_PERSIST_STAMPS)
     uint64_t* const stamps = reinterpret_cast<uint64_t*>(x32 + size_t(a.layers) * X.per_layer32) + size_t(b) * kStampWords;
+    __shared__ uint64_t st_lds[kStampWords];
+    if (t == 0)
+        for (int k = 0; k < kStampWords; ++k) st_lds[k] = 0;
 #endif
     PSTAMP_AT(40);
 
@@ -493,6 +513,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         {
             float xv[kNCH][8];
             norm_lane<kNCH>(xres, na, a.eps, xv);
+            PSUB(0);
 #pragma unroll
             for (int r = 0; r < kRA; ++r) {
                 float acc = 0.f;
@@ -501,6 +522,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 acc = wave_sum(acc);
                 if (lane == 0) red[r * kWaves + w] = acc;
             }
+            PSUB(1);
         }
         // one wave stores the workgroup's rows (runs of kWaves consecutive entries), so each run is one write of whole
         // 8-byte entries from one instruction
@@ -535,6 +557,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             const float sq = wave_sum(val * val);
             if (lane == 0) red[w] = sq;
             lds_barrier();
+            PSUB(2);
             const float rn = 1.0f / sqrtf((red[2 * grp] + red[2 * grp + 1]) / 128.0f + a.eps);
             const float nr = nwt * (val * rn), np = nwp * (valp * rn);
             const float rot = d < 64 ? nr * cs - np * sn : nr * cs + np * sn;
@@ -556,6 +579,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 }
             }
             lds_barrier();
+            PSUB(3);
             // this thread's query dims and, for the split holding pos, its slices of the new key and value (read
             // unconditionally, used through selects)
             const int d0 = 8 * (t & 15);
@@ -634,6 +658,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             };
             using Body = std::false_type;
             using Tail = std::true_type;
+            PSUB(4);
             int c = 0;
             for (; c + 2 < nch; c += 2) {  // whole pairs before the last chunk
                 chunk(C0{}, Body{}, c);
@@ -647,6 +672,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             } else {
                 chunk(C0{}, Tail{}, c);
             }
+            PSUB(5);
             // reduce the four key groups of each dim, then the partial rows of both heads, (out[128], max, sum) and
             // two pad entries, each written whole by one wave (wave hh: the XCD's query head hh) from LDS (qs and red
             // are free after the chunks)
@@ -690,6 +716,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             PITER(2, gather32x4<3>(o32 + X.part, 2 * S * kPartStride * 4, voff, min(nv, kV1), par, vec, hdr, 4, s_fail,
                                    wait_ticks));
             if (s_fail) return;
+            PSUB(12);
             if (nv > kV1) {
                 static_assert(2 * kJN * kPartVecs <= kV1 + 2 * kThreads, "the partial rows in two passes");
                 PITER(3, gather32x4<2>(o32 + X.part, 2 * S * kPartStride * 4, [&](int v) { return voff(v + kV1); },
@@ -699,6 +726,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         }
         // the next layer's first K/V chunk (its registers are free once this layer's attention is done): in flight
         // through this stage's compute and the wait for the o_proj sums, away from the next layer's first wait
+        PSUB(13);
         if (attn) fetch(C0{}, min(l + 1, a.layers - 1), 0);
         if (w < 2) {  // wave hh: the split weights 2^(m_sp - M) / sum_sp 2^(m_sp - M) l_sp of query head hh, a split per lane
             const bool ok = lane < S_used;
@@ -719,7 +747,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             qs[hh][d] = O;
         }
         lds_barrier();
+        PSUB(6);
         rows_dot<kNCC, kCW / 8>(wc, &qs[0][0], red);
+        PSUB(7);
         lds_barrier();
         PSTAMP(8);
         if (t < kRowsG) gstore32(l32 + X.p1 + xcd * kH + j * kRowsG + t, red[t], par);
@@ -749,7 +779,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         }
         {
             float xv[kNCH][8];
+            PSUB(8);
             norm_lane<kNCH>(xres, nd, a.eps, xv);
+            PSUB(9);
 #pragma unroll
             for (int jj = 0; jj < kUD; ++jj) {
                 const int ri = (w * kUD + jj) / kNCH, c = jj % kNCH;
@@ -757,6 +789,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 acc = wave_sum(acc);
                 if (lane == 0) red[ri * kNCH + c] = acc;
             }
+            PSUB(10);
         }
         lds_barrier();
         PSTAMP(10);
@@ -776,6 +809,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         if (s_fail) return;
         PSTAMP(11);
         rows_dot<kNCE, kEW / 8>(we, vec, red);
+        PSUB(11);
         lds_barrier();
         PSTAMP(12);
         if (t < kRowsG) gstore32(l32 + X.p2 + xcd * kH + j * kRowsG + t, red[t], par);
@@ -858,7 +892,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         gstore(lmp + 2 * b + 1, __uint_as_float(bn ? 0xFFFFFFFEu : ix), tag);
     }
     PSTAMP_AT(43);
-    if (b != 0) return;
+    if (b != 0) {
+        PFLUSH();
+        return;
+    }
 
     // workgroup 0: the lowest index of the maximum over the workgroups' pairs (0xFFFFFFFF when a logit is NaN)
     gather<1>([&](int i) { return lmp + i; }, 2 * kG, tag, vec, hdr, 8, s_fail, wait_ticks);
@@ -903,9 +940,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         a.state[2] = step + 1u;
         __hip_atomic_store(hdr, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // the next launch's epoch
 #if defined(LRM_PERSIST_STAMPS)
-        stamps[44] = wall_clock64();
+        st_lds[44] = wall_clock64();
 #endif
     }
+    PFLUSH();
 }
 
 }  // namespace

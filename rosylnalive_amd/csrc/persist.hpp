@@ -62,7 +62,8 @@ inline uint64_t exchange_entries64(int layers, const Shape& s) {
 // The stage-timing build (compiled with LRM_PERSIST_STAMPS): per workgroup 64 constant-clock stamps after the
 // exchange entries. Stamps k < 16 and 16 + k: stage boundary k of layers kStampLayer and kStampLayer + 1; 40 the
 // launch start, 41 the end of the layers, 42 the lm_head's x gathered, 43 the lm_head done, 44 (workgroup 0) the step's
-// end; 32 + k: thread 0's poll passes in the waits of layer kStampLayer (k: 0 A, 1 B, 2 and 3 C's two parts, 4 D, 5 E).
+// end; 32 + k: thread 0's poll passes in the waits of layer kStampLayer (k: 0 A, 1 B, 2 and 3 C's two parts, 4 D, 5 E);
+// 48 + k: thread 0's points inside the stages of layer kStampLayer (kernels_persist.hip, PSUB).
 constexpr int kStampLayer = 14, kStampWords = 64;
 #if defined(LRM_PERSIST_STAMPS)
 constexpr uint64_t kStampEntries = 256ull * kStampWords;

@@ -26,6 +26,14 @@ STAGES = [  # name, first stamp, last stamp, attention workgroups only
     ("B attention", 3, 4, True), ("C gather (partials, local)", 5, 6, False), ("C combine + o_proj", 6, 8, False),
     ("D gather (p1, global)", 8, 9, False), ("D compute", 9, 10, False), ("E gather (a, local)", 10, 11, False),
     ("E compute", 11, 12, False)]
+SUBSTAGES = [  # name, first point, last point (L k: stage boundary k; s k: point k inside a stage), attention only
+    ("A norm", "L1", "s0", False), ("A rows", "s0", "s1", False), ("A barrier", "s1", "L2", False),
+    ("B q/k norm", "L3", "s2", True), ("B rotate+append", "s2", "s3", True), ("B q to registers", "s3", "s4", True),
+    ("B chunks", "s4", "s5", True), ("B partial rows", "s5", "L4", True),
+    ("C gather 1", "L5", "s12", False), ("C gather 2", "s12", "s13", False), ("C split weights", "s13", "L6", False),
+    ("C combine", "L6", "s6", False), ("C rows", "s6", "s7", False), ("C barrier", "s7", "L8", False),
+    ("D issue W_down", "L9", "s8", False), ("D norm", "s8", "s9", False), ("D rows", "s9", "s10", False),
+    ("D barrier", "s10", "L10", False), ("E rows", "L11", "s11", False), ("E barrier", "s11", "L12", False)]
 
 
 def S_used(pos):
@@ -87,7 +95,15 @@ def main(argv):
             passes.append(("C, second part", P[:, 3]))
         passes += [("D", P[:, 4]), ("E", P[:, 5])]
         print("  poll passes of thread 0 (median / max): " +
-              "; ".join(f"{n} {np.median(v):.0f} / {v.max()}" for n, v in passes), flush=True)
+              "; ".join(f"{n} {np.median(v):.0f} / {v.max()}" for n, v in passes))
+        Q = st[:, 48:62]
+        pts = {f"s{k}": Q[:, k] for k in range(14)}
+        pts.update({f"L{k}": L[:, k] for k in range(13)})
+        parts = []
+        for name, p0, p1, only_attn in SUBSTAGES:
+            sel = attn if only_attn else slice(None)
+            parts.append(f"{name} {np.median(us(pts[p1][sel] - pts[p0][sel])):.2f}")
+        print("  inside the stages, thread 0, median us: " + "; ".join(parts), flush=True)
     m.close()
     b.close()
 
