@@ -28,7 +28,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 FP32_PEAK_TFLOPS = 157.3
 GEMV_SWIGLU_TRAFFIC_BYTES = 12675736  # measured HBM bytes per gemv_swiglu_dec launch at the 0.6B shape
-PERSIST_TRAFFIC_BYTES = 1277567271    # measured HBM bytes per decode_step_persistent launch at context 393..424
+PERSIST_TRAFFIC_BYTES = 1278457474    # measured HBM bytes per decode_step_persistent launch at context 393..424
 ROOFLINE_POS0 = 392                   # the roofline launches run at context ROOFLINE_POS0 + 1 .. ROOFLINE_POS0 + 32
 CPU_DECODE_STEPS = 128                # the bounded CPU decode sample (about 10 s on 16 host cores)
 

@@ -101,14 +101,33 @@ def test_gemm_residual_split_and_add_norm(m, n, k, splits):
         s.close()
 
 
-def test_gemm_swiglu():
-    m, inter, k = 200, 192, 128
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 256), (300, 131100, 128)])
+def test_gemm_f32_large_grids(m, n, k):
+    """gemm_f32 over grids of whole rounds of blocks (2048 x 4096: 512 tiles, the direct-to-LDS loop) and of tiles
+    partial in both m and n (131,100 columns: 1025 column tiles, the lm_head's shape class), against float64."""
+    r = np.random.default_rng(m + n + k)
+    a = f16(r.standard_normal((m, k)))
+    w = f16(r.standard_normal((n, k)) * 0.05)
+    s = Session({"a": (F16, (m, k), 0, a), "w": (F16, (n, k), RO, w), "y": (F32, (m, n), 0, None)})
+    try:
+        y = s.run("gemm_f32", ["y"], a="a", w="w", y="y", m=m, n=n, k=k)["y"]
+        assert written_everywhere(y)
+        ref = hwiden(a).astype(np.float64) @ hwiden(w).astype(np.float64).T
+        assert metrics.rel_l2(y, ref) < 1e-6, metrics.rel_l2(y, ref)
+    finally:
+        s.close()
+
+
+@pytest.mark.parametrize("m,inter,k", [(200, 192, 128), (2048, 4096, 128)])
+def test_gemm_swiglu(m, inter, k):
+    """SwiGLU epilogue: partial tiles (200 rows) and a 1024-tile grid (2048 rows, 4096 pairs)."""
     r = np.random.default_rng(3)
     a = f16(r.standard_normal((m, k)))
     w = f16(r.standard_normal((2 * inter, k)) * 0.1)
     s = Session({"a": (F16, (m, k), 0, a), "w": (F16, (2 * inter, k), RO, w), "y": (F16, (m, inter), 0, None)})
     try:
         y = hwiden(s.run("gemm_swiglu", ["y"], a="a", w="w", y="y", m=m, inter=inter, k=k)["y"])
+        assert np.isfinite(y).all()
         h = hwiden(a).astype(np.float64) @ hwiden(w).astype(np.float64).T
         g, u = h[:, :inter], h[:, inter:]
         ref = g / (1 + np.exp(-g)) * u
@@ -117,11 +136,12 @@ def test_gemm_swiglu():
         s.close()
 
 
-@pytest.mark.parametrize("T,pos0,max_pos", [(100, 37, 256), (300, 64, 512)])
+@pytest.mark.parametrize("T,pos0,max_pos", [(100, 37, 256), (300, 64, 512), (2048, 37, 2112), (2048, 64, 2112)])
 def test_gemm_qkv_rope_epilogue(T, pos0, max_pos):
     """q|k|v projection with the per-head RMSNorm + RoPE epilogue and the K / V^T cache writes, against CpuRef F64
     on the same fp16 operands: an unaligned position (element-wise V^T stores) and an aligned one (16-byte rows for the
-    two whole row tiles, element-wise for the partial third)."""
+    two whole row tiles, element-wise for the partial third); at 2048 rows (512 tiles: the direct-to-LDS loop of the
+    2048-token prefill) with an unaligned and an aligned first position."""
     H = 256
     r = np.random.default_rng(11)
     h = f16(r.standard_normal((T, H)))
