@@ -2405,21 +2405,22 @@ std::vector<KernelSpec> fast_catalog() {
                   TOK_R("x2", DT(F32) | DT(BF16) | DT(F16) | DT(U32)), TOK_R("x3", DT(F32) | DT(BF16) | DT(F16) | DT(U32))},
                  [](const uint32_t*, const uint32_t*) {}});
     // 38 decode_step_persistent: the whole one-sequence decode step in one launch of `blocks` resident workgroups.
-    // Weights and caches are the layer-stacked tensors ([layers, ...]); the exchange buffer holds the header and the
-    // tagged hand-off entries (persist::exchange_entries 8-byte entries).
+    // Weights and caches are the layer-stacked tensors ([layers, ...]); the projection matrices and the lm_head
+    // (embed16) are their exact fp16 copies; embed (bf16) feeds the embedding row. The exchange buffer holds the header
+    // and the tagged hand-off entries (persist::exchange_entries 8-byte entries).
     c.push_back({"decode_step_persistent", "fast", {persist::kThreads, 1, 1}, true,
-                 [](const uint32_t* w) { return Grid3{w[30], 1, 1}; },
+                 [](const uint32_t* w) { return Grid3{w[31], 1, 1}; },
                  {TOK_R("embed", DT(BF16)), TOK_R("final_norm", DT(BF16)), TOK_R("in_norm", DT(BF16)),
-                  TOK_R("qkv", DT(BF16)), TOK_R("q_norm", DT(BF16)), TOK_R("k_norm", DT(BF16)), TOK_R("o_proj", DT(BF16)),
-                  TOK_R("post_norm", DT(BF16)), TOK_R("gate_up", DT(BF16)), TOK_R("down", DT(BF16)),
+                  TOK_R("qkv", DT(F16)), TOK_R("q_norm", DT(BF16)), TOK_R("k_norm", DT(BF16)), TOK_R("o_proj", DT(F16)),
+                  TOK_R("post_norm", DT(BF16)), TOK_R("gate_up", DT(F16)), TOK_R("down", DT(F16)),
                   TOK_RW("k_cache", DT(F16)), TOK_RW("v_cache", DT(F16)), TOK_R("cos", DT(F32)), TOK_R("sin", DT(F32)),
                   TOK_W("logits", DT(F32)), TOK_RW("state", DT(U32)), TOK_W("out_ids", DT(U32)),
-                  TOK_RW("exchange", DT(U32)), U32F("layers"), U32F("hidden"), U32F("q_heads"), U32F("kv_heads"),
-                  U32F("inter"), U32F("vocab"), U32F("max_pos"), U32F("max_steps"), U32F("write_logits"), F32F("eps"),
-                  F32F("scale"), U32F("blocks")},
+                  TOK_RW("exchange", DT(U32)), TOK_R("embed16", DT(F16)), U32F("layers"), U32F("hidden"),
+                  U32F("q_heads"), U32F("kv_heads"), U32F("inter"), U32F("vocab"), U32F("max_pos"), U32F("max_steps"),
+                  U32F("write_logits"), F32F("eps"), F32F("scale"), U32F("blocks")},
                  [](const uint32_t* w, const uint32_t* c) {
-                     const int64_t L = w[19], H = w[20], QH = w[21], KVH = w[22], I = w[23], V = w[24], MP = w[25];
-                     const persist::Shape sh{int(H), int(QH), int(KVH), 128, int(I), int(MP), int(w[30])};
+                     const int64_t L = w[20], H = w[21], QH = w[22], KVH = w[23], I = w[24], V = w[25], MP = w[26];
+                     const persist::Shape sh{int(H), int(QH), int(KVH), 128, int(I), int(MP), int(w[31])};
                      if (L < 1 || V < 1 || MP < 1) contract_fail("decode_step_persistent: layers, vocab and max_pos >= 1");
                      if (const char* why = persist::unsupported(sh))
                          contract_fail("decode_step_persistent: this shape is not covered (%s)", why);
@@ -2438,10 +2439,11 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 11, L * KVH * MP * 128, "decode_step_persistent", "v_cache");
                      need(c, 12, MP * 64, "decode_step_persistent", "cos");
                      need(c, 13, MP * 64, "decode_step_persistent", "sin");
-                     need(c, 14, w[27] ? V : 0, "decode_step_persistent", "logits");
+                     need(c, 14, w[28] ? V : 0, "decode_step_persistent", "logits");
                      need(c, 15, 3, "decode_step_persistent", "state");
-                     need(c, 16, w[26], "decode_step_persistent", "out_ids");
+                     need(c, 16, w[27], "decode_step_persistent", "out_ids");
                      need(c, 17, 2 * int64_t(persist::exchange_entries(int(L), sh)), "decode_step_persistent", "exchange");
+                     need(c, 18, V * H, "decode_step_persistent", "embed16");
                  }});
     // 39 gemm_residual_split: a, w, partials, m, n, k, splits. partials[z] = a[:, k range z] . w[:, k range z]^T, the k
     // range split in `splits` equal parts of multiples of 64; residual_add_norm adds them to the residual stream. For

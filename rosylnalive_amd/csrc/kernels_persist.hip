@@ -80,17 +80,22 @@ constexpr int kUD = 2 * kPB * kNCH / kWaves;             // (gate/up row, chunk)
 static_assert(kRA == 2 && kNCC == 2 && kNCE == 3 && kPB == 12 && kUD == 6 && kRowsW == 4, "the 0.6B decode shape");
 static_assert(kRowsG <= 64 && kQPK * 16 == kJN, "one combine item and one row run per workgroup");
 
+// The projection matrices and the tied lm_head are read as their fp16 copies, which hold the same values as the bf16
+// weights (the executor refuses weights beyond the fp16 range; weights under 2^-14 in magnitude round to fp16's 2^-24
+// grid): a v_fma_mix_f32 takes a half of a packed pair as it is, one instruction per product where the bf16 pair
+// needs a shift or a mask before each FMA.
 struct PArgs {
-    const uint16_t* embed;       // [V, H] bf16; also the tied lm_head
-    const uint16_t* final_norm;  // [H]
+    const uint16_t* embed;       // [V, H] bf16: the embedding row
+    const uint16_t* embed16;     // [V, H] f16: the tied lm_head
+    const uint16_t* final_norm;  // [H] bf16 (every norm weight is bf16)
     const uint16_t* in_norm;     // [L, H]
-    const uint16_t* qkv;         // [L, QC + 2 KC, H]
+    const uint16_t* qkv;         // [L, QC + 2 KC, H] f16
     const uint16_t* q_norm;      // [L, 128]
     const uint16_t* k_norm;      // [L, 128]
-    const uint16_t* o_proj;      // [L, H, QC]
+    const uint16_t* o_proj;      // [L, H, QC] f16
     const uint16_t* post_norm;   // [L, H]
-    const uint16_t* gate_up;     // [L, 2 I, H] (gate rows, then up rows)
-    const uint16_t* down;        // [L, H, I]
+    const uint16_t* gate_up;     // [L, 2 I, H] f16 (gate rows, then up rows)
+    const uint16_t* down;        // [L, H, I] f16
     uint16_t* kc;                // [L, KVH, MP, 128] f16
     uint16_t* vc;                // [L, KVH, 128, MP] f16
     const float* cos_t;          // [MP, 64]
@@ -320,12 +325,16 @@ __device__ __forceinline__ void norm_lane(const float* vec, const u32x4 (&nw)[NC
     }
 }
 
-// sum over this lane's chunks of w . v (bf16 weights, f32 vector in registers), not yet reduced over the wave
+// sum over this lane's chunks of w . v (8 fp16 weights, f32 vector in registers), not yet reduced over the wave: the
+// products in element order, each a v_fma_mix_f32 on its half of the packed pair. (Written with the halves taken by
+// shifts and masks: a bit cast of the vector's element to a half pair made this compiler load only the first of the
+// four words and use it for all of them.)
 __device__ __forceinline__ float dot8(u32x4 wv, const float* v, float acc) {
-    float f[8];
-    unpack8bf(wv, f);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc = fmaf(f[e], v[e], acc);
+    for (int i = 0; i < 4; ++i) {
+        acc = fmaf(v[2 * i], h2f(uint16_t(wv[i] & 0xFFFFu)), acc);
+        acc = fmaf(v[2 * i + 1], h2f(uint16_t(wv[i] >> 16)), acc);
+    }
     return acc;
 }
 
@@ -826,7 +835,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     auto load4 = [&](u32x4 (&dst)[4][kNCH], int row) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint16_t* er = a.embed + size_t(min(row + r, V - 1)) * kH + 8 * lane;
+            const uint16_t* er = a.embed16 + size_t(min(row + r, V - 1)) * kH + 8 * lane;
 #pragma unroll
             for (int c = 0; c < kNCH; ++c) dst[r][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(er + 512 * c));
         }
@@ -950,7 +959,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
 
 // ---------------------------------------------------------------- launcher (catalog id 38)
 // fields: embed, final_norm, in_norm, qkv, q_norm, k_norm, o_proj, post_norm, gate_up, down, k_cache, v_cache, cos,
-// sin, logits, state, out_ids, exchange, layers, hidden, q_heads, kv_heads, inter, vocab, max_pos, max_steps,
+// sin, logits, state, out_ids, exchange, embed16, layers, hidden, q_heads, kv_heads, inter, vocab, max_pos, max_steps,
 // write_logits, eps, scale, blocks
 void* f16_range_word_persist() {
     void* p = nullptr;
@@ -968,6 +977,7 @@ void launch_decode_persistent(const PreparedDispatch& pd, void* const* p, hipStr
     };
     PArgs a;
     a.embed = (const uint16_t*)p[0];
+    a.embed16 = (const uint16_t*)p[18];
     a.final_norm = (const uint16_t*)p[1];
     a.in_norm = (const uint16_t*)p[2];
     a.qkv = (const uint16_t*)p[3];
@@ -985,13 +995,13 @@ void launch_decode_persistent(const PreparedDispatch& pd, void* const* p, hipStr
     a.state = (uint32_t*)p[15];
     a.out_ids = (uint32_t*)p[16];
     a.xch = (uint64_t*)p[17];
-    a.layers = int(w[19]);
-    a.vocab = int(w[24]);
-    a.max_pos = int(w[25]);
-    a.max_steps = int(w[26]);
-    a.write_logits = int(w[27]);
-    a.eps = f32(w[28]);
-    a.scale_log2 = f32(w[29]) * 1.4426950408889634f;
+    a.layers = int(w[20]);
+    a.vocab = int(w[25]);
+    a.max_pos = int(w[26]);
+    a.max_steps = int(w[27]);
+    a.write_logits = int(w[28]);
+    a.eps = f32(w[29]);
+    a.scale_log2 = f32(w[30]) * 1.4426950408889634f;
     auto kern = k_decode_persist;
     // every workgroup must be resident at once (they wait for each other): at least one per CU, G <= CUs
     static int occupancy = -1;

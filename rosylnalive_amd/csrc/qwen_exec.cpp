@@ -267,18 +267,32 @@ void QwenExec::plan() {
         add(lname(i, kLayerWeights[10]), Weights, BF16, {H, I}, ReadOnly);
     }
     if (fast) {
-        // exact fp16 copies of the matrices for the prefill MFMA GEMMs, written on device from the bf16 originals
+        // exact fp16 copies of the matrices for the prefill MFMA GEMMs (and the persistent decode step), written on
+        // device from the bf16 originals; layer-stacked like the originals when the decode step is persistent
         auto copy16 = [&](const std::string& of, const std::string& name, std::vector<uint32_t> dims) {
             add(name, Weights, F16, std::move(dims));
             f16_copy_[of] = name;
         };
         copy16("model.embed_tokens.weight", "embed.f16", {V, H});
+        if (persist_) {
+            add("stack.qkv_proj.f16", Weights, F16, {L, N1, H});
+            add("stack.o_proj.f16", Weights, F16, {L, H, QC});
+            add("stack.gate_up_proj.f16", Weights, F16, {L, 2 * I, H});
+            add("stack.down_proj.f16", Weights, F16, {L, H, I});
+        }
+        auto view16 = [&](const std::string& of, const std::string& name, const std::string& stack,
+                          std::vector<uint32_t> dims, uint64_t off) {
+            if (!persist_) return copy16(of, name, std::move(dims));
+            add_view(name, stack, std::move(dims), off);
+            f16_copy_[of] = name;
+        };
         for (int i = 0; i < c.layers; ++i) {
             std::string p = "L" + std::to_string(i);
-            copy16(p + ".qkv_proj", p + ".qkv_proj.f16", {QC + 2 * KC, H});
-            copy16(lname(i, kLayerWeights[4]), p + ".o_proj.f16", {H, QC});
-            copy16(p + ".gate_up_proj", p + ".gate_up_proj.f16", {2 * I, H});
-            copy16(lname(i, kLayerWeights[10]), p + ".down_proj.f16", {H, I});
+            const uint64_t ui = uint64_t(i);
+            view16(p + ".qkv_proj", p + ".qkv_proj.f16", "stack.qkv_proj.f16", {QC + 2 * KC, H}, ui * N1 * H);
+            view16(lname(i, kLayerWeights[4]), p + ".o_proj.f16", "stack.o_proj.f16", {H, QC}, ui * H * QC);
+            view16(p + ".gate_up_proj", p + ".gate_up_proj.f16", "stack.gate_up_proj.f16", {2 * I, H}, ui * 2 * I * H);
+            view16(lname(i, kLayerWeights[10]), p + ".down_proj.f16", "stack.down_proj.f16", {H, I}, ui * H * I);
         }
     }
     add("rope.cos", Rope, F32, {MP, HD / 2}, ReadOnly);
@@ -769,11 +783,11 @@ void QwenExec::record_decode_fast() {
     if (persist_) {
         dispatch(l, "decode_step_persistent",
                  {tk("model.embed_tokens.weight"), tk("model.norm.weight"), tk("stack.input_layernorm"),
-                  tk("stack.qkv_proj"), tk("stack.q_norm"), tk("stack.k_norm"), tk("stack.o_proj"),
-                  tk("stack.post_attention_layernorm"), tk("stack.gate_up_proj"), tk("stack.down_proj"),
+                  tk("stack.qkv_proj.f16"), tk("stack.q_norm"), tk("stack.k_norm"), tk("stack.o_proj.f16"),
+                  tk("stack.post_attention_layernorm"), tk("stack.gate_up_proj.f16"), tk("stack.down_proj.f16"),
                   tk("stack.k_cache"), tk("stack.v_cache"), tk("rope.cos"), tk("rope.sin"), tk("logits"), tk("dec.state"),
-                  tk("dec.out_ids"), tk("dec.exchange"), uint32_t(c.layers), H, uint32_t(c.heads), uint32_t(c.kv_heads),
-                  I, V, MP, MP, 1, eps, scale, uint32_t(persist_blocks_)});
+                  tk("dec.out_ids"), tk("dec.exchange"), tk("embed.f16"), uint32_t(c.layers), H, uint32_t(c.heads),
+                  uint32_t(c.kv_heads), I, V, MP, MP, 1, eps, scale, uint32_t(persist_blocks_)});
         decode_list_ = l;
         return;
     }

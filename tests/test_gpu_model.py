@@ -267,8 +267,10 @@ def test_fast_decode_runs_the_persistent_step(fast_setup):
 def test_persistent_decode_step_matches_kernel_list():
     """decode_step_persistent against the per-stage kernel list on the same weights and caches: teacher-forced steps
     at short context (one split) and over random caches at positions whose splits take 1, 2 and 3 chunks of 64 keys,
-    then 20 greedy steps. Layer 0's q|k|v projections and appended cache rows are the same bits (same per-lane
-    arithmetic); after it the residual rows differ by the order of a few partial sums, and so do the logits."""
+    then 20 greedy steps. Layer 0's appended cache rows agree to one fp16 rounding (the same per-lane products, but the
+    persistent step multiplies by the fp16 copies of the matrices, which differ from the bf16 weights only for weights
+    under 2^-14 in magnitude); after it the residual rows differ by the order of a few partial sums, and so do the
+    logits."""
     cfg = reduced_0_6b(layers=2, max_pos=4352)
     w = synthetic_weights(cfg, seed=11)
     mp = _fast_model(cfg, w, kernels=False)
@@ -293,8 +295,8 @@ def test_persistent_decode_step_matches_kernel_list():
                 for which in ("k", "v"):
                     a = mp.read_cache(layer, which, pos, 1)
                     b = mk.read_cache(layer, which, pos, 1)
-                    if layer == 0:  # the same input row: the same bits
-                        assert np.array_equal(a, b), (pos, layer, which)
+                    if layer == 0:  # the same input row: within one fp16 rounding
+                        assert np.all(np.abs(a - b) <= np.abs(b) * 2.0 ** -10 + 2.0 ** -24), (pos, layer, which)
                     else:  # the residual row entering the layer differs in the last bits
                         assert np.max(np.abs(a - b)) <= 1e-2 * max(1.0, float(np.max(np.abs(b)))), (pos, layer, which)
 
