@@ -81,9 +81,9 @@ static_assert(kRA == 2 && kNCC == 2 && kNCE == 3 && kPB == 12 && kUD == 6 && kRo
 static_assert(kRowsG <= 64 && kQPK * 16 == kJN, "one combine item and one row run per workgroup");
 
 // The projection matrices and the tied lm_head are read as their fp16 copies, which hold the same values as the bf16
-// weights (the executor refuses weights beyond the fp16 range; weights under 2^-14 in magnitude round to fp16's 2^-24
-// grid): a v_fma_mix_f32 takes a half of a packed pair as it is, one instruction per product where the bf16 pair
-// needs a shift or a mask before each FMA.
+// weights (the executor refuses weights beyond the fp16 range; weights under 2^-17 in magnitude round to fp16's
+// subnormal 2^-24 grid): a v_fma_mix_f32 takes a half of a packed pair as it is, one instruction per product where the
+// bf16 pair needs a shift or a mask before each FMA.
 struct PArgs {
     const uint16_t* embed;       // [V, H] bf16: the embedding row
     const uint16_t* embed16;     // [V, H] f16: the tied lm_head

@@ -269,7 +269,7 @@ def test_persistent_decode_step_matches_kernel_list():
     at short context (one split) and over random caches at positions whose splits take 1, 2 and 3 chunks of 64 keys,
     then 20 greedy steps. Layer 0's appended cache rows agree to one fp16 rounding (the same per-lane products, but the
     persistent step multiplies by the fp16 copies of the matrices, which differ from the bf16 weights only for weights
-    under 2^-14 in magnitude); after it the residual rows differ by the order of a few partial sums, and so do the
+    under 2^-17 in magnitude); after it the residual rows differ by the order of a few partial sums, and so do the
     logits."""
     cfg = reduced_0_6b(layers=2, max_pos=4352)
     w = synthetic_weights(cfg, seed=11)
