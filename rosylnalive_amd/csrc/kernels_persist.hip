@@ -748,11 +748,22 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         }
         lds_barrier();
         PSTAMP(6);
-        if (t < kCW) {
+        if (t < kCW) {  // in split order; four splits' weights and rows read ahead of their FMAs
             const int hh = t >> 7, d = t & 127;
             const float* rows = vec + hh * S_used * 4 * kPartVecs + d;
             float O = 0.f;
-            for (int sp = 0; sp < S_used; ++sp) O = fmaf(ps[hh][sp], rows[sp * 4 * kPartVecs], O);
+            int sp = 0;
+            for (; sp + 4 <= S_used; sp += 4) {
+                float pw[4], rv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    pw[u] = ps[hh][sp + u];
+                    rv[u] = rows[(sp + u) * 4 * kPartVecs];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) O = fmaf(pw[u], rv[u], O);
+            }
+            for (; sp < S_used; ++sp) O = fmaf(ps[hh][sp], rows[sp * 4 * kPartVecs], O);
             qs[hh][d] = O;
         }
         lds_barrier();
