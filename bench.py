@@ -213,14 +213,14 @@ def main():
         for _ in range(reps):
             cl.dispatch("decode_step_persistent", ArgBlock.encode(
                 "decode_step_persistent", embed=tok("model.embed_tokens.weight"), final_norm=tok("model.norm.weight"),
-                in_norm=tok("stack.input_layernorm"), qkv=tok("stack.qkv_proj"), q_norm=tok("stack.q_norm"),
-                k_norm=tok("stack.k_norm"), o_proj=tok("stack.o_proj"),
-                post_norm=tok("stack.post_attention_layernorm"), gate_up=tok("stack.gate_up_proj"),
-                down=tok("stack.down_proj"), k_cache=tok("stack.k_cache"), v_cache=tok("stack.v_cache"),
+                in_norm=tok("stack.input_layernorm"), qkv=tok("stack.qkv_proj.f16"), q_norm=tok("stack.q_norm"),
+                k_norm=tok("stack.k_norm"), o_proj=tok("stack.o_proj.f16"),
+                post_norm=tok("stack.post_attention_layernorm"), gate_up=tok("stack.gate_up_proj.f16"),
+                down=tok("stack.down_proj.f16"), k_cache=tok("stack.k_cache"), v_cache=tok("stack.v_cache"),
                 cos=tok("rope.cos"), sin=tok("rope.sin"), logits=tok("logits"), state=tok("dec.state"),
-                out_ids=tok("dec.out_ids"), exchange=tok("dec.exchange"), layers=L, hidden=H, q_heads=QH,
-                kv_heads=KVH, inter=I, vocab=V, max_pos=cfg.max_pos, max_steps=cfg.max_pos, write_logits=1,
-                eps=cfg.eps, scale=float(np.float32(HD ** -0.5)), blocks=256))
+                out_ids=tok("dec.out_ids"), exchange=tok("dec.exchange"), embed16=tok("embed.f16"), layers=L,
+                hidden=H, q_heads=QH, kv_heads=KVH, inter=I, vocab=V, max_pos=cfg.max_pos, max_steps=cfg.max_pos,
+                write_logits=1, eps=cfg.eps, scale=float(np.float32(HD ** -0.5)), blocks=256))
         cl.end_timer(tm)
         comp = backend.wait(backend.submit(cl))
         cl.release()
