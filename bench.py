@@ -328,8 +328,8 @@ def main():
         for i in range(L):
             cl.dispatch("attention_prefill_f16", ArgBlock.encode(
                 "attention_prefill_f16", q=tok("q"), k_cache=tok(f"L{i}.k_cache"), v_cache=tok(f"L{i}.v_cache"),
-                y=tok("o"), rows=2048, past=0, q_heads=QH, kv_heads=KVH, max_pos=cfg.max_pos,
-                scale=float(np.float32(HD ** -0.5))))
+                y=tok("o"), workspace=tok("attn.ws"), rows=2048, past=0, q_heads=QH, kv_heads=KVH,
+                max_pos=cfg.max_pos, scale=float(np.float32(HD ** -0.5))))
         cl.end_timer(tm)
         comp = backend.wait(backend.submit(cl))
         cl.release()

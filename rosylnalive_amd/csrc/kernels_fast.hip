@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "device.hpp"
+#include "attn_prefill.hpp"
 #include "fast_common.hpp"
 #include "persist.hpp"
 
@@ -663,10 +664,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 
 // ================================================================ 16 attention_prefill_f16
 // Causal GQA flash attention on v_mfma_f32_32x32x16_f16 (32 query columns per wave: half the LDS operand bytes per
-// FLOP of the 16-column form), two query heads per KV head. A workgroup takes 32 query rows of both heads of one KV group: wave w owns head 2 kvhead + w % 2
-// (32 query columns, one MFMA column tile) and key half w / 2 (keys 32 (w / 2) .. + 31) of every 64-key block, so the
-// four waves share each block's K and V^T in LDS (64 KB: two stages, one barrier per block) and each wave runs its own
-// online softmax over its half; the two halves of a head merge through LDS at the end.
+// FLOP of the 16-column form), two query heads per KV head. A tile is 32 query rows of both heads of one KV group: wave
+// w owns head 2 kvhead + w % 2 (32 query columns, one MFMA column tile) and key half w / 2 (keys 32 (w / 2) .. + 31)
+// of every 64-key block, so the four waves share each block's K and V^T in LDS (two stages, one barrier per block)
+// and each wave runs its own online softmax over its half; the two halves of a head merge through LDS at the end.
 // S^T = K Q^T (A = 32 keys x 16 dims of K from LDS, B = Q^T from registers) puts one query per lane column; lanes
 // l and l + 32 hold the other 16 keys of the same column, so the row statistics take one v_permlane32_swap. The P^T
 // operand of O^T = V^T P^T needs keys 8 h .. 8 h + 7 of a 16-key step in lane half h; a lane holds keys
@@ -674,48 +675,41 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 // stays in LDS in its natural key order. LDS rows are padded by 16 bytes (K 272, V^T 144), so the 16 lanes of each
 // read phase hit distinct banks and every operand address is a per-lane base plus an immediate. The softmax keeps a
 // reference maximum per column that moves (rescaling O and the sum) only when a block's maximum exceeds it by more
-// than 8 in the exponent: P stays at most 2^8, and most blocks need no rescale. Blocks are issued longest first for the
-// first half of the grid and shortest first for the second, so the two workgroups of a CU carry about equal causal
-// work.
-constexpr int kAttnRows = 32;
+// than 8 in the exponent: P stays at most 2^8, and most blocks need no rescale.
+//
+// Causal balance: tile i needs about i / 2 key blocks, and a workgroup alone on its CU runs its blocks more slowly
+// than two sharing one, so whole tiles would leave the longest tiles running alone at the end. Tiles pair up, short
+// tile s = p with long tile n - 1 - p, and the pair's blocks split over two workgroups: X runs the first `a` key
+// blocks of the long tile, then the whole short tile; Y runs the rest of the long tile. The two parts of the long
+// tile meet in the workspace: each part, when done, reads the pair's counter; if the other part is already there it
+// merges the other's partial (O^T, m, l) with its own and writes the rows, otherwise it stores its partial, then adds
+// to the counter, and merges if the other part arrived in between. The merge combines the parts in X, Y order
+// whichever workgroup runs it, so the result does not depend on timing; the merging workgroup resets the counter.
+// Nothing waits for another workgroup. An odd tile count leaves the middle tile whole.
+constexpr int kAttnRows = attn_prefill::kRows;
+constexpr int kAttnSlotWords = attn_prefill::kSlotWords;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// key blocks of tile `tile` (64-key blocks up to the last visible key of its last row)
+__device__ __forceinline__ int attn_tile_blocks(int tile, int T, int past) {
+    return (past + min(tile * kAttnRows + kAttnRows - 1, T - 1) + 1 + 63) / 64;
+}
+
 __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
-                                                      uint16_t* y, int T, int past, int qh, int max_pos,
-                                                      float scale_log2) {
+                                                      uint16_t* y, uint32_t* ws, int T, int past, int qh,
+                                                      int max_pos, float scale_log2) {
     // stage s: K [64 keys][128 dims + 8] at s * kStage, V^T [128 dims][64 keys + 8] at s * kStage + kVtOff
     constexpr int kKRow = 272, kVRow = 144, kVtOff = 64 * kKRow, kStage = kVtOff + 128 * kVRow;
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
+    __shared__ int s_flag;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, c32 = lane & 31, h = lane >> 5;
     const int cg = w & 1, kh = w >> 1;
-    const int ntile = (T + kAttnRows - 1) / kAttnRows, kvh = int(gridDim.y);
-    const int L = int(blockIdx.y) * ntile + int(blockIdx.x), j = L / kvh, half = (ntile + 1) / 2;
-    const int row0 = (j < half ? ntile - 1 - j : j - half) * kAttnRows;
-    const int kvhead = L % kvh;
+    const int ntile = (T + kAttnRows - 1) / kAttnRows, kvh = int(gridDim.y), npairs = ntile / 2;
+    const int L = int(blockIdx.y) * ntile + int(blockIdx.x);
+    const int kvhead = L % kvh, u = L / kvh;
     const int head = kvhead * 2 + cg;
-    const int row = row0 + c32;  // this lane's query row (its column of S^T and O^T)
     const int QC = qh * 128;
-
-    // Q^T operand of k-step s (dims 16 s .. 16 s + 15): this lane's dims 16 s + 8 h .. + 7
-    f16x8 qf[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (row < T) v = *reinterpret_cast<const u32x4*>(q + size_t(row) * QC + head * 128 + 16 * s + 8 * h);
-        qf[s] = as_f16x8(v);
-    }
-    float m_run = -INFINITY, l_run = 0.f;
-    f32x16 o[4];
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
-
-    const int last_row = min(row0 + kAttnRows - 1, T - 1);
-    const int kend = past + last_row + 1;  // keys [0, kend) are visible to some row of the tile; kend <= max_pos
-    const int nkb = (kend + 63) / 64;
-    const int qpos = past + row;
     const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kc + size_t(kvhead) * max_pos * 128, max_pos * 256);
     const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc + size_t(kvhead) * 128 * max_pos, max_pos * 256);
     // thread t moves chunks t + 256 i of a block: K row c / 16, dims 8 (c % 16) ..; V^T row (dim) c / 8, keys 8 (c % 8) ..
@@ -733,24 +727,56 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
     const int krd = (32 * kh + c32) * kKRow + 16 * h;
     const int vrd = kVtOff + c32 * kVRow + 16 * (4 * kh + h);
 
-    // The loads of a 64-key block are unconditional (kb + 63 < max_pos: kb < kend <= max_pos, both multiples of 64);
-    // keys at or past kend may hold anything. Their scores are masked, so K needs nothing; V is zeroed there before it
-    // is stored, since a zero weight times a NaN is still a NaN. Two register sets: block j is loaded into set j % 2
-    // two blocks before it is stored (past the last block: the last one again, never stored).
+    // this workgroup's items: (tile, first key block, end key block, role: -1 whole tile, 0 part X, 1 part Y)
+    int pair = 0, nitems = 1, split_a = 0, long_tile = 0, short_tile = 0;
+    if (u < 2 * npairs) {
+        pair = u < npairs ? u : u - npairs;
+        short_tile = pair;
+        long_tile = ntile - 1 - pair;
+        const int ns = attn_tile_blocks(short_tile, T, past), nl = attn_tile_blocks(long_tile, T, past);
+        // even halves, then two more blocks for X: X is dispatched first, so its waves win the issue arbitration
+        // while both run, and Y finishes alone at the end (T 2048: 16 / 17 blocks 36.3 us, 18 / 15 blocks 35.8 us)
+        const int even = (ns + nl) / 2 - ns;
+        split_a = even > 0 ? min(even + 2, nl - 1) : 0;
+        if (u < npairs && split_a > 0) nitems = 2;
+    }
+    const int ws_ctr_words = int(attn_prefill::counter_words(T, kvh));
+
+    f16x8 qf[8];
+    float m_run, l_run;
+    f32x16 o[4];
+    int row0, row, kend, kb0, nb;
     u32x4 rk[2][4], rv[2][4];
-    auto fetch = [&](auto set, int jb) __attribute__((always_inline)) {
+    float sc[16];
+
+    // Software pipeline over an item's blocks kb0 .. kb0 + nb - 1 (relative index j), one barrier per step: step j
+    // stores K(j + 2) and V^T(j + 1), issues the scores of block j + 1 to the matrix core and runs block j's softmax
+    // on the VALU while they execute, then block j's P V. K(b) lives in the K region of stage b % 2 and V^T(b) in the
+    // V^T region of stage b % 2: at step j (P = j % 2) the K region of stage P takes K(j + 2) (it held K(j), read by
+    // step j - 1), the V^T region of stage 1 - P takes V^T(j + 1) (it held V^T(j - 1), read by step j - 1), and the
+    // step reads K(j + 1) from stage 1 - P and V^T(j) from stage P, both stored by step j - 1 before this step's
+    // barrier.
+    // Global loads: group g = K(g) and V^T(g - 1), loaded into register set g % 2 by step g - 4 (or the prologue) and
+    // stored by step g - 2. The loads are unconditional (a block index past the item's last is clamped to it, and
+    // every block of an item ends below kend <= max_pos); keys at or past kend may hold anything. Their scores are
+    // masked, so K needs nothing; V is zeroed there before it is stored, since a zero weight times a NaN is still a
+    // NaN.
+    auto fetch = [&](auto set, int g) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value;
-        const int kbl = min(jb, nkb - 1) * 64;
+        const int kbk = (kb0 + min(g, nb - 1)) * 64, kbv = (kb0 + min(max(g - 1, 0), nb - 1)) * 64;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rk[S][i] = __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, koff[i], kbl * 256, 0);
+        for (int i = 0; i < 4; ++i) rk[S][i] = __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, koff[i], kbk * 256, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rv[S][i] = __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, voff[i], kbl * 2, 0);
+        for (int i = 0; i < 4; ++i) rv[S][i] = __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, voff[i], kbv * 2, 0);
     };
-    auto block = [&](auto set, int jb) __attribute__((always_inline)) {
-        constexpr int S = decltype(set)::value;
-        const int kb = jb * 64;
-        uint8_t* st = lds + S * kStage;
-        // stage S was last read by block jb - 2, which every wave finished before the previous barrier
+    auto store_k = [&](auto set, auto stage) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value, G = decltype(stage)::value;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(lds + G * kStage + kst[i]) = rk[S][i];
+    };
+    auto store_v = [&](auto set, auto stage, int j) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value, G = decltype(stage)::value;
+        const int kb = (kb0 + j) * 64;
         if (kb + 64 > kend) {  // uniform: zero V^T past kend (8 keys per chunk, two per word)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -764,34 +790,33 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *reinterpret_cast<u32x4*>(st + kst[i]) = rk[S][i];
-            *reinterpret_cast<u32x4*>(st + vst[i]) = rv[S][i];
-        }
-        fetch(set, jb + 2);
-        lds_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-
-        // S^T for this wave's 32 keys (one accumulation chain over the 8 dim steps: the matrix core chains dependent
-        // accumulations; two chains and a final add measured slower)
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(lds + G * kStage + vst[i]) = rv[S][i];
+    };
+    // S^T of the first block for this wave's 32 keys from the K region of stage 0 (one accumulation chain over the 8
+    // dim steps: the matrix core chains dependent accumulations)
+    auto first_scores = [&]() __attribute__((always_inline)) {
         f32x16 sa;
 #pragma unroll
         for (int r = 0; r < 16; ++r) sa[r] = 0.f;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const f16x8 a0 = as_f16x8(*reinterpret_cast<const u32x4*>(st + krd + 32 * s));
+            const f16x8 a0 = as_f16x8(*reinterpret_cast<const u32x4*>(lds + krd + 32 * s));
             sa = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[s], sa, 0, 0, 0);
         }
-        float sc[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = sa[r];
-
+    };
+    // block j's softmax on its scores sc with the scores of block j + 1 into sn, then O^T += V^T P^T with V^T from
+    // stage G
+    auto softmax_pv = [&](f32x16& sn, int j, auto stage) __attribute__((always_inline)) {
+        constexpr int G = decltype(stage)::value;
+        const int kb = (kb0 + j) * 64;
         // causal mask, only where the key block crosses the diagonal or the tile runs past T (uniform).
         // Register r holds key kb + 32 kh + 8 (r / 4) + 4 h + r % 4.
         const bool need_mask = kb + 63 > past + row0 || row0 + kAttnRows > T;
         if (need_mask) {  // a real branch (the empty asm keeps the compiler from running the mask on every block)
             asm volatile("");
-            const int lim = row < T ? qpos - kb - 32 * kh - 4 * h : -1;
+            const int lim = row < T ? past + row - kb - 32 * kh - 4 * h : -1;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sc[r] = (8 * (r >> 2) + (r & 3) > lim) ? -INFINITY : sc[r];
         }
@@ -819,11 +844,28 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
             m_run = m_new;
         }
         const float mc = m_run == -INFINITY ? 0.f : m_run * scale_log2;
+        // the next block's scores (K from stage 1 - G), one dim step per two of this block's exponentials: the matrix
+        // core runs the chain while the VALU computes the exponentials (one basic block, ordered below)
+        constexpr int GN = 1 - G;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sn[r] = 0.f;
         float lsum = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], scale_log2, -mc));
-            lsum += sc[r];
+        for (int s = 0; s < 8; ++s) {
+            const f16x8 a0 = as_f16x8(*reinterpret_cast<const u32x4*>(lds + GN * kStage + krd + 32 * s));
+            sn = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[s], sn, 0, 0, 0);
+#pragma unroll
+            for (int r = 2 * s; r < 2 * s + 2; ++r) {
+                sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], scale_log2, -mc));
+                lsum += sc[r];
+            }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two K operand reads
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // the MFMA of dim step s
+            if (s < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // the read of step s + 2
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // two exponentials, their FMAs and sums
         }
         {
             auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum), __float_as_uint(lsum), false, false);
@@ -841,59 +883,228 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
             const f16x8 bq = as_f16x8(u32x4{xa[0], xb[0], xa[1], xb[1]});
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const f16x8 a = as_f16x8(*reinterpret_cast<const u32x4*>(st + vrd + dt * 32 * kVRow + 32 * ks));
+                const f16x8 a = as_f16x8(
+                    *reinterpret_cast<const u32x4*>(lds + G * kStage + vrd + dt * 32 * kVRow + 32 * ks));
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bq, o[dt], 0, 0, 0);
             }
         }
     };
     using A0 = std::integral_constant<int, 0>;
     using A1 = std::integral_constant<int, 1>;
-    fetch(A0{}, 0);
-    __builtin_amdgcn_sched_barrier(0);  // set 0 issues before set 1, as in the loop, so the first wait can be partial
-    fetch(A1{}, 1);
-    for (int jb = 0;; jb += 2) {
-        block(A0{}, jb);
-        if (jb + 1 >= nkb) break;
-        block(A1{}, jb + 1);
-        if (jb + 2 >= nkb) break;
-    }
+    // step j with P = j % 2: the scores of block j + 1 are taken whether or not it exists (a uniform branch here
+    // would split the MFMAs from the softmax they overlap); past the item's last block they read a stale stage and
+    // are discarded
+    auto step = [&](auto par, int j) __attribute__((always_inline)) {
+        constexpr int P = decltype(par)::value;
+        using Q = std::integral_constant<int, 1 - P>;
+        lds_barrier();
+        if (j + 2 < nb) store_k(par, par);
+        if (j + 1 < nb) store_v(par, Q{}, j + 1);
+        fetch(par, j + 4);
+        f32x16 sn;
+        softmax_pv(sn, j, par);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[r] = sn[r];
+    };
 
-    // merge the key halves: waves 2 and 3 hand (m, l, O^T) to waves 0 and 1 (same head) through LDS
-    lds_barrier();  // every wave is done with both stages
-    float* xo = reinterpret_cast<float*>(lds) + cg * 4224;  // per head: 64 x 64 O words, then m and l per lane
-    if (kh == 1) {
+    for (int item = 0; item < nitems; ++item) {
+        // the item: X's first item is its part of the long tile, its second the short tile
+        int tile, role;
+        if (u >= 2 * npairs) {
+            tile = npairs, kb0 = 0, role = -1;  // the middle tile of an odd count
+            nb = attn_tile_blocks(tile, T, past);
+        } else if (u < npairs) {
+            if (nitems == 2 && item == 0) tile = long_tile, kb0 = 0, nb = split_a, role = 0;
+            else tile = short_tile, kb0 = 0, nb = attn_tile_blocks(short_tile, T, past), role = -1;
+        } else {
+            tile = long_tile, kb0 = split_a, role = split_a > 0 ? 1 : -1;
+            nb = attn_tile_blocks(long_tile, T, past) - split_a;
+        }
+        row0 = tile * kAttnRows;
+        row = row0 + c32;  // this lane's query row (its column of S^T and O^T)
+        kend = past + min(row0 + kAttnRows - 1, T - 1) + 1;  // keys [0, kend) are visible to some row; kend <= max_pos
+
+        // Q^T operand of k-step s (dims 16 s .. 16 s + 15): this lane's dims 16 s + 8 h .. + 7
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if (row < T) v = *reinterpret_cast<const u32x4*>(q + size_t(row) * QC + head * 128 + 16 * s + 8 * h);
+            qf[s] = as_f16x8(v);
+        }
+        m_run = -INFINITY, l_run = 0.f;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-                *reinterpret_cast<f32x4*>(xo + ((dt * 4 + r4) * 64 + lane) * 4) =
-                    f32x4{o[dt][4 * r4], o[dt][4 * r4 + 1], o[dt][4 * r4 + 2], o[dt][4 * r4 + 3]};
-        xo[4096 + lane] = m_run;
-        xo[4160 + lane] = l_run;
-    }
-    lds_barrier();
-    if (kh == 0 && row < T) {
-        const float m1 = xo[4096 + lane], l1 = xo[4160 + lane];
-        const float M = fmaxf(m_run, m1);
-        const float Mc = M == -INFINITY ? 0.f : M * scale_log2;
-        const float e0 = __builtin_amdgcn_exp2f(m_run * scale_log2 - Mc), e1 = __builtin_amdgcn_exp2f(m1 * scale_log2 - Mc);
-        const float inv = 1.0f / (l_run * e0 + l1 * e1);
-        const float f0 = e0 * inv, f1 = e1 * inv;
+            for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+
+        fetch(A0{}, 0);
+        __builtin_amdgcn_sched_barrier(0);  // group 0 issues before group 1, so the first wait can be partial
+        fetch(A1{}, 1);
+        store_k(A0{}, A0{});     // K(0)
+        store_k(A1{}, A1{});     // K(1) (K(0) again when the item has one block: never read)
+        store_v(A1{}, A0{}, 0);  // V^T(0)
+        fetch(A0{}, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(A1{}, 3);
+        lds_barrier();
+        first_scores();
+        for (int j = 0;; j += 2) {
+            step(A0{}, j);
+            if (j + 1 >= nb) break;
+            step(A1{}, j + 1);
+            if (j + 2 >= nb) break;
+        }
+
+        // merge the key halves: waves 2 and 3 hand (m, l, O^T) to waves 0 and 1 (same head) through LDS
+        lds_barrier();  // every wave is done with both stages
+        float* xo = reinterpret_cast<float*>(lds) + cg * 4224;  // per head: 64 x 64 O words, then m and l per lane
+        if (kh == 1) {
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    *reinterpret_cast<f32x4*>(xo + ((dt * 4 + r4) * 64 + lane) * 4) =
+                        f32x4{o[dt][4 * r4], o[dt][4 * r4 + 1], o[dt][4 * r4 + 2], o[dt][4 * r4 + 3]};
+            xo[4096 + lane] = m_run;
+            xo[4160 + lane] = l_run;
+        }
+        lds_barrier();
         uint16_t* yr = y + size_t(row) * QC + head * 128;
-        uint32_t bad = 0;
+        if (role < 0) {
+            if (kh == 0 && row < T) {
+                const float m1 = xo[4096 + lane], l1 = xo[4160 + lane];
+                const float M = fmaxf(m_run, m1);
+                const float Mc = M == -INFINITY ? 0.f : M * scale_log2;
+                const float e0 = __builtin_amdgcn_exp2f(m_run * scale_log2 - Mc);
+                const float e1 = __builtin_amdgcn_exp2f(m1 * scale_log2 - Mc);
+                const float inv = 1.0f / (l_run * e0 + l1 * e1);
+                const float f0 = e0 * inv, f1 = e1 * inv;
+                uint32_t bad = 0;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+                for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const f32x4 b = *reinterpret_cast<const f32x4*>(xo + ((dt * 4 + r4) * 64 + lane) * 4);
-                uint2 v;
-                v.x = pack2h(o[dt][4 * r4] * f0 + b[0] * f1, o[dt][4 * r4 + 1] * f0 + b[1] * f1);
-                v.y = pack2h(o[dt][4 * r4 + 2] * f0 + b[2] * f1, o[dt][4 * r4 + 3] * f0 + b[3] * f1);
-                bad |= f16_bad2(v.x) | f16_bad2(v.y);
-                // register r of tile dt: dim 32 dt + 8 (r / 4) + 4 h + r % 4
-                *reinterpret_cast<uint2*>(yr + 32 * dt + 8 * r4 + 4 * h) = v;
+                    for (int r4 = 0; r4 < 4; ++r4) {
+                        const f32x4 b = *reinterpret_cast<const f32x4*>(xo + ((dt * 4 + r4) * 64 + lane) * 4);
+                        uint2 v;
+                        v.x = pack2h(o[dt][4 * r4] * f0 + b[0] * f1, o[dt][4 * r4 + 1] * f0 + b[1] * f1);
+                        v.y = pack2h(o[dt][4 * r4 + 2] * f0 + b[2] * f1, o[dt][4 * r4 + 3] * f0 + b[3] * f1);
+                        bad |= f16_bad2(v.x) | f16_bad2(v.y);
+                        // register r of tile dt: dim 32 dt + 8 (r / 4) + 4 h + r % 4
+                        *reinterpret_cast<uint2*>(yr + 32 * dt + 8 * r4 + 4 * h) = v;
+                    }
+                f16_note(bad, kF16Attn);
             }
-        f16_note(bad, kF16Attn);
+        } else {
+            // this part of a split tile: waves 0 and 1 fold the key halves into (O^T, m, l) of their head
+            if (kh == 0) {
+                const float m1 = xo[4096 + lane], l1 = xo[4160 + lane];
+                const float M = fmaxf(m_run, m1);
+                const float Mc = M == -INFINITY ? 0.f : M * scale_log2;
+                const float e0 = __builtin_amdgcn_exp2f(m_run * scale_log2 - Mc);
+                const float e1 = __builtin_amdgcn_exp2f(m1 * scale_log2 - Mc);
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+                        const f32x4 b = *reinterpret_cast<const f32x4*>(xo + ((dt * 4 + r4) * 64 + lane) * 4);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[dt][4 * r4 + e] = o[dt][4 * r4 + e] * e0 + b[e] * e1;
+                    }
+                l_run = l_run * e0 + l1 * e1;
+                m_run = M;
+            }
+            const int pid = kvhead * npairs + pair;
+            uint32_t* ctr = ws + pid;
+            float* slots = reinterpret_cast<float*>(ws + ws_ctr_words) + size_t(pid) * 2 * kAttnSlotWords;
+            float* mine = slots + role * kAttnSlotWords + cg * 4096;
+            const float* other = slots + (1 - role) * kAttnSlotWords + cg * 4096;
+            float* mine_ml = slots + role * kAttnSlotWords + 8192 + cg * 128;
+            const float* other_ml = slots + (1 - role) * kAttnSlotWords + 8192 + cg * 128;
+            if (t == 0) s_flag = int(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            lds_barrier();
+            int arrived = s_flag;
+            if (!arrived) {
+                // store this part (device-scope stores: the other part may run on another XCD), wait until they are
+                // performed, then count this part in
+                if (kh == 0) {
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                        for (int r4 = 0; r4 < 4; ++r4) {
+                            uint64_t* d = reinterpret_cast<uint64_t*>(mine + ((dt * 4 + r4) * 64 + lane) * 4);
+                            __hip_atomic_store(d, uint64_t(__float_as_uint(o[dt][4 * r4])) |
+                                                      (uint64_t(__float_as_uint(o[dt][4 * r4 + 1])) << 32),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            __hip_atomic_store(d + 1, uint64_t(__float_as_uint(o[dt][4 * r4 + 2])) |
+                                                          (uint64_t(__float_as_uint(o[dt][4 * r4 + 3])) << 32),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                    __hip_atomic_store(reinterpret_cast<uint32_t*>(mine_ml) + lane, __float_as_uint(m_run),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(reinterpret_cast<uint32_t*>(mine_ml) + 64 + lane, __float_as_uint(l_run),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this wave's stores are performed
+                lds_barrier();
+                if (t == 0)
+                    s_flag = int(__hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                lds_barrier();
+                arrived = s_flag;
+            }
+            if (arrived) {
+                // the other part is stored: merge in X, Y order and write the rows
+                if (kh == 0 && row < T) {
+                    float Ob[64];
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                        for (int r4 = 0; r4 < 4; ++r4) {
+                            const uint64_t* sp = reinterpret_cast<const uint64_t*>(
+                                other + ((dt * 4 + r4) * 64 + lane) * 4);
+                            const uint64_t v0 = __hip_atomic_load(sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            const uint64_t v1 = __hip_atomic_load(sp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            Ob[(dt * 4 + r4) * 4 + 0] = __uint_as_float(uint32_t(v0));
+                            Ob[(dt * 4 + r4) * 4 + 1] = __uint_as_float(uint32_t(v0 >> 32));
+                            Ob[(dt * 4 + r4) * 4 + 2] = __uint_as_float(uint32_t(v1));
+                            Ob[(dt * 4 + r4) * 4 + 3] = __uint_as_float(uint32_t(v1 >> 32));
+                        }
+                    const float mo = __uint_as_float(__hip_atomic_load(
+                        reinterpret_cast<const uint32_t*>(other_ml) + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                    const float lo = __uint_as_float(__hip_atomic_load(
+                        reinterpret_cast<const uint32_t*>(other_ml) + 64 + lane, __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT));
+                    // (mx, lx) of part X and (my, ly) of part Y
+                    const float mx = role == 0 ? m_run : mo, lx = role == 0 ? l_run : lo;
+                    const float my = role == 0 ? mo : m_run, ly = role == 0 ? lo : l_run;
+                    const float M = fmaxf(mx, my);
+                    const float Mc = M == -INFINITY ? 0.f : M * scale_log2;
+                    const float ex = __builtin_amdgcn_exp2f(mx * scale_log2 - Mc);
+                    const float ey = __builtin_amdgcn_exp2f(my * scale_log2 - Mc);
+                    const float inv = 1.0f / (lx * ex + ly * ey);
+                    const float fx = ex * inv, fy = ey * inv;
+                    uint32_t bad = 0;
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                        for (int r4 = 0; r4 < 4; ++r4) {
+                            float vv[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const float om = o[dt][4 * r4 + e], ob = Ob[(dt * 4 + r4) * 4 + e];
+                                vv[e] = role == 0 ? om * fx + ob * fy : ob * fx + om * fy;
+                            }
+                            uint2 v;
+                            v.x = pack2h(vv[0], vv[1]);
+                            v.y = pack2h(vv[2], vv[3]);
+                            bad |= f16_bad2(v.x) | f16_bad2(v.y);
+                            *reinterpret_cast<uint2*>(yr + 32 * dt + 8 * r4 + 4 * h) = v;
+                        }
+                    f16_note(bad, kF16Attn);
+                }
+                if (t == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        lds_barrier();  // the next item's stores reuse the LDS of this one's merge
     }
 }
 
@@ -1781,13 +1992,13 @@ static void l_gemm_qkv(const PreparedDispatch& pd, void* const* p, hipStream_t s
         hipLaunchKernelGGL((k_gemm<EPI_QKV, 128, false>), grid, dim3(256), 0, s, a);
 }
 
-// 16 attention_prefill_f16: q, k_cache, v_cache, y, rows, past, q_heads, kv_heads, max_pos, scale
+// 16 attention_prefill_f16: q, k_cache, v_cache, y, workspace, rows, past, q_heads, kv_heads, max_pos, scale
 static void l_attn_prefill(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    const int T = int(w[5]);
-    hipLaunchKernelGGL(k_attn_prefill, dim3(uint32_t((T + kAttnRows - 1) / kAttnRows), w[8]), dim3(256), 0, s, (const uint16_t*)p[0],
-                       (const uint16_t*)p[1], (const uint16_t*)p[2], (uint16_t*)p[3], T, int(w[6]), int(w[7]),
-                       int(w[9]), f32_of(w[10]) * kLog2e);
+    const int T = int(w[6]);
+    hipLaunchKernelGGL(k_attn_prefill, dim3(uint32_t((T + kAttnRows - 1) / kAttnRows), w[9]), dim3(256), 0, s,
+                       (const uint16_t*)p[0], (const uint16_t*)p[1], (const uint16_t*)p[2], (uint16_t*)p[3],
+                       (uint32_t*)p[4], T, int(w[7]), int(w[8]), int(w[10]), f32_of(w[11]) * kLog2e);
 }
 
 // Residual GEMMs with few 128 x 128 tiles (o_proj and down_proj have N = hidden) use 64-wide column tiles so the
@@ -2187,20 +2398,22 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 7, kvh * mp * 128, "gemm_qkv_rope", "k_cache");
                      need(c, 8, kvh * mp * 128, "gemm_qkv_rope", "v_cache");
                  }});
-    // 16 attention_prefill_f16: q, k_cache, v_cache, y, rows, past, q_heads, kv_heads, max_pos, scale
+    // 16 attention_prefill_f16: q, k_cache, v_cache, y, workspace, rows, past, q_heads, kv_heads, max_pos, scale
     c.push_back({"attention_prefill_f16", "fast", {256, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + kAttnRows - 1) / kAttnRows, w[8], 1}; },
+                 [](const uint32_t* w) { return Grid3{(int64_t(w[6]) + kAttnRows - 1) / kAttnRows, w[9], 1}; },
                  {TOK_R("q", DT(F16)), TOK_R("k_cache", DT(F16)), TOK_R("v_cache", DT(F16)), TOK_W("y", DT(F16)),
-                  U32F("rows"), U32F("past"), U32F("q_heads"), U32F("kv_heads"), U32F("max_pos"), F32F("scale")},
+                  TOK_RW("workspace", DT(U32)), U32F("rows"), U32F("past"), U32F("q_heads"), U32F("kv_heads"),
+                  U32F("max_pos"), F32F("scale")},
                  [](const uint32_t* w, const uint32_t* c) {
-                     const int64_t rows = w[5], past = w[6], qh = w[7], kvh = w[8], mp = w[9];
-                     need_group2("attention_prefill_f16", w[7], w[8]);
-                     need_max_pos("attention_prefill_f16", w[9]);
+                     const int64_t rows = w[6], past = w[7], qh = w[8], kvh = w[9], mp = w[10];
+                     need_group2("attention_prefill_f16", w[8], w[9]);
+                     need_max_pos("attention_prefill_f16", w[10]);
                      if (past + rows > mp) contract_fail("attention_prefill_f16: positions past max_pos");
                      need(c, 0, rows * qh * 128, "attention_prefill_f16", "q");
                      need(c, 1, kvh * mp * 128, "attention_prefill_f16", "k_cache");
                      need(c, 2, kvh * mp * 128, "attention_prefill_f16", "v_cache");
                      need(c, 3, rows * qh * 128, "attention_prefill_f16", "y");
+                     need(c, 4, attn_prefill::workspace_words(rows, kvh), "attention_prefill_f16", "workspace");
                  }});
     // 17 gemm_residual: a, w, x, m, n, k
     c.push_back({"gemm_residual", "fast", {256, 1, 1}, false,

@@ -2,6 +2,7 @@
 #include "qwen_exec.hpp"
 #include "safetensors.hpp"
 
+#include "attn_prefill.hpp"
 #include "persist.hpp"
 
 #include <omp.h>
@@ -323,6 +324,8 @@ void QwenExec::plan() {
         add("o", Activations, F16, {MT, QC});
         add("a", Activations, F16, {MT, I});
         add("resid.partials", Scratch, F32, {2 * MT, H});  // the k-split partials of the prefill residual GEMMs
+        // the prefill attention's split-tile partials and counters (zeroed below; every launch leaves them zero)
+        add("attn.ws", Scratch, U32, {uint32_t(attn_prefill::workspace_words(MT, KVH))});
         const uint32_t B = uint32_t(c.batch);
         add("dec.x", Activations, F32, {B, H});
         add("dec.qkv", Scratch, F32, {B, QC + 2 * KC});
@@ -399,6 +402,10 @@ void QwenExec::plan() {
     if (persist_) {  // epoch 0, no abort, every entry untagged
         std::vector<uint8_t> zero(dev_.table().row(token("dec.exchange")).extent_bytes(), 0);
         upload_tensor("dec.exchange", zero.data(), zero.size());
+    }
+    if (fast) {
+        std::vector<uint8_t> zero(dev_.table().row(token("attn.ws")).extent_bytes(), 0);
+        upload_tensor("attn.ws", zero.data(), zero.size());
     }
     for (int i = 0; i < c.layers; ++i)
         for (int k = 0; k < 11; ++k) weight_names_.push_back(lname(i, kLayerWeights[k]));
@@ -715,8 +722,9 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
         dispatch(l, "gemm_qkv_rope", {tk("h"), tk(p + "qkv_proj.f16"), w(5), w(6), tk("rope.cos"), tk("rope.sin"),
                                       tk("q"), tk(p + "k_cache" + sq), tk(p + "v_cache" + sq), U, H,
                                       uint32_t(c.heads), uint32_t(c.kv_heads), uint32_t(pos0), MP, eps});
-        dispatch(l, "attention_prefill_f16", {tk("q"), tk(p + "k_cache" + sq), tk(p + "v_cache" + sq), tk("o"), U,
-                                              uint32_t(pos0), uint32_t(c.heads), uint32_t(c.kv_heads), MP, scale});
+        dispatch(l, "attention_prefill_f16", {tk("q"), tk(p + "k_cache" + sq), tk(p + "v_cache" + sq), tk("o"),
+                                              tk("attn.ws"), U, uint32_t(pos0), uint32_t(c.heads),
+                                              uint32_t(c.kv_heads), MP, scale});
         residual_norm("o", p + "o_proj.f16", QC, w(7));
         dispatch(l, "gemm_swiglu", {tk("h"), tk(p + "gate_up_proj.f16"), tk("a"), U, I, H});
         // the next layer's input norm (after the last layer: the final norm, which the lm_head pass below recomputes

@@ -152,6 +152,14 @@ class ArgBlock:
         return self.words[i]
 
 
+def attention_prefill_workspace_words(rows: int, kv_heads: int) -> int:
+    """u32 words of attention_prefill_f16's workspace (rosylnalive_amd/csrc/attn_prefill.hpp): a counter per
+    (KV head, pair of 32-row tiles), padded up to a whole nonzero number of 64-word lines, then two partials of 8448
+    words per pair. Its counters must be zero before the first launch; every launch leaves them zero."""
+    pairs = ((rows + 31) // 32) // 2
+    return (kv_heads * pairs // 64 + 1) * 64 + kv_heads * pairs * 2 * 8448
+
+
 def grid_physical(linear: bool, x: int, y: int, z: int) -> Tuple[int, int, int]:
     out = u32s([0, 0, 0])
     check(lib().lrm_grid_physical(int(linear), x, y, z, out))

@@ -23,7 +23,7 @@ import pytest
 
 from gpu_session import POISON_F32, Session
 from oracle import cpuref, metrics
-from rosylnalive_amd.gpu_core import DType, TensorFlags
+from rosylnalive_amd.gpu_core import DType, TensorFlags, attention_prefill_workspace_words
 from rosylnalive_amd.qwen import inv_freq_bits
 
 pytestmark = pytest.mark.gpu
@@ -211,12 +211,13 @@ def test_attention_prefill_f16_adversarial(name, gen, T, past):
     vc = np.full((8, 128, mp), 0x7E00, np.uint16)
     kc[:, :keys] = kb.reshape(keys, 8, 128).transpose(1, 0, 2)
     vc[:, :, :keys] = vb.reshape(keys, 8, 128).transpose(1, 2, 0)
+    nws = attention_prefill_workspace_words(T, 8)
     s = Session({"q": (F16, qb.shape, 0, qb), "k": (F16, kc.shape, 0, kc), "v": (F16, vc.shape, 0, vc),
-                 "y": (F16, qb.shape, 0, None)})
+                 "y": (F16, qb.shape, 0, None), "ws": (U32, (nws,), 0, np.zeros(nws, np.uint32))})
     try:
         scale = float(cpuref.attention_scale(128, np.float32))
-        y = _hw(s.run("attention_prefill_f16", ["y"], q="q", k_cache="k", v_cache="v", y="y", rows=T, past=past,
-                      q_heads=16, kv_heads=8, max_pos=mp, scale=scale)["y"])
+        y = _hw(s.run("attention_prefill_f16", ["y"], q="q", k_cache="k", v_cache="v", y="y", workspace="ws",
+                      rows=T, past=past, q_heads=16, kv_heads=8, max_pos=mp, scale=scale)["y"])
         ref = cpuref.attention(_hw(qb).astype(np.float64), _hw(kb), _hw(vb), 16, 8, 128, past, scale)
         assert np.isfinite(y).all()
         err, rel = metrics.max_abs(y, ref), metrics.rel_l2(y, ref)

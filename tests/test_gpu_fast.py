@@ -8,7 +8,7 @@ import pytest
 
 from gpu_session import POISON_16, Session, written_everywhere
 from oracle import cpuref, metrics
-from rosylnalive_amd.gpu_core import DType, TensorFlags
+from rosylnalive_amd.gpu_core import DType, TensorFlags, attention_prefill_workspace_words
 from rosylnalive_amd.qwen import inv_freq_bits, synthetic_normal_f32
 
 pytestmark = pytest.mark.gpu
@@ -201,12 +201,15 @@ def test_attention_prefill_f16(T, past):
     max_pos = ((past + T + 63) // 64) * 64 + 64
     qb, kb, vb = _qkv_inputs(T, past, max_pos, seed=T + past)
     kc, vc = _caches(kb, vb, max_pos, fill=0x7E00)  # NaN past the context: the kernel must never use it
+    nws = attention_prefill_workspace_words(T, 8)
     s = Session({"q": (F16, qb.shape, 0, qb), "k": (F16, kc.shape, 0, kc), "v": (F16, vc.shape, 0, vc),
-                 "y": (F16, qb.shape, 0, None)})
+                 "y": (F16, qb.shape, 0, None), "ws": (U32, (nws,), 0, np.zeros(nws, np.uint32))})
     try:
         scale = float(cpuref.attention_scale(128, np.float32))
-        y = hwiden(s.run("attention_prefill_f16", ["y"], q="q", k_cache="k", v_cache="v", y="y", rows=T, past=past,
-                         q_heads=16, kv_heads=8, max_pos=max_pos, scale=scale)["y"])
+        y = hwiden(s.run("attention_prefill_f16", ["y"], q="q", k_cache="k", v_cache="v", y="y", workspace="ws",
+                         rows=T, past=past, q_heads=16, kv_heads=8, max_pos=max_pos, scale=scale)["y"])
+        # every split tile was merged once per launch: the counters are back at zero
+        assert not s.read("ws")[: (8 * (((T + 31) // 32) // 2) // 64 + 1) * 64].any()
         qf, kf, vf = hwiden(qb), hwiden(kb), hwiden(vb)
         ref = cpuref.attention(qf.astype(np.float64), kf, vf, 16, 8, 128, past, float(scale))
         err, rel = metrics.max_abs(y, ref), metrics.rel_l2(y, ref)
