@@ -9,12 +9,14 @@ namespace attn_prefill {
 
 constexpr int kRows = 32;                   // query rows of a tile
 constexpr int kSlotWords = 8192 + 256;      // one partial of a split tile: O^T (2 heads x 64 lanes x 64), then m, l
+// One record of u32 words per (KV head, tile pair): the pair's counter (padded to 256 bytes), then the partials of
+// its two parts. Record p sits at p * kRecordWords whatever the row count, so launches of different lengths share
+// one buffer: counters are never overwritten by partials. The counters must be zero before the first launch; every
+// launch leaves them zero.
+constexpr int kRecordWords = 64 + 2 * kSlotWords;
 constexpr int64_t pairs(int64_t rows) { return ((rows + kRows - 1) / kRows) / 2; }
-// u32 words: one counter per (KV head, tile pair), padded up to a whole (nonzero) number of 256-byte lines, then
-// two partials per pair. The counters must be zero before the first launch; every launch leaves them zero.
-constexpr int64_t counter_words(int64_t rows, int64_t kv_heads) { return (kv_heads * pairs(rows) / 64 + 1) * 64; }
 constexpr int64_t workspace_words(int64_t rows, int64_t kv_heads) {
-    return counter_words(rows, kv_heads) + kv_heads * pairs(rows) * 2 * kSlotWords;
+    return (kv_heads * pairs(rows) > 0 ? kv_heads * pairs(rows) : 1) * kRecordWords;
 }
 
 }  // namespace attn_prefill

@@ -679,12 +679,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 //
 // Causal balance: tile i needs about i / 2 key blocks, and a workgroup alone on its CU runs its blocks more slowly
 // than two sharing one, so whole tiles would leave the longest tiles running alone at the end. Tiles pair up, short
-// tile s = p with long tile n - 1 - p, and the pair's blocks split over two workgroups: X runs the first `a` key
-// blocks of the long tile, then the whole short tile; Y runs the rest of the long tile. The two parts of the long
+// tile s = p with long tile n - 1 - p, and on grids of two workgroups per CU the pair's blocks split over two
+// workgroups: X runs the first `a` key blocks of the long tile, then the whole short tile; Y runs the rest of the
+// long tile. The two parts of the long
 // tile meet in the workspace: each part, when done, reads the pair's counter; if the other part is already there it
 // merges the other's partial (O^T, m, l) with its own and writes the rows, otherwise it stores its partial, then adds
 // to the counter, and merges if the other part arrived in between. The merge combines the parts in X, Y order
 // whichever workgroup runs it, so the result does not depend on timing; the merging workgroup resets the counter.
+// Pair p's counter and partials form record p of the workspace (attn_prefill.hpp).
 // Nothing waits for another workgroup. An odd tile count leaves the middle tile whole.
 constexpr int kAttnRows = attn_prefill::kRows;
 constexpr int kAttnSlotWords = attn_prefill::kSlotWords;
@@ -734,13 +736,14 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
         short_tile = pair;
         long_tile = ntile - 1 - pair;
         const int ns = attn_tile_blocks(short_tile, T, past), nl = attn_tile_blocks(long_tile, T, past);
-        // even halves, then two more blocks for X: X is dispatched first, so its waves win the issue arbitration
-        // while both run, and Y finishes alone at the end (T 2048: 16 / 17 blocks 36.3 us, 18 / 15 blocks 35.8 us)
+        // Only a grid of two workgroups per CU (MI355X: 256 CUs) splits: alone on its CU, X's second tile costs a
+        // whole second pipeline start (T 512, 128 workgroups: 11.7 us whole, 13.5 split). Even halves, then two more
+        // blocks for X: X is dispatched first, so its waves win the issue arbitration while both run, and Y finishes
+        // alone at the end (T 2048: 16 / 17 blocks 36.3 us, 18 / 15 blocks 35.8 us).
         const int even = (ns + nl) / 2 - ns;
-        split_a = even > 0 ? min(even + 2, nl - 1) : 0;
+        split_a = ntile * kvh >= 512 && even > 0 ? min(even + 2, nl - 1) : 0;
         if (u < npairs && split_a > 0) nitems = 2;
     }
-    const int ws_ctr_words = int(attn_prefill::counter_words(T, kvh));
 
     f16x8 qf[8];
     float m_run, l_run;
@@ -1014,8 +1017,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
                 m_run = M;
             }
             const int pid = kvhead * npairs + pair;
-            uint32_t* ctr = ws + pid;
-            float* slots = reinterpret_cast<float*>(ws + ws_ctr_words) + size_t(pid) * 2 * kAttnSlotWords;
+            uint32_t* ctr = ws + size_t(pid) * attn_prefill::kRecordWords;
+            float* slots = reinterpret_cast<float*>(ctr + 64);
             float* mine = slots + role * kAttnSlotWords + cg * 4096;
             const float* other = slots + (1 - role) * kAttnSlotWords + cg * 4096;
             float* mine_ml = slots + role * kAttnSlotWords + 8192 + cg * 128;

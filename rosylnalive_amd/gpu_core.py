@@ -152,12 +152,15 @@ class ArgBlock:
         return self.words[i]
 
 
+ATTN_PREFILL_RECORD_WORDS = 64 + 2 * 8448
+
+
 def attention_prefill_workspace_words(rows: int, kv_heads: int) -> int:
-    """u32 words of attention_prefill_f16's workspace (rosylnalive_amd/csrc/attn_prefill.hpp): a counter per
-    (KV head, pair of 32-row tiles), padded up to a whole nonzero number of 64-word lines, then two partials of 8448
-    words per pair. Its counters must be zero before the first launch; every launch leaves them zero."""
-    pairs = ((rows + 31) // 32) // 2
-    return (kv_heads * pairs // 64 + 1) * 64 + kv_heads * pairs * 2 * 8448
+    """u32 words of attention_prefill_f16's workspace (rosylnalive_amd/csrc/attn_prefill.hpp): one record per
+    (KV head, pair of 32-row tiles) = a counter padded to 64 words, then two partials of 8448 words, so launches of
+    any length share one buffer. The counters (word 0 of each record) must be zero before the first launch; every
+    launch leaves them zero."""
+    return max(1, kv_heads * (((rows + 31) // 32) // 2)) * ATTN_PREFILL_RECORD_WORDS
 
 
 def grid_physical(linear: bool, x: int, y: int, z: int) -> Tuple[int, int, int]:

@@ -198,11 +198,11 @@ FAST_CASES = [
 ]
 
 
-@pytest.mark.parametrize("T,past", [(96, 300), (1, 2000), (200, 0)])
+@pytest.mark.parametrize("T,past", [(96, 300), (1, 2000), (200, 0), (2048, 0)])
 @pytest.mark.parametrize("name,gen", FAST_CASES, ids=[c[0] for c in FAST_CASES])
 def test_attention_prefill_f16_adversarial(name, gen, T, past):
     """attention_prefill_f16 on fp16 q, K, V^T with the adversarial scores (head_dim 128, 16/8 heads); positions past
-    the context hold NaN."""
+    the context hold NaN. At T 2048 (512 workgroups) the long tiles run in two parts merged through the workspace."""
     keys, mp = past + T, ((past + T + 63) // 64 + 1) * 64
     q, k, v = gen(rng(f"fast.{name}.{T}.{past}"), 2048, 1024, T, keys)
     qb = _f16(q.reshape(T, 2048))

@@ -8,7 +8,8 @@ import pytest
 
 from gpu_session import POISON_16, Session, written_everywhere
 from oracle import cpuref, metrics
-from rosylnalive_amd.gpu_core import DType, TensorFlags, attention_prefill_workspace_words
+from rosylnalive_amd.gpu_core import (ATTN_PREFILL_RECORD_WORDS, DType, TensorFlags,
+                                      attention_prefill_workspace_words)
 from rosylnalive_amd.qwen import inv_freq_bits, synthetic_normal_f32
 
 pytestmark = pytest.mark.gpu
@@ -196,6 +197,34 @@ def _caches(kb, vb, max_pos, fill=0):
     return kc, vc
 
 
+def test_attention_prefill_f16_shared_workspace():
+    """Launches of different lengths on one workspace (a record per tile pair): 2048 rows (512 workgroups: the long
+    tiles split in two parts), then 512 (no split), then 2048 again, each against the oracle's attention, with the
+    counters back at zero after each."""
+    max_pos = 2112
+    qb, kb, vb = _qkv_inputs(2048, 0, max_pos, seed=77)
+    kc, vc = _caches(kb, vb, max_pos, fill=0x7E00)
+    nws = attention_prefill_workspace_words(2048, 8)
+    s = Session({"q": (F16, qb.shape, 0, qb), "k": (F16, kc.shape, 0, kc), "v": (F16, vc.shape, 0, vc),
+                 "y": (F16, qb.shape, 0, None), "ws": (U32, (nws,), 0, np.zeros(nws, np.uint32))})
+    try:
+        scale = float(cpuref.attention_scale(128, np.float32))
+        qf, kf, vf = hwiden(qb), hwiden(kb), hwiden(vb)
+        for T in (2048, 512, 2048):
+            cl = s.backend.begin()
+            cl.dispatch("attention_prefill_f16", s.fields("attention_prefill_f16", q="q", k_cache="k", v_cache="v",
+                                                          y="y", workspace="ws", rows=T, past=0, q_heads=16,
+                                                          kv_heads=8, max_pos=max_pos, scale=scale))
+            s.backend.wait(s.backend.submit(cl))
+            cl.release()
+            y = hwiden(s.read("y")[:T])
+            ref = cpuref.attention(qf[:T].astype(np.float64), kf[:T], vf[:T], 16, 8, 128, 0, float(scale))
+            assert metrics.max_abs(y, ref) <= 1e-2 and metrics.rel_l2(y, ref) <= 5e-3, T
+            assert not s.read("ws")[::ATTN_PREFILL_RECORD_WORDS].any()
+    finally:
+        s.close()
+
+
 @pytest.mark.parametrize("T,past", [(64, 0), (100, 0), (2048, 0), (77, 300), (1, 0), (33, 31), (512, 2048)])
 def test_attention_prefill_f16(T, past):
     max_pos = ((past + T + 63) // 64) * 64 + 64
@@ -208,8 +237,8 @@ def test_attention_prefill_f16(T, past):
         scale = float(cpuref.attention_scale(128, np.float32))
         y = hwiden(s.run("attention_prefill_f16", ["y"], q="q", k_cache="k", v_cache="v", y="y", workspace="ws",
                          rows=T, past=past, q_heads=16, kv_heads=8, max_pos=max_pos, scale=scale)["y"])
-        # every split tile was merged once per launch: the counters are back at zero
-        assert not s.read("ws")[: (8 * (((T + 31) // 32) // 2) // 64 + 1) * 64].any()
+        # every split tile was merged once per launch: the counters (word 0 of each record) are back at zero
+        assert not s.read("ws")[::ATTN_PREFILL_RECORD_WORDS].any()
         qf, kf, vf = hwiden(qb), hwiden(kb), hwiden(vb)
         ref = cpuref.attention(qf.astype(np.float64), kf, vf, 16, 8, 128, past, float(scale))
         err, rel = metrics.max_abs(y, ref), metrics.rel_l2(y, ref)
