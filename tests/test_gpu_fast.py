@@ -197,6 +197,36 @@ def _caches(kb, vb, max_pos, fill=0):
     return kc, vc
 
 
+def test_attention_prefill_f16_split_across_xcds():
+    """8 query / 4 KV heads at T 4160: 130 tiles x 4 KV heads = 520 workgroups, so the long tiles split, and the two
+    parts of a pair are 65 x 4 = 260 workgroups apart: on the 8 XCDs of an MI355X (workgroup L on XCD L % 8) they run
+    on different XCDs, so their partials meet only through device-scope memory. Against the oracle's attention, with
+    the counters back at zero."""
+    T, qh, kvh, max_pos = 4160, 8, 4, 4224
+    r = np.random.default_rng(4160)
+    qb = f16(r.standard_normal((T, qh * 128)))
+    kb = f16(r.standard_normal((T, kvh * 128)))
+    vb = f16(r.standard_normal((T, kvh * 128)))
+    kc = np.full((kvh, max_pos, 128), 0x7E00, np.uint16)
+    vc = np.full((kvh, 128, max_pos), 0x7E00, np.uint16)
+    kc[:, :T, :] = kb.reshape(T, kvh, 128).transpose(1, 0, 2)
+    vc[:, :, :T] = vb.reshape(T, kvh, 128).transpose(1, 2, 0)
+    nws = attention_prefill_workspace_words(T, kvh)
+    s = Session({"q": (F16, qb.shape, 0, qb), "k": (F16, kc.shape, 0, kc), "v": (F16, vc.shape, 0, vc),
+                 "y": (F16, qb.shape, 0, None), "ws": (U32, (nws,), 0, np.zeros(nws, np.uint32))})
+    try:
+        scale = float(cpuref.attention_scale(128, np.float32))
+        y = hwiden(s.run("attention_prefill_f16", ["y"], q="q", k_cache="k", v_cache="v", y="y", workspace="ws",
+                         rows=T, past=0, q_heads=qh, kv_heads=kvh, max_pos=max_pos, scale=scale)["y"])
+        assert not s.read("ws")[::ATTN_PREFILL_RECORD_WORDS].any()
+        ref = cpuref.attention(hwiden(qb).astype(np.float64), hwiden(kb), hwiden(vb), qh, kvh, 128, 0, scale)
+        err, rel = metrics.max_abs(y, ref), metrics.rel_l2(y, ref)
+        print(f"attention prefill 8/4 heads T={T}: max-abs {err:.3g}, relL2 {rel:.3g}", flush=True)
+        assert err <= 1e-2 and rel <= 5e-3
+    finally:
+        s.close()
+
+
 def test_attention_prefill_f16_shared_workspace():
     """Launches of different lengths on one workspace (a record per tile pair): 2048 rows (512 workgroups: the long
     tiles split in two parts), then 512 (no split), then 2048 again, each against the oracle's attention, with the
