@@ -205,8 +205,10 @@ struct GemmArgs {
 // tiles go through two register sets into two padded LDS buffers with every load two k steps ahead.
 template <int EPI, int BN, bool DMA>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
-    static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID || EPI == EPI_PART)),
-                  "SwiGLU and QKV pair 128 columns");
+    static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID || EPI == EPI_PART)) ||
+                      (BN == 192 && EPI == EPI_SWIGLU && DMA),
+                  "QKV takes 128 columns, SwiGLU 128 or 192 (64 or 96 gate / up pairs)");
+    constexpr int PAIR = BN / 2;  // SWIGLU: gate / up pairs per tile
     // the k range of this block: all of k, or split z of a PART launch (A and W then start kz columns in)
     const int kz = EPI == EPI_PART ? int(blockIdx.z) * p.ksplit : 0;
     const int KE = EPI == EPI_PART ? p.ksplit : p.K;
@@ -262,8 +264,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             const int r = 8 * (4 * i + w) + (lane >> 3), c = (lane & 7) ^ (r & 7);
             int n;
             if (EPI == EPI_SWIGLU) {
-                const int j = min(tx * 64 + (r & 63), p.inter - 1);
-                n = r < 64 ? j : p.inter + j;
+                const int j = min(tx * PAIR + (r < PAIR ? r : r - PAIR), p.inter - 1);
+                n = r < PAIR ? j : p.inter + j;
             } else {
                 n = min(n0 + r, p.N - 1);
             }
@@ -332,8 +334,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
             int n;
             if (EPI == EPI_SWIGLU) {
-                const int j = min(tx * 64 + (r & 63), p.inter - 1);
-                n = r < 64 ? j : p.inter + j;
+                const int j = min(tx * PAIR + (r < PAIR ? r : r - PAIR), p.inter - 1);
+                n = r < PAIR ? j : p.inter + j;
             } else {
                 n = min(n0 + r, p.N - 1);
             }
@@ -551,53 +553,54 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         }
     }
 
-    // SWIGLU and the V heads of QKV pair column c (wave wn = 0) with column c + 64 (wave wn = 1, same lane and tile
+    // SWIGLU and the V heads of QKV pair column c (wave wn = 0) with column c + PAIR (wave wn = 1, same lane and tile
     // index): the second half goes through LDS to the first.
-    float* x32 = reinterpret_cast<float*>(lds);  // 2 (wm) x 64 values x 64 lanes = 32 KiB
+    float* x32 = reinterpret_cast<float*>(lds);  // 2 (wm) x 4 JT x 4 values x 64 lanes: 32 KiB (JT 4), 48 KiB (JT 6)
     if (wn == 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < JT; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) x32[((wm * 16 + i * 4 + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+                for (int r = 0; r < 4; ++r) x32[((wm * 4 * JT + i * JT + j) * 4 + r) * 64 + lane] = acc[i][j][r];
     }
     __syncthreads();
     const int head = tx;  // QKV: a V head (the q and k heads returned above)
     // the partner half of row tile i, read back from LDS
-    auto load_hi = [&](int i, float (&hi)[4][4]) {
+    auto load_hi = [&](int i, float (&hi)[JT][4]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < JT; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) hi[j][r] = x32[((wm * 16 + i * 4 + j) * 4 + r) * 64 + lane];
+            for (int r = 0; r < 4; ++r) hi[j][r] = x32[((wm * 4 * JT + i * JT + j) * 4 + r) * 64 + lane];
     };
 
     if (EPI == EPI_SWIGLU) {
-        // a[m, j0 + c] = silu(gate) * up, silu(g) = g / (1 + exp(-g)), into an fp16 tile in LDS after the 32 KiB of x32
-        // (rows of 64 columns padded to 72), then out as 16-byte row chunks by all four waves
-        uint16_t* As = lds + 16384;
+        // a[m, j0 + c] = silu(gate) * up, silu(g) = g / (1 + exp(-g)), into an fp16 tile in LDS after x32 (rows of PAIR
+        // columns padded by 8), then out as 16-byte row chunks by all four waves
+        constexpr int AR = PAIR + 8, CH = PAIR / 8;  // LDS row stride (halves), 16-byte chunks per row
+        uint16_t* As = lds + 2 * 4 * 4 * JT * 64 * 2;
         if (wn == 0) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float hi[4][4];
+                float hi[JT][4];
                 load_hi(i, hi);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < JT; ++j)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float gv = acc[i][j][r];
                         const float sg = gv / (1.0f + __expf(-gv));
-                        As[(wm * 64 + i * 16 + 4 * g + r) * 72 + j * 16 + c16] = f2h(sg * hi[j][r]);
+                        As[(wm * 64 + i * 16 + 4 * g + r) * AR + j * 16 + c16] = f2h(sg * hi[j][r]);
                     }
             }
         }
         __syncthreads();
         uint32_t bad = 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int q = t + 256 * k, row = q >> 3, ch = q & 7, m = m0 + row, col = tx * 64 + ch * 8;
+        for (int k = 0; k < CH / 2; ++k) {  // 128 rows x CH chunks = 256 (CH / 2) chunks
+            const int q = t + 256 * k, row = q / CH, ch = q % CH, m = m0 + row, col = tx * PAIR + ch * 8;
             if (m >= p.M || col >= p.inter) continue;
-            const u32x4 v = *reinterpret_cast<const u32x4*>(As + row * 72 + ch * 8);
+            const u32x4 v = *reinterpret_cast<const u32x4*>(As + row * AR + ch * 8);
             uint16_t* dst = p.y16 + size_t(m) * p.inter + col;
             if (col + 8 <= p.inter && (p.inter & 7) == 0) {
                 bad |= f16_bad8(v);
@@ -621,10 +624,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         if (wn == 0) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float hi[4][4];
+                float hi[JT][4];
                 load_hi(i, hi);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < JT; ++j) {
                     uint16_t* vr = Vs + (j * 16 + c16) * 136 + wm * 64 + i * 16 + 4 * g;
                     *reinterpret_cast<uint2*>(vr) =
                         make_uint2(pack2h(acc[i][j][0], acc[i][j][1]), pack2h(acc[i][j][2], acc[i][j][3]));
@@ -2022,14 +2025,25 @@ static void l_gemm_resid(const PreparedDispatch& pd, void* const* p, hipStream_t
                            s, a);
 }
 
+// gemm_swiglu's grid: 96 gate / up pairs per tile where that makes whole rounds of 512 tiles for the direct-to-LDS
+// loop (Qwen3-0.6B at 2048 rows: 32 x 16 tiles, where 64 pairs give 768 tiles, one and a half rounds), else 64
+static bool swiglu_wide(uint32_t m, uint32_t inter) {
+    return inter % 96 == 0 && (uint64_t(inter / 96) * ((m + GBM - 1) / GBM)) % 512 == 0;
+}
+static dim3 swiglu_grid(uint32_t m, uint32_t inter) {
+    return dim3(swiglu_wide(m, inter) ? inter / 96 : (inter + 63) / 64, (m + GBM - 1) / GBM);
+}
+
 // 18 gemm_swiglu: a, w (2 inter rows), y, m, inter, k
 static void l_gemm_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     GemmArgs a = gemm_base(p, w[4], 2 * w[5], w[6]);
     a.y16 = (uint16_t*)p[2];
     a.inter = int(w[5]);
-    const dim3 grid((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM);
-    if (two_per_cu(grid))
+    const dim3 grid = swiglu_grid(w[4], w[5]);
+    if (swiglu_wide(w[4], w[5]))
+        hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 192, true>), grid, dim3(256), 0, s, a);
+    else if (two_per_cu(grid))
         hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 128, true>), grid, dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 128, false>), grid, dim3(256), 0, s, a);
@@ -2433,7 +2447,10 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 18 gemm_swiglu: a, w, y, m, inter, k
     c.push_back({"gemm_swiglu", "fast", {256, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 63) / 64, (int64_t(w[4]) + 127) / 128, 1}; },
+                 [](const uint32_t* w) {
+                     const dim3 g = swiglu_grid(w[4], w[5]);
+                     return Grid3{g.x, g.y, 1};
+                 },
                  {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F16)), U32F("m"), U32F("inter"), U32F("k")},
                  [](const uint32_t* w, const uint32_t* c) {
                      if (w[6] % 64 || w[6] < 64) contract_fail("gemm_swiglu: k must be a positive multiple of 64");
