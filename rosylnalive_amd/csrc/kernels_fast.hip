@@ -943,7 +943,11 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
 
-        fetch(A0{}, 0);
+        {  // group 0 is K(0) alone (its V^T(-1) does not exist)
+            const int kbk = kb0 * 64;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rk[0][i] = __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, koff[i], kbk * 256, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);  // group 0 issues before group 1, so the first wait can be partial
         fetch(A1{}, 1);
         store_k(A0{}, A0{});     // K(0)
