@@ -205,9 +205,9 @@ struct GemmArgs {
 // tiles go through two register sets into two padded LDS buffers with every load two k steps ahead.
 template <int EPI, int BN, bool DMA>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
-    static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID || EPI == EPI_PART || EPI == EPI_SWIGLU)) ||
+    static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID || EPI == EPI_PART)) ||
                       (BN == 192 && EPI == EPI_SWIGLU && DMA),
-                  "QKV takes 128 columns, SwiGLU 64, 128 or 192 (32, 64 or 96 gate / up pairs)");
+                  "QKV takes 128 columns, SwiGLU 128 or 192 (64 or 96 gate / up pairs)");
     constexpr int PAIR = BN / 2;  // SWIGLU: gate / up pairs per tile
     // the k range of this block: all of k, or split z of a PART launch (A and W then start kz columns in)
     const int kz = EPI == EPI_PART ? int(blockIdx.z) * p.ksplit : 0;
@@ -2030,12 +2030,10 @@ static void l_gemm_resid(const PreparedDispatch& pd, void* const* p, hipStream_t
 }
 
 // gemm_swiglu's gate / up pairs per tile: 96 where that makes whole rounds of 512 tiles for the direct-to-LDS loop
-// (Qwen3-0.6B at 2048 rows: 32 x 16 tiles, where 64 pairs give 768 tiles, one and a half rounds); 32 where 64 would
-// leave CUs without a tile (at 512 rows: 96 x 4 tiles instead of 48 x 4); else 64
+// (Qwen3-0.6B at 2048 rows: 32 x 16 tiles, where 64 pairs give 768 tiles, one and a half rounds); else 64
 static int swiglu_pairs(uint32_t m, uint32_t inter) {
     const uint64_t rows = (m + GBM - 1) / GBM;
     if (inter % 96 == 0 && (uint64_t(inter / 96) * rows) % 512 == 0) return 96;
-    if (uint64_t((inter + 63) / 64) * rows < 256) return 32;
     return 64;
 }
 static dim3 swiglu_grid(uint32_t m, uint32_t inter) {
@@ -2053,8 +2051,6 @@ static void l_gemm_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_
     const int pairs = swiglu_pairs(w[4], w[5]);
     if (pairs == 96)
         hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 192, true>), grid, dim3(256), 0, s, a);
-    else if (pairs == 32)
-        hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 64, false>), grid, dim3(256), 0, s, a);
     else if (two_per_cu(grid))
         hipLaunchKernelGGL((k_gemm<EPI_SWIGLU, 128, true>), grid, dim3(256), 0, s, a);
     else

@@ -122,9 +122,9 @@ def test_gemm_f32_large_grids(m, n, k):
 @pytest.mark.parametrize("m,inter,k", [(200, 192, 128), (512, 3072, 1024), (2048, 4096, 128), (2048, 3072, 1024),
                                        (2000, 3072, 256)])
 def test_gemm_swiglu(m, inter, k):
-    """SwiGLU epilogue on 32-pair tiles where 64 would leave CUs without a tile (200 rows: partial tiles; 512 rows:
-    96 x 4 tiles), on 64-pair tiles (2048 rows, 4096 pairs: 1024 tiles), and on the 96-pair tiles (3072 pairs: 32 x 16
-    = 512 tiles) of the 2048-token prefill, also with a partial last row tile."""
+    """SwiGLU epilogue on 64-pair tiles (200 rows: partial tiles; 512 rows: 48 x 4 tiles on the register loop; 2048
+    rows, 4096 pairs: 1024 tiles on the direct-to-LDS loop), and on the 96-pair tiles (3072 pairs: 32 x 16 = 512 tiles)
+    of the 2048-token prefill, also with a partial last row tile."""
     r = np.random.default_rng(3)
     a = f16(r.standard_normal((m, k)))
     w = f16(r.standard_normal((2 * inter, k)) * 0.1)
