@@ -33,9 +33,9 @@
 // Stages of layer l (Qwen3-0.6B: hidden 1024, 16/8 heads, intermediate 3072), workgroup b on XCD h, j = b / 8:
 //   A  q|k|v of KV head h = W . RMSNorm(x): 2 of the XCD's 512 rows per wave. Waits for x, i.e. for the previous
 //      layer's down_proj partial sums of all XCDs (all of x: the RMSNorm needs the whole row).
-//   B  attention: split j of KV head h takes keys [j KPS, (j + 1) KPS) (KPS a multiple of 64 chosen so 32 splits cover
-//      pos + 1 keys), both query heads, 64 keys at a time with an online softmax; the split holding pos also
-//      normalises, rotates and appends the new key and value. Writes (out[128], max, sum) per query head.
+//   B  attention: split j of KV head h takes keys [j KPS, (j + 1) KPS) (KPS a multiple of 64 chosen so at most 32
+//      splits cover pos + 1 keys), both query heads, 64 keys at a time with an online softmax; the split holding pos
+//      also normalises, rotates and appends the new key and value. Writes (out[128], max, sum) per query head.
 //   C  o_h = the combine of the splits (every workgroup of the XCD forms all 256 dims), then
 //      p1[h] = W_o[:, 256 h .. + 255] . o_h: 32 rows per workgroup.
 //   D  a_h = silu(W_g . r) * (W_u . r), r = RMSNorm(x + sum_h p1[h]): 12 of the XCD's 384 gate/up pairs.
@@ -454,7 +454,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     // attention split of this workgroup (stage B): fixed for the step
     const int hk = xcd, s = j;
     const int ntot = int(pos) + 1;
-    const int KPS = ((ntot + S - 1) / S + 63) / 64 * 64;
+    // keys per split: whole 64-key chunks covering pos + 1 keys in 32 splits, one chunk more where that would take
+    // more than 28 splits (stage C gathers the partial rows of up to 23 splits in one pass; a second pass over 29-32
+    // splits costs more than the longer chain of one more chunk: per token at contexts 2000 / 4000 / 5500, 479.8 /
+    // 520.7 / 550.6 us against 502.5 / 537.9 / 557.5; at 24-26 splits (contexts 1600, 3200, 4500) the extra chunk
+    // measured no better, 478.8 / 513.3 / 542.8 against 467.3 / 512.8 / 543.1)
+    int KPS = ((ntot + S - 1) / S + 63) / 64 * 64;
+    if ((ntot + KPS - 1) / KPS > 28) KPS += 64;
     const int S_used = (ntot + KPS - 1) / KPS;
     const bool attn = s < S_used;
     const bool has_pos = s == S_used - 1;  // the split of the last key, pos

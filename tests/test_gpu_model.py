@@ -266,8 +266,9 @@ def test_fast_decode_runs_the_persistent_step(fast_setup):
 
 def test_persistent_decode_step_matches_kernel_list():
     """decode_step_persistent against the per-stage kernel list on the same weights and caches: teacher-forced steps
-    at short context (one split) and over random caches at positions whose splits take 1, 2 and 3 chunks of 64 keys,
-    then 20 greedy steps. Layer 0's appended cache rows agree to one fp16 rounding (the same per-lane products, but the
+    at short context (one split) and over random caches at positions whose splits take 1, 2 and 3 chunks of 64 keys
+    (2047 and 3700: one chunk more than 32 splits need, to keep to 28 splits; 3000: 24 splits, gathered in two
+    passes), then 20 greedy steps. Layer 0's appended cache rows agree to one fp16 rounding (the same per-lane products, but the
     persistent step multiplies by the fp16 copies of the matrices, which differ from the bf16 weights only for weights
     under 2^-17 in magnitude); after it the residual rows differ by the order of a few partial sums, and so do the
     logits."""
@@ -308,8 +309,8 @@ def test_persistent_decode_step_matches_kernel_list():
             step(tok, prompt.size + i)
         for m in (mp, mk):
             m.fill_cache_random(5, 4320)
-        toks = synthetic_ids(11, "persist/long", 5, cfg.vocab)
-        for tok, pos in zip(toks, (63, 2047, 2048, 3000, 4319)):
+        toks = synthetic_ids(11, "persist/long", 6, cfg.vocab)
+        for tok, pos in zip(toks, (63, 2047, 2048, 3000, 3700, 4319)):
             step(tok, pos)
         print(f"persistent vs kernel-list decode: worst logits max-abs {worst:.3g}", flush=True)
         g = [m.greedy(prompt, 20) for m in (mp, mk)]
