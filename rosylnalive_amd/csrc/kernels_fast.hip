@@ -2712,9 +2712,10 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 2, sp * m * n, "gemm_residual_split", "partials");
                  }});
     // 40 residual_add_norm: x, partials, w, y, rows, cols, splits, eps. x += the partials in split order, then
-    // y = RMSNorm(x) in f16 (as rmsnorm_rows_f16)
+    // y = RMSNorm(x) in f16 (as rmsnorm_rows_f16). The catalog's block size is the four-row form's; up to 64 rows
+    // launch one 64-thread block per row
     c.push_back({"residual_add_norm", "fast", {256, 1, 1}, true,
-                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 3) / 4, 1, 1}; },
+                 [](const uint32_t* w) { return Grid3{w[5] <= 64 ? int64_t(w[5]) : (int64_t(w[5]) + 3) / 4, 1, 1}; },
                  {TOK_RW("x", DT(F32)), TOK_R("partials", DT(F32)), TOK_R("w", DT(BF16)), TOK_W("y", DT(F16)),
                   U32F("rows"), U32F("cols"), U32F("splits"), F32F("eps")},
                  [](const uint32_t* w, const uint32_t* c) {
