@@ -203,11 +203,13 @@ struct GemmArgs {
 // Two main loops, chosen by the launcher: DMA (a grid of at least two blocks per CU) moves tiles from memory
 // straight into two LDS stages, the two blocks on a CU hiding each other's load latency; otherwise (one block per CU)
 // tiles go through two register sets into two padded LDS buffers with every load two k steps ahead.
-template <int EPI, int BN, bool DMA>
+template <int EPI, int BN, bool DMA, int BM = GBM>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID || EPI == EPI_PART)) ||
                       (BN == 192 && EPI == EPI_SWIGLU && DMA),
                   "QKV takes 128 columns, SwiGLU 128 or 192 (64 or 96 gate / up pairs)");
+    static_assert(BM == GBM || (BM == 64 && EPI == EPI_QKV && !DMA), "64-row tiles: the q|k|v register loop only");
+    constexpr int MI = BM / 32;   // MFMA row tiles per wave: each wave owns BM / 2 rows
     constexpr int PAIR = BN / 2;  // SWIGLU: gate / up pairs per tile
     // the k range of this block: all of k, or split z of a PART launch (A and W then start kz columns in)
     const int kz = EPI == EPI_PART ? int(blockIdx.z) * p.ksplit : 0;
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     // both paths: unpadded LDS rows of GBK halves, the 16-byte chunks XOR-swizzled (row r, position q holds k chunk
     // q ^ (r % 8)), so a fragment read (16 rows, one chunk) spreads over the banks (padded 144-byte rows measured
     // 14 % of the register path's cycles stalled on bank conflicts)
-    constexpr int STAGE = (GBM + BN) * GBK;  // halves: the A tile then the W tile
+    constexpr int STAGE = (BM + BN) * GBK;  // halves: the A tile then the W tile
     // the two stages, or what the QKV epilogue needs after them (x32 32 KiB + the V^T tile 128 x 136 halves)
     constexpr int LDS_HALVES = EPI == EPI_QKV ? (2 * STAGE > 33792 ? 2 * STAGE : 33792) : 2 * STAGE;
     __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALVES];
@@ -237,12 +239,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         ty = sr * GM + within % rows;
         tx = within / rows;
     }
-    const int m0 = ty * GBM;
+    const int m0 = ty * BM;
     const int n0 = tx * BN;
 
-    f32x4 acc[4][JT];
+    f32x4 acc[MI][JT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < JT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (DMA) {
@@ -252,7 +254,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         // r, position q holds k chunk q ^ (r % 8), so a fragment read (16 rows, one chunk) spreads over the banks. Each wave
         // issues instructions i = 0, 1, ... for the 1 KiB blocks 4 i + w. A row past the matrix is clamped to its last row
         // (it only feeds outputs that are never stored); the k offset is a scalar.
-        constexpr int NA = GBM / 32, NB = BN / 32;  // load instructions per wave per stage
+        constexpr int NA = BM / 32, NB = BN / 32;  // load instructions per wave per stage
         int aoff[NA], boff[NB];
     #pragma unroll
         for (int i = 0; i < NA; ++i) {
@@ -278,20 +280,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     #pragma unroll
             for (int i = 0; i < NA; ++i) buffer_load_lds16(a_rsrc, st + (4 * i + w) * 512, aoff[i], k0 * 2);
     #pragma unroll
-            for (int i = 0; i < NB; ++i) buffer_load_lds16(w_rsrc, st + GBM * GBK + (4 * i + w) * 512, boff[i], k0 * 2);
+            for (int i = 0; i < NB; ++i) buffer_load_lds16(w_rsrc, st + BM * GBK + (4 * i + w) * 512, boff[i], k0 * 2);
         };
 
         // one k step of a stage: per 32-wide half, the A fragments (rows of this wave's 4 MFMA row tiles) and the W
         // fragments, read from their swizzled chunk, then the MFMAs
         auto compute = [&](int buf) __attribute__((always_inline)) {
             const uint16_t* As = lds + buf * STAGE;
-            const uint16_t* Bs = As + GBM * GBK;
+            const uint16_t* Bs = As + BM * GBK;
     #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                f16x8 af[4], bf[JT];
+                f16x8 af[MI], bf[JT];
     #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = wm * 64 + i * 16 + c16;
+                for (int i = 0; i < MI; ++i) {
+                    const int r = wm * (BM / 2) + i * 16 + c16;
                     af[i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + r * GBK + (((ks * 4 + g) ^ (r & 7)) * 8)));
                 }
     #pragma unroll
@@ -300,7 +302,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                     bf[j] = as_f16x8(*reinterpret_cast<const u32x4*>(Bs + r * GBK + (((ks * 4 + g) ^ (r & 7)) * 8)));
                 }
     #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < MI; ++i)
     #pragma unroll
                     for (int j = 0; j < JT; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
@@ -323,9 +325,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         // feeds output rows / columns that are never stored, and the loads stay unconditional, so the compiler can keep
         // several tiles in flight (a guarded load makes it wait for every outstanding load).
         constexpr int BCH = BN / 32;  // B chunks per thread
-        int aoff[4], boff[BCH];  // byte offsets: the loads are buffer loads with the k offset in a scalar register
+        int aoff[MI], boff[BCH];  // byte offsets: the loads are buffer loads with the k offset in a scalar register
     #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < MI; ++i) {
             const int c = t + 256 * i, r = c >> 3, kc = (c & 7) * 8;
             aoff[i] = (min(m0 + r, p.M - 1) * p.K + kc) * 2;
         }
@@ -346,20 +348,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         // Two register sets, two LDS buffers: tile j is loaded into set j % 2 at the top of iteration j - 2 and stored to
         // LDS buffer j % 2 at the end of iteration j - 1, so each load has two iterations of MFMAs to land. The loop is
         // unrolled by two so every register set is named at compile time.
-        u32x4 ra[2][4], rb[2][BCH];
+        u32x4 ra[2][MI], rb[2][BCH];
         auto gload = [&](auto set, int k0) __attribute__((always_inline)) {
             constexpr int S = decltype(set)::value;
     #pragma unroll
-            for (int i = 0; i < 4; ++i) ra[S][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, aoff[i], k0 * 2, 0);
+            for (int i = 0; i < MI; ++i) ra[S][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, aoff[i], k0 * 2, 0);
     #pragma unroll
             for (int i = 0; i < BCH; ++i) rb[S][i] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, boff[i], k0 * 2, 0);
         };
         auto sstore = [&](auto set, int buf) __attribute__((always_inline)) {
             constexpr int S = decltype(set)::value;
             uint16_t* As = lds + buf * STAGE;
-            uint16_t* Bs = As + GBM * GBK;
+            uint16_t* Bs = As + BM * GBK;
     #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < MI; ++i) {
                 const int c = t + 256 * i, r = c >> 3;
                 *reinterpret_cast<u32x4*>(As + r * GBK + (((c & 7) ^ (r & 7)) * 8)) = ra[S][i];
             }
@@ -373,14 +375,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 
         // MFMA operands of one 32-wide k half (ks) of an LDS buffer: two named register sets, F0 for ks 0 and F1 for
         // ks 1, so the reads of one half run under the MFMAs of the other
-        f16x8 fa[2][4], fb[2][JT];
+        f16x8 fa[2][MI], fb[2][JT];
         auto read_frags = [&](auto ksc, int buf) __attribute__((always_inline)) {
             constexpr int KS = decltype(ksc)::value;
             const uint16_t* As = lds + buf * STAGE;
-            const uint16_t* Bs = As + GBM * GBK;
+            const uint16_t* Bs = As + BM * GBK;
     #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = wm * 64 + i * 16 + c16;
+            for (int i = 0; i < MI; ++i) {
+                const int r = wm * (BM / 2) + i * 16 + c16;
                 fa[KS][i] = as_f16x8(*reinterpret_cast<const u32x4*>(As + r * GBK + (((KS * 4 + g) ^ (r & 7)) * 8)));
             }
     #pragma unroll
@@ -392,13 +394,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         auto mfma_half = [&](auto ksc) __attribute__((always_inline)) {
             constexpr int KS = decltype(ksc)::value;
     #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
     #pragma unroll
                 for (int j = 0; j < JT; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[KS][i], fb[KS][j], acc[i][j], 0, 0, 0);
         };
         // the MFMAs of one half interleaved with the LDS reads of the other: MPR MFMAs, then one read
-        constexpr int NRD = 4 + JT, NMF = 4 * JT, MPR = NMF / NRD;
+        constexpr int NRD = MI + JT, NMF = MI * JT, MPR = NMF / NRD;
         auto interleave = [&]() __attribute__((always_inline)) {
     #pragma unroll
             for (int i = 0; i < NRD; ++i) {
@@ -458,14 +460,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     if (EPI == EPI_F32 || EPI == EPI_RESID || EPI == EPI_PART) {
         float* const y = EPI == EPI_PART ? p.y32 + size_t(blockIdx.z) * p.M * p.N : p.y32;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int j = 0; j < JT; ++j) {
                 int n = n0 + wn * WN + j * 16 + c16;
                 if (n >= p.N) continue;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    int m = m0 + wm * 64 + i * 16 + 4 * g + r;
+                    int m = m0 + wm * (BM / 2) + i * 16 + 4 * g + r;
                     if (m >= p.M) continue;
                     size_t o = size_t(m) * p.N + n;
                     y[o] = EPI == EPI_RESID ? p.resid[o] + acc[i][j][r] : acc[i][j][r];
@@ -484,17 +486,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         if (head < p.qh + p.kvh) {
             float* tile = reinterpret_cast<float*>(lds);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < JT; ++j)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int row = wm * 64 + i * 16 + 4 * g + r, col = wn * WN + j * 16 + c16;
+                        const int row = wm * (BM / 2) + i * 16 + 4 * g + r, col = wn * WN + j * 16 + c16;
                         tile[row * 128 + (col ^ ((row & 15) << 2))] = acc[i][j][r];
                     }
             __syncthreads();
             const bool is_q = head < p.qh;
             const int row = t >> 1, hf = t & 1, m = m0 + row;
+            if (row >= BM) return;  // 64-row tiles: threads 128 .. 255 have no row
             float x[2][32];
 #pragma unroll
             for (int part = 0; part < 2; ++part)
@@ -558,11 +561,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     float* x32 = reinterpret_cast<float*>(lds);  // 2 (wm) x 4 JT x 4 values x 64 lanes: 32 KiB (JT 4), 48 KiB (JT 6)
     if (wn == 1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int j = 0; j < JT; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) x32[((wm * 4 * JT + i * JT + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+                for (int r = 0; r < 4; ++r) x32[((wm * MI * JT + i * JT + j) * 4 + r) * 64 + lane] = acc[i][j][r];
     }
     __syncthreads();
     const int head = tx;  // QKV: a V head (the q and k heads returned above)
@@ -571,17 +574,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < JT; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) hi[j][r] = x32[((wm * 4 * JT + i * JT + j) * 4 + r) * 64 + lane];
+            for (int r = 0; r < 4; ++r) hi[j][r] = x32[((wm * MI * JT + i * JT + j) * 4 + r) * 64 + lane];
     };
 
     if (EPI == EPI_SWIGLU) {
         // a[m, j0 + c] = silu(gate) * up, silu(g) = g / (1 + exp(-g)), into an fp16 tile in LDS after x32 (rows of PAIR
         // columns padded by 8), then out as 16-byte row chunks by all four waves
         constexpr int AR = PAIR + 8, CH = PAIR / 8;  // LDS row stride (halves), 16-byte chunks per row
-        uint16_t* As = lds + 2 * 4 * 4 * JT * 64 * 2;
+        uint16_t* As = lds + 2 * MI * 4 * JT * 64 * 2;
         if (wn == 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < MI; ++i) {
                 float hi[JT][4];
                 load_hi(i, hi);
 #pragma unroll
@@ -590,7 +593,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                     for (int r = 0; r < 4; ++r) {
                         const float gv = acc[i][j][r];
                         const float sg = gv / (1.0f + __expf(-gv));
-                        As[(wm * 64 + i * 16 + 4 * g + r) * AR + j * 16 + c16] = f2h(sg * hi[j][r]);
+                        As[(wm * (BM / 2) + i * 16 + 4 * g + r) * AR + j * 16 + c16] = f2h(sg * hi[j][r]);
                     }
             }
         }
@@ -623,12 +626,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         uint16_t* Vs = lds + 16384;
         if (wn == 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < MI; ++i) {
                 float hi[JT][4];
                 load_hi(i, hi);
 #pragma unroll
                 for (int j = 0; j < JT; ++j) {
-                    uint16_t* vr = Vs + (j * 16 + c16) * 136 + wm * 64 + i * 16 + 4 * g;
+                    uint16_t* vr = Vs + (j * 16 + c16) * 136 + wm * (BM / 2) + i * 16 + 4 * g;
                     *reinterpret_cast<uint2*>(vr) =
                         make_uint2(pack2h(acc[i][j][0], acc[i][j][1]), pack2h(acc[i][j][2], acc[i][j][3]));
                     *reinterpret_cast<uint2*>(vr + 64 * 136) =
@@ -638,13 +641,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         }
         __syncthreads();
         const int p0 = p.pos0 + m0;
-        const bool whole = (p0 & 7) == 0 && m0 + GBM <= p.M;  // 16-byte aligned, every row of the tile present
-        const int ch = t & 15;
+        const bool whole = (p0 & 7) == 0 && m0 + BM <= p.M;  // 16-byte aligned, every row of the tile present
+        constexpr int CHV = BM / 8, RPP = 256 / CHV;  // 16-byte chunks per V^T row, rows per pass
+        const int ch = t % CHV;
         uint32_t bad = 0;
         uint16_t* vbase = p.vc + size_t(head - p.qh - p.kvh) * 128 * p.max_pos + p0 + ch * 8;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int d = (t >> 4) + 16 * k;
+        for (int k = 0; k < 128 / RPP; ++k) {
+            const int d = t / CHV + RPP * k;
             const u32x4 v = *reinterpret_cast<const u32x4*>(Vs + d * 136 + ch * 8);
             uint16_t* dst = vbase + size_t(d) * p.max_pos;
             if (whole) {
@@ -1996,6 +2000,9 @@ static bool two_per_cu(const dim3& g) {
     const uint64_t tiles = uint64_t(g.x) * g.y;
     return tiles >= 512 && (tiles % 512 == 0 || tiles >= 4 * 512);
 }
+// q|k|v tiles of 64 rows where 128-row tiles leave CUs without a tile (512 rows: 32 x 4 tiles on half the CUs, 32 x 8
+// on all of them; the 512-token forward 2.40-2.41 -> 2.27 ms)
+static bool qkv_rows64(uint32_t m, uint32_t heads) { return m > 64 && uint64_t(heads) * ((m + 127) / 128) < 256; }
 
 // eps
 static void l_gemm_qkv(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
@@ -2017,6 +2024,8 @@ static void l_gemm_qkv(const PreparedDispatch& pd, void* const* p, hipStream_t s
     const dim3 grid(uint32_t(qh + 2 * kvh), (w[10] + GBM - 1) / GBM);
     if (two_per_cu(grid))
         hipLaunchKernelGGL((k_gemm<EPI_QKV, 128, true>), grid, dim3(256), 0, s, a);
+    else if (qkv_rows64(w[10], qh + 2 * kvh))
+        hipLaunchKernelGGL((k_gemm<EPI_QKV, 128, false, 64>), dim3(grid.x, (w[10] + 63) / 64), dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL((k_gemm<EPI_QKV, 128, false>), grid, dim3(256), 0, s, a);
 }
@@ -2426,7 +2435,10 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 15 gemm_qkv_rope
     c.push_back({"gemm_qkv_rope", "fast", {256, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{int64_t(w[12]) + 2 * w[13], (int64_t(w[10]) + 127) / 128, 1}; },
+                 [](const uint32_t* w) {
+                     const uint32_t heads = w[12] + 2 * w[13], rows = qkv_rows64(w[10], heads) ? 64 : 128;
+                     return Grid3{heads, (int64_t(w[10]) + rows - 1) / rows, 1};
+                 },
                  {TOK_R("h", DT(F16)), TOK_R("w", DT(F16)), TOK_R("q_norm", DT(BF16)), TOK_R("k_norm", DT(BF16)),
                   TOK_R("cos_table", DT(F32)), TOK_R("sin_table", DT(F32)), TOK_W("q", DT(F16)),
                   TOK_W("k_cache", DT(F16)), TOK_W("v_cache", DT(F16)), U32F("m"), U32F("hidden"), U32F("q_heads"),

@@ -140,12 +140,14 @@ def test_gemm_swiglu(m, inter, k):
         s.close()
 
 
-@pytest.mark.parametrize("T,pos0,max_pos", [(100, 37, 256), (300, 64, 512), (2048, 37, 2112), (2048, 64, 2112)])
+@pytest.mark.parametrize("T,pos0,max_pos", [(100, 37, 256), (300, 64, 512), (512, 64, 640), (1100, 37, 1152),
+                                           (2048, 37, 2112), (2048, 64, 2112)])
 def test_gemm_qkv_rope_epilogue(T, pos0, max_pos):
     """q|k|v projection with the per-head RMSNorm + RoPE epilogue and the K / V^T cache writes, against CpuRef F64
-    on the same fp16 operands: an unaligned position (element-wise V^T stores) and an aligned one (16-byte rows for the
-    two whole row tiles, element-wise for the partial third); at 2048 rows (512 tiles: the direct-to-LDS loop of the
-    2048-token prefill) with an unaligned and an aligned first position."""
+    on the same fp16 operands. Under 256 tiles of 128 rows the tiles are 64 rows: 100 and 300 rows at an unaligned
+    position (element-wise V^T stores) and an aligned one (16-byte rows for the whole row tiles, element-wise for the
+    partial last), 512 rows (the 512-token prefill: 32 x 8 tiles); 1100 rows: 128-row tiles on the register loop;
+    2048 rows (512 tiles: the direct-to-LDS loop of the 2048-token prefill) at both kinds of first position."""
     H = 256
     r = np.random.default_rng(11)
     h = f16(r.standard_normal((T, H)))
