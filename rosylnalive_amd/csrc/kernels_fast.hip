@@ -208,7 +208,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     static_assert(BN == 128 || (BN == 64 && (EPI == EPI_F32 || EPI == EPI_RESID || EPI == EPI_PART)) ||
                       (BN == 192 && EPI == EPI_SWIGLU && DMA),
                   "QKV takes 128 columns, SwiGLU 128 or 192 (64 or 96 gate / up pairs)");
-    static_assert(BM == GBM || (BM == 64 && EPI == EPI_QKV && !DMA), "64-row tiles: the q|k|v register loop only");
+    static_assert(BM == GBM || (BM == 64 && (EPI == EPI_QKV || EPI == EPI_PART) && !DMA),
+                  "64-row tiles: the q|k|v and k-split register loops only");
     constexpr int MI = BM / 32;   // MFMA row tiles per wave: each wave owns BM / 2 rows
     constexpr int PAIR = BN / 2;  // SWIGLU: gate / up pairs per tile
     // the k range of this block: all of k, or split z of a PART launch (A and W then start kz columns in)
@@ -2303,6 +2304,8 @@ static void l_prefetch(const PreparedDispatch& pd, void* const* p, hipStream_t s
 static bool resid_split_skinny(uint32_t m, uint32_t k, uint32_t splits) {
     return m <= 16 && (k / splits) % (kSkWaves * 128) == 0;
 }
+// 64-row tiles for grids of 128 x 64 tiles under one block per CU
+static bool resid_rows64(uint32_t m, uint64_t blocks128) { return m > 64 && blocks128 < 256; }
 static void l_gemm_resid_split(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     if (resid_split_skinny(w[4], w[6], w[7])) {
@@ -2318,6 +2321,9 @@ static void l_gemm_resid_split(const PreparedDispatch& pd, void* const* p, hipSt
     const uint64_t blocks = uint64_t(grid.x) * grid.y * grid.z;
     if (blocks % 512 == 0)  // whole rounds of two blocks per CU: the direct-to-LDS loop
         hipLaunchKernelGGL((k_gemm<EPI_PART, 64, true>), grid, dim3(256), 0, s, a);
+    else if (resid_rows64(w[4], blocks))  // 64-row tiles, twice the blocks
+        hipLaunchKernelGGL((k_gemm<EPI_PART, 64, false, 64>), dim3(grid.x, (w[4] + 63) / 64, grid.z), dim3(256), 0, s,
+                           a);
     else
         hipLaunchKernelGGL((k_gemm<EPI_PART, 64, false>), grid, dim3(256), 0, s, a);
 }
@@ -2727,7 +2733,9 @@ std::vector<KernelSpec> fast_catalog() {
     c.push_back({"gemm_residual_split", "fast", {256, 1, 1}, false,
                  [](const uint32_t* w) {
                      if (resid_split_skinny(w[4], w[6], w[7])) return Grid3{(int64_t(w[5]) + 15) / 16, w[7], 1};
-                     return Grid3{(int64_t(w[5]) + 63) / 64, (int64_t(w[4]) + 127) / 128, w[7]};
+                     const int64_t gx = (int64_t(w[5]) + 63) / 64, g128 = (int64_t(w[4]) + 127) / 128;
+                     const int64_t rows = resid_rows64(w[4], uint64_t(gx * g128 * w[7])) ? 64 : 128;
+                     return Grid3{gx, (int64_t(w[4]) + rows - 1) / rows, w[7]};
                  },
                  {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("partials", DT(F32)), U32F("m"), U32F("n"), U32F("k"),
                   U32F("splits")},
