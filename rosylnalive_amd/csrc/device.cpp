@@ -309,25 +309,43 @@ void CommandList::dispatch(int kernel, const uint32_t* words) {
 }
 
 void CommandList::dispatch_library(int kernel, const uint32_t* words, int library_field, void* library_ptr) {
+    const LibraryDispatch d{kernel, words, library_field, library_ptr};
+    dispatch_library_all(&d, 1, nullptr);
+}
+
+void CommandList::dispatch_library_all(const LibraryDispatch* d, size_t n, const LibraryCheck& check) {
     check_open();
     if (exec_) contract_fail("a reusable list cannot be changed after its first submission");
     if (!dev_->kernels_loaded()) contract_fail("Dispatch before LoadKernels");
-    if (!dev_->contains(kernel)) contract_fail("kernel %d is not in the loaded kernel set", kernel);
-    if (!library_ptr) contract_fail("no library buffer for field %d", library_field);
-    Cmd c{};
-    c.kind = Cmd::Launch;
-    c.pd = prepare_library_field(dev_->table(), kernel, words, library_field);
-    const KernelSpec& k = catalog()[size_t(kernel)];
-    c.ptr.assign(k.fields.size() + 1, nullptr);
-    for (const TokenUse& u : c.pd.tokens) {
-        if (u.access == Access::Meta)
-            c.ptr[size_t(u.field)] = static_cast<uint8_t*>(dev_->slot_ptr(0)) + size_t(u.token) * kRowBytes;
-        else
-            c.ptr[size_t(u.field)] = dev_->resolve(u.token);
+    std::vector<Cmd> staged;
+    staged.reserve(n);
+    for (size_t i = 0; i < n; ++i) {
+        if (!dev_->contains(d[i].kernel)) contract_fail("kernel %d is not in the loaded kernel set", d[i].kernel);
+        if (!d[i].library_ptr) contract_fail("no library buffer for field %d", d[i].library_field);
+        Cmd c{};
+        c.kind = Cmd::Launch;
+        c.pd = prepare_library_field(dev_->table(), d[i].kernel, d[i].words, d[i].library_field);
+        const KernelSpec& k = catalog()[size_t(d[i].kernel)];
+        c.ptr.assign(k.fields.size() + 1, nullptr);
+        for (const TokenUse& u : c.pd.tokens) {
+            if (u.access == Access::Meta)
+                c.ptr[size_t(u.field)] = static_cast<uint8_t*>(dev_->slot_ptr(0)) + size_t(u.token) * kRowBytes;
+            else
+                c.ptr[size_t(u.field)] = dev_->resolve(u.token);
+        }
+        c.ptr[size_t(d[i].library_field)] = d[i].library_ptr;
+        staged.push_back(std::move(c));
     }
-    c.ptr[size_t(library_field)] = library_ptr;
-    cmds_.push_back(std::move(c));
-    ++dispatches_;
+    if (check) {
+        std::vector<const PreparedDispatch*> pds;
+        for (const Cmd& c : staged) pds.push_back(&c.pd);
+        check(pds);
+    }
+    // nothing was refused: record them all
+    for (Cmd& c : staged) {
+        cmds_.push_back(std::move(c));
+        ++dispatches_;
+    }
 }
 
 void CommandList::dispatch_overlapped(int kernel, const uint32_t* words) {

@@ -14,6 +14,7 @@
 
 #include <array>
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <memory>
 #include <stdexcept>
@@ -94,6 +95,17 @@ class CommandList {
     // A dispatch whose token field `library_field` is device memory the library owns (`library_ptr`) rather than a
     // tensor of the heap; its word is 0 (prepare_library_field). The caller has checked the bytes the launch touches.
     void dispatch_library(int kernel, const uint32_t* words, int library_field, void* library_ptr);
+    // Several library dispatches recorded together or not at all: each is prepared (every contract check) before the
+    // first is recorded, and `check`, when set, sees their prepared argument words and may refuse the group by
+    // throwing. A refused group leaves the list as it was.
+    struct LibraryDispatch {
+        int kernel;
+        const uint32_t* words;
+        int library_field;
+        void* library_ptr;
+    };
+    using LibraryCheck = std::function<void(const std::vector<const PreparedDispatch*>&)>;
+    void dispatch_library_all(const LibraryDispatch* d, size_t n, const LibraryCheck& check);
     void barrier();
     void copy(int src_slot, uint64_t src_off, int dst_slot, uint64_t dst_off, uint64_t bytes);
     int begin_timer(const std::string& name);

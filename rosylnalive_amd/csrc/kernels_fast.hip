@@ -2152,10 +2152,6 @@ void* f16_range_word_fast() {
     return p;
 }
 
-uint32_t decode_attention_splits(uint32_t max_pos, uint32_t chunks, uint32_t splits) {
-    return dec_grid_splits(max_pos, chunks, splits);
-}
-
 static void l_attn_dec(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     const int max_pos = int(w[12]);

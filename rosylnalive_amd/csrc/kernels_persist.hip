@@ -13,7 +13,10 @@
 //
 // XCD mapping. An MI355X has 8 XCDs, each with its own L2; the dispatcher puts workgroup b on XCD (b + c) % 8, with c
 // fixed for a launch (it depends on the hardware queue), so each XCD holds 32 workgroups. A workgroup reads its XCD from
-// the hardware register XCC_ID and takes role j = b / 8 on it: every (XCD, j) is taken once. A device-scope store writes
+// the hardware register XCC_ID and takes role j = b / 8 on it: every (XCD, j) is taken once. That placement is the
+// dispatcher's, not a documented guarantee, so each workgroup claims its role at launch (an exchange of the launch's
+// tag into the role's header word): a role claimed twice aborts the step, which the host then reports, instead of
+// leaving another role untaken and its readers on entries of an earlier step. A device-scope store writes
 // through to memory
 // and a device-scope load from another XCD fetches it there: 0.7 us one way, about 2.2 us for an all-gather between all
 // 256 workgroups. A plain store stays in the writer's L2, where a device-scope load from the same XCD finds it: 0.3 us.
@@ -484,10 +487,17 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
         for (int c = 0; c < kNCH; ++c) na[c] = ld16(a.in_norm + size_t(l) * kH + 512 * c + 8 * lane);
     };
 
+    // claim role (xcd, j) for this launch; the answer is checked after the embed, behind the loads issued before it
+    uint32_t prior_claim = 0;
+    if (t == 0)
+        prior_claim = __hip_atomic_exchange(hdr + kClaimWord + xcd * kJN + j, tag, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+
     // x = widen(E[id]) (NaN for an id outside the vocabulary, as embed_dec)
     issue_a(0);
     for (int k = t; k < kH; k += kThreads)
         xres[k] = id < uint32_t(a.vocab) ? bf2f(a.embed[size_t(id) * kH + k]) : __uint_as_float(0x7FC00000u);
+    if (t == 0 && prior_claim == tag) abort_step(hdr, kStageClaim);  // another workgroup holds this role
     lds_barrier();
 
     // This split's first 64-key chunks of K and V^T (one when the split holds one, else two): they do not depend on

@@ -8,9 +8,12 @@ namespace lrm {
 namespace persist {
 
 constexpr int kWaves = 8, kThreads = 512;
-// 256-byte header before the entries: u32 word 0 = launch epoch, 1 = abort, 2 = the stage that aborted, 3 = the bound
-// of every wait in 100 MHz constant-clock ticks (0: 0.2 s)
-constexpr int kHdrEntries = 32;
+// Header before the entries: u32 word 0 = launch epoch, 1 = abort, 2 = the stage that aborted, 3 = the bound of every
+// wait in 100 MHz constant-clock ticks (0: 0.2 s); words kClaimWord .. + 255: the role claims, one per (XCD, j), each
+// holding the tag of the last launch whose workgroup took that role (a second claim in one launch aborts the step).
+constexpr int kHdrEntries = 32 + 128;
+constexpr int kClaimWord = 64;
+constexpr int kStageClaim = 9;  // the abort stage of a role taken twice
 constexpr int kVecMax = 8704;  // floats of the LDS vector a stage gathers its input into
 // The accelerator complex dies (XCDs) of an MI355X, each with its own L2. KV head h lives on XCD h: its q|k|v rows,
 // attention splits, and the o_proj / down_proj columns that read them, so three of a layer's five hand-offs stay

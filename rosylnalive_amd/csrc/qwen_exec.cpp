@@ -933,6 +933,10 @@ void QwenExec::run_decode_steps(int steps) {
     if (persist_) {  // a workgroup that waited past its bound aborted the step (and every later one)
         uint32_t hdr[3];
         download_tensor("dec.exchange", hdr, sizeof hdr);
+        if (hdr[1] && hdr[2] == uint32_t(persist::kStageClaim))
+            throw std::runtime_error("decode_step_persistent: two workgroups of one launch took the same (XCD, role) "
+                                     "slot (the dispatcher placed the workgroups otherwise than the step assumes); "
+                                     "the step's results are not valid");
         if (hdr[1])
             throw std::runtime_error("decode_step_persistent: a workgroup waited past its bound at stage " +
                                      std::to_string(hdr[2]) + "; the decode state did not advance from there");

@@ -20,8 +20,6 @@ static __device__ __align__(256) float scratch[kStaticScratchBytes / sizeof(floa
 
 namespace lrm {
 
-uint32_t decode_attention_splits(uint32_t max_pos, uint32_t chunks, uint32_t splits);  // kernels_fast.hip
-
 size_t static_scratch_bytes() { return kStaticScratchBytes; }
 
 void* static_scratch_address(int device) {
@@ -44,27 +42,32 @@ void* static_scratch_address(int device) {
 
 // attention_decode_f16 then attention_combine (f32 output), the split partials in this GPU's static scratch.
 // words: the attention_decode_f16 argument block with its partials word 0; y: the combine's output token.
+// Both dispatches are contract-checked, and the partials' bytes are computed from the checked words, before either
+// is recorded: a refused call leaves the list unchanged.
 void record_decode_attention_static(Device& dev, CommandList* l, const uint32_t* words, uint32_t y) {
     const int dec = catalog_find("attention_decode_f16"), comb = catalog_find("attention_combine");
-    const uint32_t qh = words[10], mp = words[12], B = words[15], chunks = words[16], splits = words[17];
-    // the bytes the launches touch: per sequence and query head, one 130-float row per split
-    const uint64_t S = decode_attention_splits(mp, chunks, splits);
-    const uint64_t bytes = uint64_t(B) * qh * S * 130 * sizeof(float);
-    if (bytes > kStaticScratchBytes)
-        contract_fail("decode attention (static scratch): %u sequences x %u query heads x %llu splits need %llu bytes "
-                      "of split partials; the static scratch holds %zu",
-                      B, qh, (unsigned long long)S, (unsigned long long)bytes, kStaticScratchBytes);
-    void* p = dev.static_scratch();
-    l->dispatch_library(dec, words, 7, p);
     uint32_t cw[32] = {0};
-    cw[2] = y;            // y
-    cw[3] = words[9];     // state
-    cw[4] = qh;           // q_heads
-    cw[5] = mp;           // max_pos
-    cw[6] = B;            // batch
-    cw[7] = chunks;       // chunks
-    cw[8] = splits;       // splits
-    l->dispatch_library(comb, cw, 0, p);
+    cw[2] = y;              // y
+    cw[3] = words[9];       // state
+    cw[4] = words[10];      // q_heads
+    cw[5] = words[12];      // max_pos
+    cw[6] = words[15];      // batch
+    cw[7] = words[16];      // chunks
+    cw[8] = words[17];      // splits
+    void* p = dev.static_scratch();
+    const CommandList::LibraryDispatch both[2] = {{dec, words, 7, p}, {comb, cw, 0, p}};
+    l->dispatch_library_all(both, 2, [](const std::vector<const PreparedDispatch*>& pd) {
+        // the bytes the launches touch: per sequence and query head, one 130-float row per split
+        const uint32_t* w = pd[0]->words.data();
+        const uint64_t qh = w[10], mp = w[12], B = w[15], chunks = w[16] ? w[16] : 1, splits = w[17];
+        const uint64_t S = splits ? splits : (mp + 64 * chunks - 1) / (64 * chunks);
+        const uint64_t bytes = B * qh * S * 130 * sizeof(float);
+        if (bytes > kStaticScratchBytes)
+            contract_fail("decode attention (static scratch): %llu sequences x %llu query heads x %llu splits need "
+                          "%llu bytes of split partials; the static scratch holds %zu",
+                          (unsigned long long)B, (unsigned long long)qh, (unsigned long long)S,
+                          (unsigned long long)bytes, kStaticScratchBytes);
+    });
 }
 
 }  // namespace lrm

@@ -36,12 +36,6 @@ SUBSTAGES = [  # name, first point, last point (L k: stage boundary k; s k: poin
     ("D barrier", "s10", "L10", False), ("E rows", "L11", "s11", False), ("E barrier", "s11", "L12", False)]
 
 
-def S_used(pos):
-    """Attention splits holding keys at position pos (32 splits of a whole number of 64-key chunks)."""
-    kps = ((pos + 1 + 31) // 32 + 63) // 64 * 64
-    return (pos + 1 + kps - 1) // kps
-
-
 def main(argv):
     contexts = [int(c) for c in (argv[0] if argv else "392,4000").split(",")]
     if not os.path.exists(STAMPS_LIB):
@@ -91,7 +85,8 @@ def main(argv):
         print(f"  layer (first start to last end) {us(L[:, 12].max() - lay0):.2f} us")
         P = st[:, 32:38]
         passes = [("A", P[:, 0]), ("B", P[attn, 1]), ("C", P[:, 2])]
-        if 2 * S_used(ctx + 8) * 33 > 3 * 512:  # the partial rows took a second gather
+        s_used = int(attn.sum()) // 8  # splits holding keys: the attention workgroups of one XCD
+        if 2 * s_used * 33 > 3 * 512:  # the partial rows took a second gather
             passes.append(("C, second part", P[:, 3]))
         passes += [("D", P[:, 4]), ("E", P[:, 5])]
         print("  poll passes of thread 0 (median / max): " +

@@ -106,6 +106,32 @@ def test_every_scalars_class_equals_the_oracles(tables):
     assert bad.size == 0, [hex(c) for c in bad[:20]]
 
 
+def test_every_scalars_class_agrees_with_the_regex_module(tables):
+    """Pins the compiled class table by something other than the probe file it was generated from: Python's regex
+    module (its own Unicode 17.0 tables) classifies every scalar as \\p{L}, \\p{N}, \\s or other; the compiled
+    table (Unicode 16.0, the tokenizer specification's) may differ from it only on scalars that Python's unicodedata
+    (Unicode 13.0) leaves unassigned, i.e. on letters and numbers added after 13.0. A class moved between two assigned
+    scalars, a dropped run or a shifted run boundary fails here."""
+    import unicodedata
+
+    regex = pytest.importorskip("regex")
+    cls, _, _ = tables
+    L, N, S = regex.compile(r"\p{L}"), regex.compile(r"\p{N}"), regex.compile(r"\s")
+    differ = []
+    for c in SCALARS:
+        ch = chr(c)
+        theirs = 0 if L.match(ch) else 1 if N.match(ch) else 2 if S.match(ch) else 3
+        if int(cls[c]) != theirs:
+            differ.append(c)
+    assigned = [hex(c) for c in differ if unicodedata.category(chr(c)) != "Cn"]
+    assert not assigned, assigned[:20]
+    # the Unicode 14.0-16.0 additions the two versions disagree on are a few thousand scalars, not a whole plane
+    assert len(differ) < 20000, len(differ)
+    # and the well-known members of each class
+    for c, k in ((ord("a"), 0), (0x4E00, 0), (ord("7"), 1), (0x0663, 1), (ord(" "), 2), (0x3000, 2), (ord("!"), 3)):
+        assert int(cls[c]) == k, hex(c)
+
+
 def test_the_contraction_group_matches_exactly_the_oracles_letters(tables):
     _, con, _ = tables
     want = {}

@@ -113,16 +113,58 @@ def test_static_scratch_in_a_replayed_graph(sess):
         cl.release()
 
 
-def test_static_scratch_rejects_more_partials_than_it_holds(sess):
-    """4 MiB holds batch * 16 heads * splits * 130 floats up to 8065 (batch, split) rows of 16 heads: four sequences
-    at 32 splits fit, 4 x 1024 splits do not (max_pos 65536 would need 34 MB)."""
-    words = sess.fields("attention_decode_f16", **dict(_fields([1, 2, 3, 4], 0, 0), max_pos=65536))
+def test_static_scratch_rejects_more_partials_than_it_holds():
+    """4 MiB holds batch * 16 heads * splits * 130 floats up to 504 (batch, split) pairs: 16 sequences at max_pos
+    2048 and 32 splits (4,259,840 bytes) do not fit, 15 do. The bound is computed from the contract-checked words, and
+    a refused call records nothing."""
+    B, mp = 16, 2048
+    s = Session({"qkv": (F32, (B, 4096), RO, None), "qn": (BF16, (128,), RO, None), "kn": (BF16, (128,), RO, None),
+                 "cos": (F32, (mp, 64), RO, None), "sin": (F32, (mp, 64), RO, None),
+                 "kc": (F16, (B * 8, mp, 128), 0, None), "vc": (F16, (B * 8, 128, mp), 0, None),
+                 "part": (F32, (B * 16 * (mp // 64) * 130,), 0, None),
+                 "y": (F32, (B, 2048), 0, None), "state": (U32, (2 * B + 2,), 0, None)})
+    try:
+        def words(batch, partials=0):
+            return s.fields("attention_decode_f16", qkv="qkv", q_norm="qn", k_norm="kn", cos_table="cos",
+                            sin_table="sin", k_cache="kc", v_cache="vc", partials=partials, state="state", q_heads=16,
+                            kv_heads=8, max_pos=mp, eps=1e-6, scale=0.08838834764831845, batch=batch, chunks=1,
+                            splits=0)
+
+        cl = s.backend.begin()
+        try:
+            with pytest.raises(GpuContractException, match="static scratch holds"):
+                cl.dispatch_decode_attention_static(words(16), s.tok["y"])
+            with pytest.raises(GpuContractException, match="library supplies"):
+                cl.dispatch_decode_attention_static(words(1, "part"), s.tok["y"])
+            c = s.backend.wait(s.backend.submit(cl))
+            assert c.dispatches == 0  # the refused calls recorded neither kernel
+        finally:
+            cl.release()
+        cl = s.backend.begin()
+        try:
+            cl.dispatch_decode_attention_static(words(15), s.tok["y"])  # 3,993,600 bytes: fits (recorded, not run)
+        finally:
+            cl.release()
+    finally:
+        s.close()
+
+
+def test_refused_combine_leaves_the_list_and_caches_unchanged(sess):
+    """The combine's own contract check (here: y too small for the batch, then y of the wrong dtype) refuses the call
+    after the attention's check passed: neither kernel is recorded, so submitting the list runs nothing and the K/V
+    caches keep their bits (an orphan attention launch would append rows)."""
+    positions = [5, 64, 700, 2000]
+    _reset(sess, positions)
+    words = sess.fields("attention_decode_f16", **_fields(positions, 0, 0))
     cl = sess.backend.begin()
     try:
-        with pytest.raises(GpuContractException, match="static scratch holds"):
-            cl.dispatch_decode_attention_static(words, sess.tok["y"])
-        with pytest.raises(GpuContractException, match="library supplies"):
-            cl.dispatch_decode_attention_static(
-                sess.fields("attention_decode_f16", **_fields([1], 0, "part")), sess.tok["y"])
+        with pytest.raises(GpuContractException):
+            cl.dispatch_decode_attention_static(words, sess.tok["qn"])  # bf16 [128]: wrong dtype and too small
+        with pytest.raises(GpuContractException):
+            cl.dispatch_decode_attention_static(words, 0)  # token 0: the null tensor
+        c = sess.backend.wait(sess.backend.submit(cl))
+        assert c.dispatches == 0
     finally:
         cl.release()
+    assert sess.read("kc").tobytes() == sess.kc0.tobytes()
+    assert sess.read("vc").tobytes() == sess.vc0.tobytes()
