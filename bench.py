@@ -31,6 +31,7 @@ GEMV_SWIGLU_TRAFFIC_BYTES = 12675736  # measured HBM bytes per gemv_swiglu_dec l
 PERSIST_TRAFFIC_BYTES = 1278457474    # measured HBM bytes per decode_step_persistent launch at context 393..424
 ROOFLINE_POS0 = 392                   # the roofline launches run at context ROOFLINE_POS0 + 1 .. ROOFLINE_POS0 + 32
 CPU_DECODE_STEPS = 128                # the bounded CPU decode sample (about 10 s on 16 host cores)
+CTX4K_CHECK_STEPS = 8                 # decode steps of the 4K-context leg whose ids the oracle checks
 
 
 def log(*a):
@@ -314,7 +315,7 @@ def main():
         },
     }
 
-    e_sample = None
+    e_sample = ctx4k_sample = None
     if not args.no_extras:
         # 512-token prefill with every logit row (all 512 x 151936 logits)
         out["prefill_512_all_logits"] = prefill(512, 512, "bench/prefill512")
@@ -346,6 +347,10 @@ def main():
         model.decode_run(4)
         model.decode_run(64)
         d_ms = model.last_ms()
+        if not args.no_cpu:  # the prefill's caches and the first ids, for the oracle's check of this leg
+            ctx4k_sample = {"first": int(nxt), "ids": model.decode_ids(CTX4K_CHECK_STEPS).tolist(),
+                            "k": [model.read_cache(l_, "k", 0, 4096) for l_ in range(L)],
+                            "v": [model.read_cache(l_, "v", 0, 4096) for l_ in range(L)]}
         b4 = sum(weight_bytes + kv_bytes(4096 + 4 + s + 1) for s in range(64))
         out["decode_4k"] = {"tok_s": round(64 / (d_ms / 1e3), 1), "ms_per_token": round(d_ms / 64, 4),
                             "gbs": round(b4 / (d_ms / 1e3) / 1e9, 1),
@@ -442,6 +447,29 @@ def main():
                                          f"({t_pre:.2f} s, {128 / t_pre:.1f} tok/s) then {steps} greedy decode steps, "
                                          f"context 129..{128 + steps} ({t_dec:.2f} s)"}
         log("cpu baseline:", out["cpu_baseline"])
+        if ctx4k_sample is not None:
+            # the 4K-context leg's first steps: the oracle over the device's own prefill caches (positions 0..4095),
+            # fed the device's ids; its argmax at each step against the device's id
+            cos4, sin4 = cpuref.rope_table(inv_freq_bits(HD), 4096 + 64)
+            ocfg4 = cfg.oracle_dict()
+            ocfg4["max_pos"] = 4096 + 64
+            o4 = cpuref.QwenOracle(ocfg4, weights, cos4, sin4)
+            kc4, vc4 = o4.new_cache()
+            for l_ in range(L):
+                kc4[l_, :4096] = ctx4k_sample["k"][l_]
+                vc4[l_, :4096] = ctx4k_sample["v"][l_]
+            feed = [ctx4k_sample["first"]] + ctx4k_sample["ids"][:-1]
+            t4 = time.perf_counter()
+            o_ids = [int(np.argmax(o4.forward((kc4, vc4), 4096 + s_, np.array([feed[s_]], np.int32))[-1]))
+                     for s_ in range(CTX4K_CHECK_STEPS)]
+            same4 = [a == b for a, b in zip(ctx4k_sample["ids"], o_ids)]
+            out["decode_4k"]["ids_vs_oracle"] = {
+                "compared": CTX4K_CHECK_STEPS, "equal": int(sum(same4)), "oracle_s": round(time.perf_counter() - t4, 2),
+                "what": "the first %d decode steps' greedy ids (context 4097..%d) against the oracle's argmax, the "
+                        "oracle run over the device's prefill caches (read back) and fed the device's ids"
+                        % (CTX4K_CHECK_STEPS, 4096 + CTX4K_CHECK_STEPS)}
+            log("decode 4k ids vs oracle:", out["decode_4k"]["ids_vs_oracle"])
+            del kc4, vc4, o4, ctx4k_sample
         if not args.no_extras:
             out["cpu_configs"] = cpu_configs(args.seed, cfg, weights, threads, e_sample)
             log("cpu configs:", out["cpu_configs"])

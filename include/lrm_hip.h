@@ -107,9 +107,18 @@ int lrm_hip_upload(lrm_hip_device *d, int slot, uint64_t offset, const void *src
 int lrm_hip_download(lrm_hip_device *d, int slot, uint64_t offset, void *dst, uint64_t bytes);
 
 /* IGpuBackend.LoadKernels / IKernelSet (Backend.fs:104-108,144-147): the gfx950 code objects are part of this
- * library; the shader-set hash is the SHA-256 of the library file. Runs the fp32 denormal probe
- * (Backend.fs:457-547): mode 1 preserve, 2 flush, 3 mixed. */
+ * library. Loads the reference kernel set (catalog ids 0-13, Kernels.g.fs:27-285), which keeps the BatchInvariance
+ * contract (docs/contracts/batch-invariance.md:7-12). The shader-set hash, which fills ExecutionClass.ShaderSetHash
+ * (ExecutionClass.fs:58), is the SHA-256 of the set's name and the library file's SHA-256. Runs the fp32 denormal
+ * probe (Backend.fs:457-547): mode 1 preserve, 2 flush, 3 mixed. */
 int lrm_hip_load_kernels(lrm_hip_device *d, uint8_t shader_set_hash[32]);
+/* An extension of LoadKernels: the set to load, once per backend. LRM_HIP_KERNELS_FAST is every id (0-40, the
+ * appended fast path included) under its own shader-set hash, so its results form their own ExecutionClass: it only
+ * claims that the same work on the same inputs gives the same bits (the row count chooses its k-split and attention
+ * splits; its prefill and decode kernels sum in different orders), and no bit-identity claim crosses the two sets. */
+#define LRM_HIP_KERNELS_REFERENCE 0u
+#define LRM_HIP_KERNELS_FAST 1u
+int lrm_hip_load_kernel_set(lrm_hip_device *d, uint32_t set, uint8_t shader_set_hash[32]);
 int lrm_hip_contains(lrm_hip_device *d, uint32_t kernel); /* 1 or 0 */
 int lrm_hip_denormal_probe(lrm_hip_device *d, int *mode, uint32_t results[7]);
 

@@ -320,9 +320,14 @@ int lrm_hip_download(lrm_hip_device* d, int slot, uint64_t off, void* dst, uint6
 }
 
 int lrm_hip_load_kernels(lrm_hip_device* d, uint8_t hash[32]) {
+    return lrm_hip_load_kernel_set(d, LRM_HIP_KERNELS_REFERENCE, hash);
+}
+
+int lrm_hip_load_kernel_set(lrm_hip_device* d, uint32_t set, uint8_t hash[32]) {
     return guard([&] {
         need_ptr(d, "device");
-        auto h = d->d.load_kernels();
+        if (set != LRM_HIP_KERNELS_REFERENCE && set != LRM_HIP_KERNELS_FAST) contract_fail("unknown kernel set %u", set);
+        auto h = d->d.load_kernels(set == LRM_HIP_KERNELS_FAST ? Device::KernelSet::Fast : Device::KernelSet::Reference);
         if (hash) std::memcpy(hash, h.data(), 32);
     });
 }

@@ -222,10 +222,15 @@ static std::array<uint8_t, 32> hash_of_this_library() {
     return Sha256::of(bytes.data(), bytes.size());
 }
 
-std::array<uint8_t, 32> Device::load_kernels() {
+std::array<uint8_t, 32> Device::load_kernels(KernelSet set) {
     if (loaded_) contract_fail("LoadKernels runs exactly once per backend");
+    if (set != KernelSet::Reference && set != KernelSet::Fast) contract_fail("unknown kernel set %d", int(set));
     HIPC(hipSetDevice(index_));
-    shader_hash_ = hash_of_this_library();
+    const std::array<uint8_t, 32> lib = hash_of_this_library();
+    std::string msg = set == KernelSet::Reference ? "lrm-hip kernel set: reference\n" : "lrm-hip kernel set: fast\n";
+    msg.append(reinterpret_cast<const char*>(lib.data()), lib.size());
+    shader_hash_ = Sha256::of(msg.data(), msg.size());
+    set_ = set;
     loaded_ = true;
     run_probe();
     return shader_hash_;
@@ -233,6 +238,7 @@ std::array<uint8_t, 32> Device::load_kernels() {
 
 bool Device::contains(int kernel) const {
     if (kernel < 0 || kernel >= catalog_size()) return false;
+    if (set_ == KernelSet::Reference && kernel >= fast_first_id()) return false;
     if (kernel < fast_first_id()) return catalog_launchers()[kernel] != nullptr;
     return fast_launchers()[kernel - fast_first_id()] != nullptr;
 }

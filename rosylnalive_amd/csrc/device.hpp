@@ -157,9 +157,18 @@ class Device {
     bool table_written() const { return !table_host_.empty(); }
     SealedTableView table() const;
 
-    // IKernelSet
-    std::array<uint8_t, 32> load_kernels();
+    // IKernelSet. Two kernel sets, each its own ExecutionClass (its own shader-set hash), since they make different
+    // bit-identity claims:
+    //   Reference: the reference's catalog, ids 0 .. fast_first_id() - 1, which keeps the BatchInvariance contract
+    //     (a row alone equals the row in any batch; prefill equals decode and any chunked prefill);
+    //   Fast: every id (the reference's catalog and the fast path), which only claims that the same work on the same
+    //     inputs gives the same bits: its k-split and attention-split choices depend on the row count, and its
+    //     prefill and decode kernels sum in different orders.
+    // The hash is the SHA-256 of the set's name and the library file's SHA-256.
+    enum class KernelSet { Reference = 0, Fast = 1 };
+    std::array<uint8_t, 32> load_kernels(KernelSet set = KernelSet::Reference);
     bool kernels_loaded() const { return loaded_; }
+    KernelSet kernel_set() const { return set_; }
     bool contains(int kernel) const;
     const std::array<uint8_t, 32>& shader_set_hash() const { return shader_hash_; }
     // fp32 denormal mode measured by the probe after load_kernels (gpu-backend.md "fp32 denormals"): 0 unknown,
@@ -203,6 +212,7 @@ class Device {
     std::vector<void*> pages_;  // slot i at pages_[i], slot 0 = the table buffer
     std::vector<uint8_t> table_host_;
     bool loaded_ = false;
+    KernelSet set_ = KernelSet::Reference;
     std::array<uint8_t, 32> shader_hash_{};
     int denormal_mode_ = 0;
     std::array<uint32_t, 7> probe_results_{};

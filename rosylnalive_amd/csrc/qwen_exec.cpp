@@ -195,7 +195,13 @@ QwenExec::QwenExec(Device& dev, const QwenConfig& cfg, const uint32_t* inv_freq_
     } else if (c.batch != 1) {
         arg_fail("the fp32 mode holds one sequence");
     }
-    if (!dev_.kernels_loaded()) dev_.load_kernels();
+    // each mode runs under its kernel set's ExecutionClass: fp32 the reference set, fast the fast set (a fast-set
+    // device also runs the fp32 mode, whose results it then classes as the fast set's)
+    const Device::KernelSet need = c.mode == 0 ? Device::KernelSet::Reference : Device::KernelSet::Fast;
+    if (!dev_.kernels_loaded()) dev_.load_kernels(need);
+    if (c.mode != 0 && dev_.kernel_set() != Device::KernelSet::Fast)
+        arg_fail("the fast mode needs a device with the fast kernel set loaded (lrm_hip_load_kernel_set, "
+                 "LRM_HIP_KERNELS_FAST); this one has the reference set");
     plan();
     upload_rope(inv_freq_bits);
 }

@@ -402,9 +402,14 @@ class HipBackend:
         self.heap = HipHeap(self, layout)
         return self.heap
 
-    def load_kernels(self) -> bytes:
+    KERNEL_SETS = {"reference": 0, "fast": 1}
+
+    def load_kernels(self, kernel_set: str = "reference") -> bytes:
+        """LoadKernels, once per backend: "reference" (catalog ids 0-13, the BatchInvariance contract) or "fast"
+        (every id, its own ExecutionClass: same work, same inputs, same bits, and no more). Returns the set's
+        shader-set hash."""
         h = C.create_string_buffer(32)
-        check(lib().lrm_hip_load_kernels(self._h, h))
+        check(lib().lrm_hip_load_kernel_set(self._h, self.KERNEL_SETS[kernel_set], h))
         self.shader_set_hash = h.raw
         return h.raw
 

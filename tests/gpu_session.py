@@ -17,7 +17,7 @@ class Session:
     def __init__(self, tensors: dict, backend: HipBackend = None):
         """tensors: name -> (dtype, shape, flags, initial ndarray or None)."""
         self.backend = backend or HipBackend(0)
-        self.backend.load_kernels()
+        self.backend.load_kernels("fast")  # every id: the cases dispatch catalog and fast kernels alike
         planner = HeapPlanner()
         self.spec = tensors
         places = {}

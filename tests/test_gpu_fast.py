@@ -38,7 +38,7 @@ def hwiden(h):
 # ---------------------------------------------------------------- prefill kernels
 
 @pytest.mark.parametrize("m,n,k", [(128, 128, 64), (512, 1024, 1024), (37, 300, 192), (2048, 2048, 1024),
-                                   (300, 200, 128), (2048, 1024, 3072)])
+                                   (300, 200, 128), (2048, 1024, 3072), (4000, 1024, 1024)])
 def test_gemm_f32_and_residual(m, n, k):
     """f32 and residual epilogues over whole and partial tiles; the residual GEMMs with few tiles and an even number
     of 64-wide k steps (1024, 128, 3072) run with K split between two wave groups of the block."""
@@ -64,7 +64,7 @@ def test_gemm_f32_and_residual(m, n, k):
 
 @pytest.mark.parametrize("m,n,k,splits", [(2048, 1024, 3072, 2), (512, 1024, 2048, 8), (300, 256, 512, 4),
                                           (128, 512, 1024, 1), (77, 1024, 1024, 2), (16, 2048, 6144, 2),
-                                          (5, 2048, 2048, 2), (16, 1024, 4096, 4)])
+                                          (5, 2048, 2048, 2), (16, 1024, 4096, 4), (4000, 1024, 3072, 2)])
 def test_gemm_residual_split_and_add_norm(m, n, k, splits):
     """The k-split residual GEMM: each split's partial product against float64 (whole and partial tiles, the
     direct-to-LDS loop at 512 blocks and the register loop otherwise, the skinny form for m <= 16); residual_add_norm: x + p0 + p1 + ... in split

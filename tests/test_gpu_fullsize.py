@@ -6,6 +6,9 @@
   * a 128-token prompt then 256 greedy tokens: the device's greedy ids are the oracle's greedy ids (the oracle's
     argmax along the device's sequence equals the device's id at every step, up to near-ties), and teacher-forced
     decode steps along that sequence match the oracle's logits.
+  * the 4K-context regime of the batch-1 decode: a 4096-token prefill (two 2048-row chunks), then 8 persistent decode
+    steps at context 4097..4104 (22 attention splits of three 64-key chunks each), every step's logits against the
+    oracle run over the device's own prefill caches, and the cache rows the device wrote against the oracle's.
 - Qwen3-1.7B shape (hidden 2048, SwiGLU 6144), 16 sequences whose caches hold 8192 positions of N(0, 1) fp16 values
   (written on the device), two batched decode steps: sequences 0, 7 and 15 against the oracle run over the same
   caches read back from the device.
@@ -96,6 +99,78 @@ def test_qwen3_0_6b_greedy_128_plus_256(qwen06b):
     assert same.mean() >= TOP1
     # every step where the device's greedy id is not the oracle's argmax is a near-tie in the oracle's logits
     assert np.all(ol[~same, oracle_ids[~same]] - ol[~same, g[~same]] <= 2 * err)
+
+
+def _row_err(dev, ref):
+    """Largest |dev - ref| of any row relative to max(1, that row's largest |ref|): fp16 storage of the device's
+    cache rows against the oracle's float32 rows."""
+    scale = np.maximum(1.0, np.max(np.abs(ref), axis=-1, keepdims=True))
+    return float(np.max(np.abs(dev - ref) / scale))
+
+
+def test_qwen3_0_6b_decode_at_4k_context():
+    """The 4K regime of batch-1 decode (the context the decode roofline bar is quoted at): a 4096-token prompt
+    prefilled on the device in two 2048-row chunks, then 8 greedy decode steps through the persistent step at context
+    4097..4104, where each of a KV head's 22 attention splits holds three 64-key chunks.
+
+    - The decode steps: the oracle is run over the device's own K/V caches for positions 0..4095 (read back), fed the
+      device's ids, and each step's logits are compared with the device's (max-abs, top-1, near-ties); the rows the
+      steps append to every layer's caches are compared with the oracle's.
+    - The prefill: the oracle's own prefill of the first 256 tokens gives every layer's cache rows 0..255 exactly;
+      the oracle's forward of tokens 4032..4095 over the device's rows 0..4031 gives rows 4032..4095 (the end of the
+      second chunk) and the last row's logits, compared with the device's."""
+    cfg = QwenConfig.qwen3_0_6b(max_pos=4160)
+    T, steps, tail = 4096, 8, 4032
+    w = synthetic_weights(cfg, seed=41)
+    ids = synthetic_ids(41, "fullsize/ctx4k", T, cfg.vocab)
+    b = HipBackend(0)
+    m = QwenModel(b, cfg, mode="fast", max_tokens=2048)
+    try:
+        m.load_weights(w)
+        assert m.persistent_decode()
+        print("0.6B 4K: prefill of 4096 tokens, then 8 persistent decode steps", flush=True)
+        lg_pre, nxt = m.forward(ids, 0, logits_rows=1)
+        m.decode_set(int(nxt), T)
+        dev_rows, dev_ids = [], []
+        for s in range(steps):
+            m.decode_run(1)
+            dev_rows.append(m.read_logits(1)[0])
+            dev_ids.append(int(m.decode_ids(s + 1)[s]))
+            assert dev_ids[-1] == int(np.argmax(dev_rows[-1])), s
+        kd = np.stack([m.read_cache(l, "k", 0, T + steps) for l in range(cfg.layers)])
+        vd = np.stack([m.read_cache(l, "v", 0, T + steps) for l in range(cfg.layers)])
+    finally:
+        m.close()
+        b.close()
+    assert np.isfinite(kd).all() and np.isfinite(vd).all()
+
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), cfg.max_pos)
+    orc = cpuref.QwenOracle(cfg.oracle_dict(), w, cos, sin)
+    # the prefill's first rows: the oracle's own prefill of the first 256 tokens
+    kc, vc = orc.new_cache()
+    orc.forward((kc, vc), 0, ids[:256])
+    head = max(_row_err(kd[:, :256], kc[:, :256]), _row_err(vd[:, :256], vc[:, :256]))
+    # the end of the second chunk over the device's rows 0..4031
+    kc[:, :tail], vc[:, :tail] = kd[:, :tail], vd[:, :tail]
+    ol_tail = orc.forward((kc, vc), tail, ids[tail:])
+    tail_rows = max(_row_err(kd[:, tail:T], kc[:, tail:T]), _row_err(vd[:, tail:T], vc[:, tail:T]))
+    pre_err = metrics.max_abs(lg_pre, ol_tail[-1:])
+    pre_ok, pre_gaps = _near_ties(lg_pre, ol_tail[-1:], max(pre_err, 1e-6))
+    # the decode steps over the device's prefill rows, fed the device's ids
+    kc[:, :T], vc[:, :T] = kd[:, :T], vd[:, :T]
+    feed = [int(nxt)] + dev_ids[:-1]
+    ol = np.concatenate([orc.forward((kc, vc), T + s, np.array([feed[s]], np.int32)) for s in range(steps)])
+    lg = np.stack(dev_rows)
+    err, top1 = metrics.max_abs(lg, ol), metrics.top1_agreement(lg, ol)
+    ok, gaps = _near_ties(lg, ol, err)
+    appended = max(_row_err(kd[:, T:], kc[:, T:T + steps]), _row_err(vd[:, T:], vc[:, T:T + steps]))
+    print(f"0.6B 4K: prefill cache rows 0..255 within {head:.3g}, rows 4032..4095 within {tail_rows:.3g}; last "
+          f"prefill row max-abs {pre_err:.4g} (id {nxt}, oracle {int(np.argmax(ol_tail[-1]))}); decode at "
+          f"4097..4104: max-abs {err:.4g}, top-1 {top1:.4f} (ids {dev_ids}, oracle {np.argmax(ol, axis=1).tolist()}), "
+          f"flip gaps {np.round(gaps, 5).tolist()}; appended rows within {appended:.3g}", flush=True)
+    assert head <= 1e-2 and tail_rows <= 1e-2 and appended <= 1e-2
+    assert pre_err <= MAX_ABS and pre_ok
+    assert err <= MAX_ABS and top1 >= TOP1 and ok
 
 
 def test_qwen3_1_7b_batch16_context_8192():
