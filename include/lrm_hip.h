@@ -120,6 +120,12 @@ int lrm_hip_load_kernels(lrm_hip_device *d, uint8_t shader_set_hash[32]);
 #define LRM_HIP_KERNELS_FAST 1u
 int lrm_hip_load_kernel_set(lrm_hip_device *d, uint32_t set, uint8_t shader_set_hash[32]);
 int lrm_hip_contains(lrm_hip_device *d, uint32_t kernel); /* 1 or 0 */
+/* Diagnostics, no counterpart in the reference: the per-workgroup stamps of the prefill GEMMs' direct-to-LDS loop
+ * recorded by the stage-timing build of this library (python -m rosylnalive_amd.build --stamps), for the last launch
+ * of each GEMM kind (kind = epilogue: 0 f32, 1 residual, 2 SwiGLU, 3 q|k|v, 4 k-split partials). 32 words per
+ * workgroup (linear block id): word 0 = (XCC_ID << 32) | HW_ID, 1 start, 2 + kt tile kt landed, 30 main loop end, 31
+ * epilogue end, in 100 MHz constant-clock ticks. The shipped build records nothing and returns LRM_E_ARG. */
+int lrm_hip_debug_gemm_stamps(lrm_hip_device *d, uint32_t kind, uint64_t *dst, uint64_t words);
 int lrm_hip_denormal_probe(lrm_hip_device *d, int *mode, uint32_t results[7]);
 
 /* ICommandList (Backend.fs:125-136) and IGpuBackend.Begin/Submit/Wait (Backend.fs:148-153). A list created with

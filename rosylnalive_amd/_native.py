@@ -119,6 +119,7 @@ PROTOTYPES = {
     "lrm_hip_download": (C.c_int, [P, C.c_int, C.c_uint64, P, C.c_uint64]),
     "lrm_hip_load_kernels": (C.c_int, [P, P]),
     "lrm_hip_load_kernel_set": (C.c_int, [P, C.c_uint32, P]),
+    "lrm_hip_debug_gemm_stamps": (C.c_int, [P, C.c_uint32, P, C.c_uint64]),
     "lrm_hip_contains": (C.c_int, [P, C.c_uint32]),
     "lrm_hip_denormal_probe": (C.c_int, [P, C.POINTER(C.c_int), U32P]),
     "lrm_hip_begin": (C.c_int, [P, C.c_int, C.POINTER(P)]),

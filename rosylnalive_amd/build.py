@@ -64,7 +64,7 @@ def build(verbose: bool = False, stamps: bool = False) -> str:
     cxx = shutil.which("g++") or "g++"
     build_dir = os.path.join(STAMPS_DIR, "_build") if stamps else BUILD
     lib_path = STAMPS_LIB if stamps else LIB
-    extra = ["-DLRM_PERSIST_STAMPS"] if stamps else []
+    extra = ["-DLRM_PERSIST_STAMPS", "-DLRM_GEMM_STAMPS"] if stamps else []
     os.makedirs(build_dir, exist_ok=True)
     jobs = []
     for s in HIP_SOURCES:

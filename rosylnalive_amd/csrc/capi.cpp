@@ -332,6 +332,17 @@ int lrm_hip_load_kernel_set(lrm_hip_device* d, uint32_t set, uint8_t hash[32]) {
     });
 }
 
+int lrm_hip_debug_gemm_stamps(lrm_hip_device* d, uint32_t kind, uint64_t* dst, uint64_t words) {
+    return guard([&] {
+        need_ptr(d, "device");
+        need_ptr(dst, "dst");
+        hip_check(hipSetDevice(d->d.index()), "hipSetDevice");
+        if (!gemm_stamps_read(int(kind), dst, size_t(words)))
+            throw std::invalid_argument("no GEMM stamps: this library is not the stage-timing build, or kind " +
+                                        std::to_string(kind) + " / " + std::to_string(words) + " words is out of range");
+    });
+}
+
 int lrm_hip_contains(lrm_hip_device* d, uint32_t kernel) {
     if (!d) return 0;
     return d->d.kernels_loaded() && d->d.contains(int(kernel)) ? 1 : 0;

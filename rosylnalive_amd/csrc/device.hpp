@@ -55,6 +55,7 @@ void record_decode_attention_static(Device& dev, CommandList* l, const uint32_t*
 // sticky bits of the sites where a kernel stored an inf or NaN half (1 normed hidden rows, 2 q, 4 K/V cache, 8 attention
 // output, 16 SwiGLU output).
 void* f16_range_word_fast();
+bool gemm_stamps_read(int kind, uint64_t* dst, size_t words);  // kernels_fast.hip: the stage-timing build's stamps
 void* f16_range_word_persist();
 // The site names of a set of those bits, comma-separated.
 std::string f16_range_sites(uint32_t bits);
@@ -183,6 +184,7 @@ class Device {
     void release(CommandList* list);  // frees a list; the caller releases every list it began
 
     hipStream_t stream() const { return stream_; }
+    int index() const { return index_; }
     // This device's copy of the library's static scratch array (its address from hipGetSymbolAddress at creation)
     void* static_scratch() const { return static_scratch_; }
     // The fp16 range sites (bits as f16_range_word_fast) that kernels on this GPU flagged since the last call, then

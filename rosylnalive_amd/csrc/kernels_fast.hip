@@ -200,6 +200,39 @@ struct GemmArgs {
     int ksplit;
 };
 
+// The stage-timing build (LRM_GEMM_STAMPS): wave 0 of every block of the direct-to-LDS loop records constant-clock
+// stamps, per GEMM kind (the epilogue), of the last launch of that kind: word 0 the hardware CU (HW_ID) and XCD
+// (XCC_ID) ids, 1 the block's start, 2 + kt tile kt landed (after the step's wait and barrier, kt < kGemmStampSteps),
+// 30 the main loop's end, 31 the epilogue's end. Lane k of wave 0 keeps stamp k in a register (one select per stamp)
+// and the lanes store them once, at the end, so no stamp store is in flight while the block runs; the shipped build
+// has none.
+#if defined(LRM_GEMM_STAMPS)
+constexpr int kGemmStampWords = 32, kGemmStampSteps = 28, kGemmStampBlocks = 4096, kGemmStampKinds = 5;
+__device__ uint64_t g_gemm_stamps[kGemmStampKinds][kGemmStampBlocks * kGemmStampWords];
+struct GemmStampEnd {  // the epilogue's end, at whichever return the lane leaves by
+    uint64_t* at;
+    uint64_t& v;
+    int lane;
+    __device__ ~GemmStampEnd() {
+        if (at && lane < kGemmStampWords) {
+            const uint64_t e = wall_clock64();
+            at[lane] = lane == kGemmStampWords - 1 ? e : v;
+        }
+    }
+};
+#define GSTAMP(k)                                   \
+    do {                                            \
+        if (gst) {                                  \
+            const uint64_t now_ = wall_clock64();   \
+            gsv = lane == (k) ? now_ : gsv;         \
+        }                                           \
+    } while (0)
+#else
+#define GSTAMP(k) \
+    do {          \
+    } while (0)
+#endif
+
 // Two main loops, chosen by the launcher: DMA (a grid of at least two blocks per CU) moves tiles from memory
 // straight into two LDS stages, the two blocks on a CU hiding each other's load latency; otherwise (one block per CU)
 // tiles go through two register sets into two padded LDS buffers with every load two k steps ahead.
@@ -242,6 +275,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     }
     const int m0 = ty * BM;
     const int n0 = tx * BN;
+#if defined(LRM_GEMM_STAMPS)
+    uint64_t* gst = nullptr;  // wave 0 of a direct-to-LDS block: where its stamps go
+    uint64_t gsv = 0;         // lane k: stamp k
+    {
+        const int Lb = (int(blockIdx.z) * int(gridDim.y) + int(blockIdx.y)) * int(gridDim.x) + int(blockIdx.x);
+        if (DMA && w == 0 && Lb < kGemmStampBlocks) {
+            gst = g_gemm_stamps[EPI] + size_t(Lb) * kGemmStampWords;
+            const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4), xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20);
+            gsv = lane == 0 ? (uint64_t(xcc) << 32) | hw : 0;
+        }
+    }
+    GSTAMP(1);
+    GemmStampEnd gst_end{gst, gsv, lane};
+#endif
 
     f32x4 acc[MI][JT];
 #pragma unroll
@@ -317,9 +364,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         for (int kt = 0; kt < nk; ++kt) {
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile kt have landed in LDS
             lds_barrier();
+#if defined(LRM_GEMM_STAMPS)
+            if (kt < kGemmStampSteps) GSTAMP(2 + kt);
+#endif
             if (kt + 1 < nk) issue((kt + 1) & 1, (kt + 1) * GBK);  // uniform
             compute(kt & 1);
         }
+        GSTAMP(30);
     } else {
         // the rows this thread loads: chunk c = t + 256 i -> row c / 8, 16-byte column (c % 8), as element offsets from
         // the matrix base (every matrix is under 2^31 elements). A row past the matrix is clamped to its last row: it only
@@ -485,6 +536,27 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     if constexpr (EPI == EPI_QKV) {
         const int head = tx;
         if (head < p.qh + p.kvh) {
+            const bool is_q = head < p.qh;
+            const int row = t >> 1, hf = t & 1, m = m0 + row;
+            // Every global load of the epilogue first: the norm weights and this row's cos / sin (the row clamped to
+            // the last one for rows past M, which store nothing), so their latency runs under the staging below and is
+            // paid once. (Loaded between the stores, which the compiler may not reorder them across, the four groups
+            // each waited a whole load latency: 7.8 of a 24.5 us block at 2048 x 4096 x 1024.)
+            const int pos = p.pos0 + min(m, p.M - 1);
+            const uint16_t* nw = (is_q ? p.qn : p.kn) + hf * 32;
+            const float* cst = p.cos_t + size_t(pos) * 64 + hf * 32;
+            const float* snt = p.sin_t + size_t(pos) * 64 + hf * 32;
+            u32x4 wlv[4], whv[4];
+            f32x4 c0v[4], c1v[4], s0v[4], s1v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                wlv[u] = *reinterpret_cast<const u32x4*>(nw + 8 * u);
+                whv[u] = *reinterpret_cast<const u32x4*>(nw + 64 + 8 * u);
+                c0v[u] = *reinterpret_cast<const f32x4*>(cst + 8 * u);
+                c1v[u] = *reinterpret_cast<const f32x4*>(cst + 8 * u + 4);
+                s0v[u] = *reinterpret_cast<const f32x4*>(snt + 8 * u);
+                s1v[u] = *reinterpret_cast<const f32x4*>(snt + 8 * u + 4);
+            }
             float* tile = reinterpret_cast<float*>(lds);
 #pragma unroll
             for (int i = 0; i < MI; ++i)
@@ -492,12 +564,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                 for (int j = 0; j < JT; ++j)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int row = wm * (BM / 2) + i * 16 + 4 * g + r, col = wn * WN + j * 16 + c16;
-                        tile[row * 128 + (col ^ ((row & 15) << 2))] = acc[i][j][r];
+                        const int rw = wm * (BM / 2) + i * 16 + 4 * g + r, col = wn * WN + j * 16 + c16;
+                        tile[rw * 128 + (col ^ ((rw & 15) << 2))] = acc[i][j][r];
                     }
-            __syncthreads();
-            const bool is_q = head < p.qh;
-            const int row = t >> 1, hf = t & 1, m = m0 + row;
+            lds_barrier();  // LDS only: the loads above stay in flight
             if (row >= BM) return;  // 64-row tiles: threads 128 .. 255 have no row
             float x[2][32];
 #pragma unroll
@@ -514,23 +584,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             for (int k = 0; k < 32; ++k) ss = fmaf(x[1][k], x[1][k], fmaf(x[0][k], x[0][k], ss));
             ss += dpp_f<0xB1>(ss);  // + the other half of the row (lane t ^ 1)
             if (m >= p.M) return;
-            const int pos = p.pos0 + m;
             const float rr = 1.0f / sqrtf(ss / 128.0f + p.eps);
-            const uint16_t* nw = (is_q ? p.qn : p.kn) + hf * 32;
-            const float* cst = p.cos_t + size_t(pos) * 64 + hf * 32;
-            const float* snt = p.sin_t + size_t(pos) * 64 + hf * 32;
             uint16_t* out = is_q ? p.q_out + size_t(m) * (p.qh * 128) + head * 128
                                  : p.kc + (size_t(head - p.qh) * p.max_pos + pos) * 128;
             out += hf * 32;
             uint32_t bad = 0;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {  // 8 dims d = 32 hf + 8 u + e and their partners d + 64
-                const u32x4 wl = *reinterpret_cast<const u32x4*>(nw + 8 * u);
-                const u32x4 wh = *reinterpret_cast<const u32x4*>(nw + 64 + 8 * u);
-                const f32x4 c0 = *reinterpret_cast<const f32x4*>(cst + 8 * u);
-                const f32x4 c1 = *reinterpret_cast<const f32x4*>(cst + 8 * u + 4);
-                const f32x4 s0 = *reinterpret_cast<const f32x4*>(snt + 8 * u);
-                const f32x4 s1 = *reinterpret_cast<const f32x4*>(snt + 8 * u + 4);
+                const u32x4 wl = wlv[u], wh = whv[u];
+                const f32x4 c0 = c0v[u], c1 = c1v[u], s0 = s0v[u], s1 = s1v[u];
                 uint32_t lo[4], hi[4];
 #pragma unroll
                 for (int e2 = 0; e2 < 4; ++e2) {
@@ -557,46 +619,55 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         }
     }
 
-    // SWIGLU and the V heads of QKV pair column c (wave wn = 0) with column c + PAIR (wave wn = 1, same lane and tile
-    // index): the second half goes through LDS to the first.
-    float* x32 = reinterpret_cast<float*>(lds);  // 2 (wm) x 4 JT x 4 values x 64 lanes: 32 KiB (JT 4), 48 KiB (JT 6)
-    if (wn == 1) {
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int j = 0; j < JT; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) x32[((wm * MI * JT + i * JT + j) * 4 + r) * 64 + lane] = acc[i][j][r];
-    }
-    __syncthreads();
-    const int head = tx;  // QKV: a V head (the q and k heads returned above)
-    // the partner half of row tile i, read back from LDS
-    auto load_hi = [&](int i, float (&hi)[JT][4]) {
-#pragma unroll
-        for (int j = 0; j < JT; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) hi[j][r] = x32[((wm * MI * JT + i * JT + j) * 4 + r) * 64 + lane];
-    };
-
-    if (EPI == EPI_SWIGLU) {
-        // a[m, j0 + c] = silu(gate) * up, silu(g) = g / (1 + exp(-g)), into an fp16 tile in LDS after x32 (rows of PAIR
-        // columns padded by 8), then out as 16-byte row chunks by all four waves
-        constexpr int AR = PAIR + 8, CH = PAIR / 8;  // LDS row stride (halves), 16-byte chunks per row
+    if constexpr (EPI == EPI_SWIGLU) {
+        // a[m, j0 + c] = silu(gate) * up, silu(g) = g / (1 + exp(-g)). The gate column c (wave wn = 0) and its up
+        // column c + PAIR (wave wn = 1, same lane and tile index) meet through LDS, half the row tiles each way, so
+        // every wave computes: wave wn takes row tiles [wn MI / 2, (wn + 1) MI / 2). Values cross as 16-byte units
+        // (an MFMA tile's 4 rows per lane). The products go to an fp16 tile in LDS after the exchange area (rows of
+        // PAIR columns padded by 8), then out as 16-byte row chunks by all four waves. (Two waves with an IEEE
+        // division per value took 6 us of a 27 us block at 2048 x 3072 x 1024.)
+        constexpr int HM = MI / 2, AR = PAIR + 8, CH = PAIR / 8;  // LDS row stride (halves), 16-byte chunks per row
+        f32x4* xq = reinterpret_cast<f32x4*>(lds);  // [wm][dir][HM][JT][64 lanes]: same size as 2 x MI x JT x 1 KiB
         uint16_t* As = lds + 2 * MI * 4 * JT * 64 * 2;
+        auto slot = [&](int dir, int i, int j) { return ((wm * 2 + dir) * HM * JT + i * JT + j) * 64 + lane; };
+        if (wn == 0) {  // dir 1: the gate values of row tiles HM .. MI - 1, to wave wn = 1
+#pragma unroll
+            for (int i = 0; i < HM; ++i)
+#pragma unroll
+                for (int j = 0; j < JT; ++j) xq[slot(1, i, j)] = acc[HM + i][j];
+        } else {  // dir 0: the up values of row tiles 0 .. HM - 1, to wave wn = 0
+#pragma unroll
+            for (int i = 0; i < HM; ++i)
+#pragma unroll
+                for (int j = 0; j < JT; ++j) xq[slot(0, i, j)] = acc[i][j];
+        }
+        __syncthreads();
+        const int rt0 = wn * HM;  // this wave's first row tile
+        auto emit = [&](int i, int j, const f32x4& gv4, const f32x4& uv4) __attribute__((always_inline)) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float gv = gv4[r];
+                const float sg = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv));
+                As[(wm * (BM / 2) + (rt0 + i) * 16 + 4 * g + r) * AR + j * 16 + c16] = f2h(sg * uv4[r]);
+            }
+        };
+        // the partner's values first, all of them: read between the product stores, each read would wait for the
+        // stores before it (the compiler cannot tell the two LDS regions apart)
+        f32x4 other[HM][JT];
+#pragma unroll
+        for (int i = 0; i < HM; ++i)
+#pragma unroll
+            for (int j = 0; j < JT; ++j) other[i][j] = xq[slot(wn == 0 ? 0 : 1, i, j)];
         if (wn == 0) {
 #pragma unroll
-            for (int i = 0; i < MI; ++i) {
-                float hi[JT][4];
-                load_hi(i, hi);
+            for (int i = 0; i < HM; ++i)
 #pragma unroll
-                for (int j = 0; j < JT; ++j)
+                for (int j = 0; j < JT; ++j) emit(i, j, acc[i][j], other[i][j]);
+        } else {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float gv = acc[i][j][r];
-                        const float sg = gv / (1.0f + __expf(-gv));
-                        As[(wm * (BM / 2) + i * 16 + 4 * g + r) * AR + j * 16 + c16] = f2h(sg * hi[j][r]);
-                    }
-            }
+            for (int i = 0; i < HM; ++i)
+#pragma unroll
+                for (int j = 0; j < JT; ++j) emit(i, j, other[i][j], acc[HM + i][j]);
         }
         __syncthreads();
         uint32_t bad = 0;
@@ -620,6 +691,28 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         f16_note(bad, kF16Swiglu);
         return;
     }
+
+
+    // The V heads of QKV pair column c (wave wn = 0) with column c + PAIR (wave wn = 1, same lane and tile index): the
+    // second half goes through LDS to the first.
+    float* x32 = reinterpret_cast<float*>(lds);  // 2 (wm) x 4 JT x 4 values x 64 lanes: 32 KiB (JT 4), 48 KiB (JT 6)
+    if (wn == 1) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < JT; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x32[((wm * MI * JT + i * JT + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    const int head = tx;  // QKV: a V head (the q and k heads returned above)
+    // the partner half of row tile i, read back from LDS
+    auto load_hi = [&](int i, float (&hi)[JT][4]) {
+#pragma unroll
+        for (int j = 0; j < JT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) hi[j][r] = x32[((wm * MI * JT + i * JT + j) * 4 + r) * 64 + lane];
+    };
 
     if (EPI == EPI_QKV) {
         // V: the cache is V^T ([dim][position]), so the tile is transposed through LDS (after the 32 KiB of x32, rows
@@ -2145,6 +2238,22 @@ static uint32_t dec_splits(uint32_t max_pos, uint32_t chunks) {
 static uint32_t dec_grid_splits(uint32_t max_pos, uint32_t chunks, uint32_t splits) {
     return splits ? splits : dec_splits(max_pos, chunks);
 }
+// The GEMM stamps of the stage-timing build (kind = the epilogue, 0 .. 4; words <= kGemmStampBlocks x 32): false in
+// the shipped build, which records none.
+bool gemm_stamps_read(int kind, uint64_t* dst, size_t words) {
+#if defined(LRM_GEMM_STAMPS)
+    if (kind < 0 || kind >= kGemmStampKinds || words > size_t(kGemmStampBlocks) * kGemmStampWords) return false;
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    hip_check(hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_gemm_stamps), words * 8, size_t(kind) * kGemmStampBlocks * kGemmStampWords * 8,
+                                  hipMemcpyDeviceToHost),
+              "hipMemcpyFromSymbol(g_gemm_stamps)");
+    return true;
+#else
+    (void)kind, (void)dst, (void)words;
+    return false;
+#endif
+}
+
 void* f16_range_word_fast() {
     void* p = nullptr;
     hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(fast::f16_range_word)), "hipGetSymbolAddress(f16_range_word)");
