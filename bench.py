@@ -28,10 +28,39 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 FP32_PEAK_TFLOPS = 157.3
 GEMV_SWIGLU_TRAFFIC_BYTES = 12675736  # measured HBM bytes per gemv_swiglu_dec launch at the 0.6B shape
-PERSIST_TRAFFIC_BYTES = 1278457474    # measured HBM bytes per decode_step_persistent launch at context 393..424
+PERSIST_TRAFFIC_BYTES = 1281006770    # measured HBM bytes per decode_step_persistent launch at context 393..424
 ROOFLINE_POS0 = 392                   # the roofline launches run at context ROOFLINE_POS0 + 1 .. ROOFLINE_POS0 + 32
+COPY_BYTES = 1 << 30                  # the reference copy of the traffic calibration: 4 x the last-level cache
 CPU_DECODE_STEPS = 128                # the bounded CPU decode sample (about 10 s on 16 host cores)
 CTX4K_CHECK_STEPS = 8                 # decode steps of the 4K-context leg whose ids the oracle checks
+
+
+def reference_copy() -> float:
+    """scale_f32 (a = 1) over COPY_BYTES on a backend of its own: COPY_BYTES read and COPY_BYTES written, more than the
+    256 MB last-level cache holds, so every byte crosses HBM. The HBM byte counters (FETCH_SIZE, WRITE_SIZE) of a
+    profiling run are scaled by what they read for it. Returns its duration in microseconds (HIP events)."""
+    from rosylnalive_amd.gpu_core import Arena, ArgBlock, DType, HeapPlanner, HipBackend, TensorTable
+    b = HipBackend(0)
+    try:
+        b.load_kernels()
+        n = COPY_BYTES // 4
+        planner = HeapPlanner()
+        px, py = planner.allocate(Arena.ACTIVATIONS, COPY_BYTES), planner.allocate(Arena.ACTIVATIONS, COPY_BYTES)
+        layout = planner.build()
+        heap = b.create_heap(layout)
+        table = TensorTable(layout)
+        tx = table.add_placed("copy.x", px, DType.F32, [n])
+        ty = table.add_placed("copy.y", py, DType.F32, [n])
+        heap.write_table(table.seal())
+        cl = b.begin()
+        tm = cl.begin_timer("gpu.scale_f32")
+        cl.dispatch("scale_f32", ArgBlock.encode("scale_f32", x=tx, y=ty, n=n, a=1.0))
+        cl.end_timer(tm)
+        comp = b.wait(b.submit(cl))
+        cl.release()
+        return comp.timers[0].duration_ns / 1e3
+    finally:
+        b.close()
 
 
 def log(*a):
@@ -127,7 +156,7 @@ def main():
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill_2048", "prefill_512"],
+    ap.add_argument("--only", choices=["prefill_2048", "prefill_512", "attention_2048", "roofline"],
                     help="run only this workload (for profiling runs) and print its figures as the JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -167,7 +196,34 @@ def main():
         return {"ms": round(best, 3), "tok_s": round(T / (best / 1e3), 1), "tflops": round(fl / (best / 1e3) / 1e12, 1),
                 "mfma_frac": round(fl / (best / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flop": fl}
 
-    if args.only:
+    def attention_2048():
+        """The isolated GQA prefill attention at T = 2048 on the caches a 2048-token prefill wrote, each layer's in
+        turn, 28 launches in one list timed with HIP events."""
+        tok = model.token
+        cl = backend.begin()
+        tm = cl.begin_timer("gpu.attention_prefill_f16")
+        for i in range(L):
+            cl.dispatch("attention_prefill_f16", ArgBlock.encode(
+                "attention_prefill_f16", q=tok("q"), k_cache=tok(f"L{i}.k_cache"), v_cache=tok(f"L{i}.v_cache"),
+                y=tok("o"), workspace=tok("attn.ws"), rows=2048, past=0, q_heads=QH, kv_heads=KVH,
+                max_pos=cfg.max_pos, scale=float(np.float32(HD ** -0.5))))
+        cl.end_timer(tm)
+        comp = backend.wait(backend.submit(cl))
+        cl.release()
+        a_us = comp.timers[0].duration_ns / 1e3 / L
+        a_fl = QH * (2048 * 2049 // 2) * (4 * HD + 3)
+        return {"us": round(a_us, 2), "tflops": round(a_fl / (a_us * 1e-6) / 1e12, 1),
+                "mfma_frac": round(a_fl / (a_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4), "flop": a_fl}
+
+    if args.only == "attention_2048":
+        prefill(2048, 1, "bench/prefill2048")
+        res = min((attention_2048() for _ in range(3)), key=lambda r: r["us"])
+        log(args.only, res)
+        print(json.dumps({"workload": args.only, **res}), flush=True)
+        model.close()
+        backend.close()
+        return
+    if args.only in ("prefill_2048", "prefill_512"):
         T, rows = (2048, 1) if args.only == "prefill_2048" else (512, 512)
         res = prefill(T, rows, "bench/" + args.only.replace("_", ""))
         log(args.only, res)
@@ -176,33 +232,14 @@ def main():
         backend.close()
         return
 
-    # ---------------------------------------------------------------- headline: decode, context 128 + ...
-    prompt = synthetic_ids(args.seed, "bench/prompt", 128, V)
-    _, first = model.forward(prompt, 0, logits_rows=1)
-    model.decode_set(int(first), 128)
-    if args.warmup:
-        model.decode_run(args.warmup)
-    ctx0 = 128 + args.warmup
-    t1 = time.perf_counter()
-    model.decode_run(args.steps)
-    wall = time.perf_counter() - t1
-    dev_ms = model.last_ms()
-    # the greedy ids of the run (the prefill's, then every decode step's), checked against the oracle's below
-    gpu_ids = [int(first)] + model.decode_ids(args.warmup + args.steps).tolist()
-    tok_s = args.steps / (dev_ms / 1e3)
-    step_bytes = sum(weight_bytes + kv_bytes(ctx0 + s + 1) for s in range(args.steps))
-    log(f"decode: {args.steps} steps in {dev_ms:.2f} ms device ({wall * 1e3:.2f} ms wall): {tok_s:.1f} tok/s, "
-        f"{step_bytes / (dev_ms / 1e3) / 1e9:.0f} GB/s algorithmic")
-
     # ---------------------------------------------------------------- dominant kernel roofline
     # The decode step is one launch of decode_step_persistent (the whole token: every layer, the lm_head and the
     # argmax): its duration per launch, from HIP events on the device stream around `reps` launches recorded in one
     # list, against the algorithmic bytes of each launch (every weight once, the KV cache up to its position, the
     # appended K/V rows and the logits row).
     tok = model.token
-    persistent = model.persistent_decode()
-    pk = None
-    if persistent:
+
+    def persist_roofline():
         # at a fixed context, 393..424, whatever --steps is (the context the traffic profile was taken at): a prefill
         # of 392 tokens writes the caches the launches read
         reps = 32
@@ -227,9 +264,43 @@ def main():
         cl.release()
         p_us = comp.timers[0].duration_ns / 1e3 / reps
         p_bytes = sum(weight_bytes + kv_bytes(pos0 + r + 1) + 2 * L * KVH * HD * 2 + V * 4 for r in range(reps)) / reps
-        pk = {"us": p_us, "bytes": p_bytes, "gbs": p_bytes / (p_us * 1e-6) / 1e9}
+        res = {"us": p_us, "bytes": p_bytes, "gbs": p_bytes / (p_us * 1e-6) / 1e9}
         log(f"decode_step_persistent: {p_us:.2f} us per launch at context {pos0 + 1}..{pos0 + reps}, "
-            f"{pk['gbs']:.0f} GB/s ({pk['gbs'] / HBM_PEAK_GBS:.1%} of HBM peak)")
+            f"{res['gbs']:.0f} GB/s ({res['gbs'] / HBM_PEAK_GBS:.1%} of HBM peak)")
+        return res
+
+    persistent = model.persistent_decode()
+    if args.only == "roofline":
+        pk = persist_roofline() if persistent else None
+        c_us = reference_copy()
+        log(f"reference copy (scale_f32, 1 GiB read + 1 GiB written): {c_us:.1f} us, "
+            f"{2 * COPY_BYTES / (c_us * 1e-6) / 1e9:.0f} GB/s")
+        print(json.dumps({"workload": "roofline", "decode_step_persistent_us": round(pk["us"], 3) if pk else None,
+                          "bytes_per_launch": int(pk["bytes"]) if pk else None, "copy_us": round(c_us, 2)}),
+              flush=True)
+        model.close()
+        backend.close()
+        return
+
+    # ---------------------------------------------------------------- headline: decode, context 128 + ...
+    prompt = synthetic_ids(args.seed, "bench/prompt", 128, V)
+    _, first = model.forward(prompt, 0, logits_rows=1)
+    model.decode_set(int(first), 128)
+    if args.warmup:
+        model.decode_run(args.warmup)
+    ctx0 = 128 + args.warmup
+    t1 = time.perf_counter()
+    model.decode_run(args.steps)
+    wall = time.perf_counter() - t1
+    dev_ms = model.last_ms()
+    # the greedy ids of the run (the prefill's, then every decode step's), checked against the oracle's below
+    gpu_ids = [int(first)] + model.decode_ids(args.warmup + args.steps).tolist()
+    tok_s = args.steps / (dev_ms / 1e3)
+    step_bytes = sum(weight_bytes + kv_bytes(ctx0 + s + 1) for s in range(args.steps))
+    log(f"decode: {args.steps} steps in {dev_ms:.2f} ms device ({wall * 1e3:.2f} ms wall): {tok_s:.1f} tok/s, "
+        f"{step_bytes / (dev_ms / 1e3) / 1e9:.0f} GB/s algorithmic")
+
+    pk = persist_roofline() if persistent else None  # the dominant kernel's roofline (defined above)
 
     # the fused gate/up SwiGLU GEMV of the per-stage decode list (the dominant kernel of that list)
     reps = 4
@@ -249,13 +320,9 @@ def main():
     k_gbs = k_bytes / (k_us * 1e-6) / 1e9
     log(f"gemv_swiglu_dec: {k_us:.2f} us per launch, {k_gbs:.0f} GB/s ({k_gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
 
-    # a plain copy of known size (scale_f32 by 1: 8 MiB read, 8 MiB written), the reference that the HBM byte
-    # counters of a profiling run are scaled by
-    cl = backend.begin()
-    n_copy = 2048 * H
-    cl.dispatch("scale_f32", ArgBlock.encode("scale_f32", x=tok("x"), y=tok("logits"), n=n_copy, a=1.0))
-    backend.wait(backend.submit(cl))
-    cl.release()
+    # a plain copy of known size larger than the last-level cache, the reference that the HBM byte counters of a
+    # profiling run are scaled by
+    reference_copy()
 
     out = {
         "metric": "Qwen3-0.6B prefill & decode tok/s on 1 MI355X; % of HBM/MFMA roofline",
@@ -283,8 +350,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(pk["gbs"] / HBM_PEAK_GBS, 4),
-            # HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the same counters on the 8 MiB
-            # copy below (profiles/decode_persistent_traffic_qwen3_0.6b.md)
+            # HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the same counters on the 1 GiB
+            # reference copy (profiles/decode_persistent_qwen3_0.6b.md)
             "traffic": PERSIST_TRAFFIC_BYTES,
             "bytes_per_launch": int(pk["bytes"]),
             "us_per_launch": round(pk["us"], 3),
@@ -323,22 +390,8 @@ def main():
         # 2048-token prefill, last-row logits
         out["prefill_2048"] = prefill(2048, 1, "bench/prefill2048")
         log("prefill 2048:", out["prefill_2048"])
-        # the isolated GQA prefill attention at T = 2048 on the caches the prefill just wrote (layer 0)
-        cl = backend.begin()
-        tm = cl.begin_timer("gpu.attention_prefill_f16")
-        for i in range(L):
-            cl.dispatch("attention_prefill_f16", ArgBlock.encode(
-                "attention_prefill_f16", q=tok("q"), k_cache=tok(f"L{i}.k_cache"), v_cache=tok(f"L{i}.v_cache"),
-                y=tok("o"), workspace=tok("attn.ws"), rows=2048, past=0, q_heads=QH, kv_heads=KVH,
-                max_pos=cfg.max_pos, scale=float(np.float32(HD ** -0.5))))
-        cl.end_timer(tm)
-        comp = backend.wait(backend.submit(cl))
-        cl.release()
-        a_us = comp.timers[0].duration_ns / 1e3 / L
-        a_fl = QH * (2048 * 2049 // 2) * (4 * HD + 3)
-        out["attention_prefill_2048"] = {"us": round(a_us, 2), "tflops": round(a_fl / (a_us * 1e-6) / 1e12, 1),
-                                         "mfma_frac": round(a_fl / (a_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                                         "flop": a_fl}
+        # the isolated GQA prefill attention at T = 2048 on the caches the prefill just wrote
+        out["attention_prefill_2048"] = attention_2048()
         log("attention 2048:", out["attention_prefill_2048"])
         # decode at 4096 context: a real 4096-token prefill (two chunks), then 64 decode steps
         ids = synthetic_ids(args.seed, "bench/ctx4k", 4096, V)
