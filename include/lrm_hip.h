@@ -211,6 +211,15 @@ double lrm_qwen_last_ms(lrm_qwen *q); /* device time of the last forward / decod
  * of per-stage kernels, -1 for a null model. No counterpart in the reference: its decode loop is the planned
  * Lrm.Gpu.Exec composition of per-op dispatches (docs/dev-plan.md:166-170), which the per-stage list mirrors. */
 int lrm_qwen_persistent_decode(lrm_qwen *q);
+/* Mode 1: the binades s by which the SwiGLU output is shifted down before it is stored as fp16 (a 2^-s; the down_proj
+ * GEMM multiplies its sums by 2^s, so every result equals the unshifted one while a 2^-s stays a normal fp16 number).
+ * 0 until a forward's SwiGLU output overflows fp16; that forward then runs again with s raised by 8, up to 16, and s
+ * stays for later calls until a weight is written. A decode call that overflows there fails and raises s for the calls
+ * after it. -1 for a null model. No counterpart in the reference, whose kernels keep these activations in float32. */
+int lrm_qwen_swiglu_shift(lrm_qwen *q);
+/* Sets s (0 .. 24) for the calls that follow, until a weight is written or an overflow raises it: for a checkpoint
+ * whose SwiGLU range is known ahead, which then needs no rerun. LRM_E_ARG outside that range or in mode 0. */
+int lrm_qwen_set_swiglu_shift(lrm_qwen *q, int shift);
 int lrm_qwen_token(lrm_qwen *q, const char *name, uint32_t *token);
 lrm_hip_device *lrm_qwen_device(lrm_qwen *q);
 int lrm_qwen_tap_count(lrm_qwen *q);

@@ -174,6 +174,8 @@ PROTOTYPES = {
     "lrm_qwen_read_logits": (C.c_int, [P, P, C.c_int]),
     "lrm_qwen_last_ms": (C.c_double, [P]),
     "lrm_qwen_persistent_decode": (C.c_int, [P]),
+    "lrm_qwen_swiglu_shift": (C.c_int, [P]),
+    "lrm_qwen_set_swiglu_shift": (C.c_int, [P, C.c_int]),
     "lrm_qwen_token": (C.c_int, [P, C.c_char_p, U32P]),
     "lrm_qwen_device": (P, [P]),
     "lrm_qwen_tap_count": (C.c_int, [P]),

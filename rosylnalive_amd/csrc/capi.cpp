@@ -563,6 +563,15 @@ double lrm_qwen_last_ms(lrm_qwen* q) { return q ? q->q.last_ms() : -1.0; }
 
 int lrm_qwen_persistent_decode(lrm_qwen* q) { return q ? (q->q.persistent_decode() ? 1 : 0) : -1; }
 
+int lrm_qwen_swiglu_shift(lrm_qwen* q) { return q ? q->q.swiglu_shift() : -1; }
+
+int lrm_qwen_set_swiglu_shift(lrm_qwen* q, int shift) {
+    return guard([&] {
+        need_ptr(q, "model");
+        q->q.set_swiglu_shift_checked(shift);
+    });
+}
+
 int lrm_qwen_token(lrm_qwen* q, const char* name, uint32_t* token) {
     return guard([&] {
         need_ptr(q, "model");

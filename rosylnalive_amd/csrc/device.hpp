@@ -59,6 +59,7 @@ bool gemm_stamps_read(int kind, uint64_t* dst, size_t words);  // kernels_fast.h
 void* f16_range_word_persist();
 // The site names of a set of those bits, comma-separated.
 std::string f16_range_sites(uint32_t bits);
+constexpr uint32_t kF16SiteSwiglu = 16u;  // the SwiGLU output's bit in that word
 
 struct DeviceInfo {
     int index;

@@ -198,6 +198,9 @@ struct GemmArgs {
     float eps;
     // PART: block z multiplies k range [z ksplit, (z + 1) ksplit) and writes its f32 partial to y32 + z M N
     int ksplit;
+    // SWIGLU stores a 2^-s, RESID and PART multiply their sums by 2^s: the SwiGLU output's fp16 range moved up by s
+    // binades (1 for s = 0, which changes no bit)
+    float ascale;
 };
 
 // The stage-timing build (LRM_GEMM_STAMPS): wave 0 of every block of the direct-to-LDS loop records constant-clock
@@ -522,7 +525,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                     int m = m0 + wm * (BM / 2) + i * 16 + 4 * g + r;
                     if (m >= p.M) continue;
                     size_t o = size_t(m) * p.N + n;
-                    y[o] = EPI == EPI_RESID ? p.resid[o] + acc[i][j][r] : acc[i][j][r];
+                    const float v = EPI == EPI_F32 ? acc[i][j][r] : acc[i][j][r] * p.ascale;
+                    y[o] = EPI == EPI_RESID ? p.resid[o] + v : v;
                 }
             }
         return;
@@ -648,7 +652,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
             for (int r = 0; r < 4; ++r) {
                 const float gv = gv4[r];
                 const float sg = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv));
-                As[(wm * (BM / 2) + (rt0 + i) * 16 + 4 * g + r) * AR + j * 16 + c16] = f2h(sg * uv4[r]);
+                As[(wm * (BM / 2) + (rt0 + i) * 16 + 4 * g + r) * AR + j * 16 + c16] = f2h(sg * uv4[r] * p.ascale);
             }
         };
         // the partner's values first, all of them: read between the product stores, each read would wait for the
@@ -1897,7 +1901,7 @@ enum SkEpi { SK_F32 = 0, SK_RESID = 1, SK_SWIGLU = 2, SK_PART = 3 };
 
 template <int EPI, int NT>
 __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const uint16_t* w, float* y32, uint16_t* y16,
-                                                     int M, int N, int K, int inter) {
+                                                     int M, int N, int K, int inter, float ascale) {
     static_assert(NT == 1 || NT == 2, "MFMA column tiles per block");
     static_assert(EPI != SK_SWIGLU || NT == 2, "SwiGLU pairs a gate and an up tile");
     __shared__ float red[kSkWaves][NT][256];
@@ -1984,7 +1988,7 @@ __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const ui
             uv += red[i][NT - 1][t];
         }
         if (row < M && col < inter) {
-            const uint16_t hv = f2h(gv / (1.0f + __expf(-gv)) * uv);
+            const uint16_t hv = f2h(gv / (1.0f + __expf(-gv)) * uv * ascale);
             f16_note(f16_bad2(hv), kF16Swiglu);
             y16[size_t(row) * inter + col] = hv;
         }
@@ -1997,6 +2001,7 @@ __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const ui
 #pragma unroll
     for (int i = 0; i < kSkWaves; ++i) v += red[i][tile][e];
     if (row >= M || col >= N) return;
+    if (EPI != SK_F32) v *= ascale;
     if (EPI == SK_RESID)
         y32[size_t(row) * N + col] += v;
     else if (EPI == SK_PART)
@@ -2075,6 +2080,14 @@ static void l_rmsnorm_f16(const PreparedDispatch& pd, void* const* p, hipStream_
 #undef L_RMS
 }
 
+// The SwiGLU output's shift s (catalog field a_shift, at most kMaxAShift): its producers store a 2^-s, its consumers
+// multiply their sums by 2^s. Powers of two scale exactly, so the results equal the unshifted ones wherever a 2^-s
+// stays a normal fp16 number (|a| >= 2^(s - 14)); below that a keeps 2^(s - 24) of absolute precision.
+constexpr uint32_t kMaxAShift = 24;
+static_assert(fast::kF16Swiglu == kF16SiteSwiglu, "the host's SwiGLU range bit");
+static float a_scale(uint32_t s) { return std::ldexp(1.0f, -int(s)); }
+static float a_unscale(uint32_t s) { return std::ldexp(1.0f, int(s)); }
+
 static GemmArgs gemm_base(void* const* p, uint32_t m, uint32_t n, uint32_t k) {
     GemmArgs a{};
     a.a = (const uint16_t*)p[0];
@@ -2082,6 +2095,7 @@ static GemmArgs gemm_base(void* const* p, uint32_t m, uint32_t n, uint32_t k) {
     a.M = int(m);
     a.N = int(n);
     a.K = int(k);
+    a.ascale = 1.0f;
     return a;
 }
 
@@ -2137,12 +2151,13 @@ static void l_attn_prefill(const PreparedDispatch& pd, void* const* p, hipStream
 // grid covers the CUs.
 static bool resid_narrow(uint32_t m, uint32_t n) { return ((m + 127) / 128) * ((n + 127) / 128) < 512; }
 
-// 17 gemm_residual: a, w, x, m, n, k
+// 17 gemm_residual: a, w, x, m, n, k, a_shift
 static void l_gemm_resid(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     GemmArgs a = gemm_base(p, w[4], w[5], w[6]);
     a.y32 = (float*)p[2];
     a.resid = (const float*)p[2];
+    a.ascale = a_unscale(w[7]);
     if (resid_narrow(w[4], w[5]))  // under two blocks per CU by construction
         hipLaunchKernelGGL((k_gemm<EPI_RESID, 64, false>), dim3((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM), dim3(256), 0, s,
                            a);
@@ -2163,12 +2178,13 @@ static dim3 swiglu_grid(uint32_t m, uint32_t inter) {
     return dim3((inter + pairs - 1) / pairs, (m + GBM - 1) / GBM);
 }
 
-// 18 gemm_swiglu: a, w (2 inter rows), y, m, inter, k
+// 18 gemm_swiglu: a, w (2 inter rows), y, m, inter, k, a_shift
 static void l_gemm_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     GemmArgs a = gemm_base(p, w[4], 2 * w[5], w[6]);
     a.y16 = (uint16_t*)p[2];
     a.inter = int(w[5]);
+    a.ascale = a_scale(w[7]);
     const dim3 grid = swiglu_grid(w[4], w[5]);
     const int pairs = swiglu_pairs(w[4], w[5]);
     if (pairs == 96)
@@ -2365,7 +2381,8 @@ static void l_argmax_final(const PreparedDispatch& pd, void* const* p, hipStream
                        int(pd.words[3]));
 }
 
-// 32 gemm_skinny_f32, 33 gemm_skinny_residual: a, w, y, m, n, k; 34 gemm_skinny_swiglu: a, w, y, m, inter, k
+// 32 gemm_skinny_f32: a, w, y, m, n, k; 33 gemm_skinny_residual: a, w, y, m, n, k, a_shift; 34 gemm_skinny_swiglu:
+// a, w, y, m, inter, k, a_shift
 // One 16-column tile per block while that still leaves under two blocks per CU; two for wide N (the lm_head), whose
 // A rows would otherwise be read from L2 once per 16 columns.
 static bool skinny_one_tile(uint32_t n) { return (n + 15) / 16 < 512; }
@@ -2373,20 +2390,23 @@ static void l_gemm_skinny_f32(const PreparedDispatch& pd, void* const* p, hipStr
     const uint32_t* w = pd.words.data();
     if (skinny_one_tile(w[5]))
         hipLaunchKernelGGL((k_gemm_skinny<SK_F32, 1>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
-                           (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
+                           (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0, 1.0f);
     else
         hipLaunchKernelGGL((k_gemm_skinny<SK_F32, 2>), dim3((w[5] + 31) / 32), dim3(512), 0, s, (const uint16_t*)p[0],
-                           (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
+                           (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0,
+                           1.0f);
 }
 static void l_gemm_skinny_resid(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     hipLaunchKernelGGL((k_gemm_skinny<SK_RESID, 1>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
-                       (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0);
+                       (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0,
+                       a_unscale(w[7]));
 }
 static void l_gemm_skinny_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
     hipLaunchKernelGGL((k_gemm_skinny<SK_SWIGLU, 2>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
-                       (const uint16_t*)p[1], (float*)nullptr, (uint16_t*)p[2], int(w[4]), 0, int(w[6]), int(w[5]));
+                       (const uint16_t*)p[1], (float*)nullptr, (uint16_t*)p[2], int(w[4]), 0, int(w[6]), int(w[5]),
+                       a_scale(w[7]));
 }
 
 // 36 decode_advance: argmax, state, out_ids, batch, max_steps
@@ -2404,7 +2424,7 @@ static void l_prefetch(const PreparedDispatch& pd, void* const* p, hipStream_t s
                        (const u32x4*)p[2], n[2], (const u32x4*)p[3], n[3]);
 }
 
-// 39 gemm_residual_split: a, w, partials, m, n, k, splits. 128 x 64 tiles, blockIdx.z = the k split.
+// 39 gemm_residual_split: a, w, partials, m, n, k, splits, a_shift. 128 x 64 tiles, blockIdx.z = the k split.
 // the skinny (m <= 16) form of gemm_residual_split: 8 waves over each split's k, 128 per wave per step
 static bool resid_split_skinny(uint32_t m, uint32_t k, uint32_t splits) {
     return m <= 16 && (k / splits) % (kSkWaves * 128) == 0;
@@ -2416,12 +2436,13 @@ static void l_gemm_resid_split(const PreparedDispatch& pd, void* const* p, hipSt
     if (resid_split_skinny(w[4], w[6], w[7])) {
         hipLaunchKernelGGL((k_gemm_skinny<SK_PART, 1>), dim3((w[5] + 15) / 16, w[7]), dim3(512), 0, s,
                            (const uint16_t*)p[0], (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]),
-                           int(w[5]), int(w[6]), 0);
+                           int(w[5]), int(w[6]), 0, a_unscale(w[8]));
         return;
     }
     GemmArgs a = gemm_base(p, w[4], w[5], w[6]);
     a.y32 = (float*)p[2];
     a.ksplit = int(w[6] / w[7]);
+    a.ascale = a_unscale(w[8]);
     const dim3 grid((w[5] + 63) / 64, (w[4] + GBM - 1) / GBM, w[7]);
     const uint64_t blocks = uint64_t(grid.x) * grid.y * grid.z;
     if (blocks % 512 == 0)  // whole rounds of two blocks per CU: the direct-to-LDS loop
@@ -2527,6 +2548,10 @@ static void check_skinny(const char* k, const uint32_t* w, const uint32_t* c, in
     need(c, 2, m * ycols, k, "y");
 }
 
+static void need_a_shift(const char* k, uint32_t s) {
+    if (s > kMaxAShift) contract_fail("%s: a_shift must be at most %u", k, kMaxAShift);
+}
+
 static void need_max_pos(const char* k, uint32_t mp) {
     if (mp < 64 || mp % 64 || mp > 64u * kMaxSplits)
         contract_fail("%s: max_pos must be a multiple of 64 in 64 .. %d", k, 64 * kMaxSplits);
@@ -2586,28 +2611,32 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 3, rows * qh * 128, "attention_prefill_f16", "y");
                      need(c, 4, attn_prefill::workspace_words(rows, kvh), "attention_prefill_f16", "workspace");
                  }});
-    // 17 gemm_residual: a, w, x, m, n, k
+    // 17 gemm_residual: a, w, x, m, n, k, a_shift
     c.push_back({"gemm_residual", "fast", {256, 1, 1}, false,
                  [](const uint32_t* w) {
                      const int64_t bn = resid_narrow(w[4], w[5]) ? 64 : 128;
                      return Grid3{(int64_t(w[5]) + bn - 1) / bn, (int64_t(w[4]) + 127) / 128, 1};
                  },
-                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_RW("x", DT(F32)), U32F("m"), U32F("n"), U32F("k")},
+                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_RW("x", DT(F32)), U32F("m"), U32F("n"), U32F("k"),
+                  U32F("a_shift")},
                  [](const uint32_t* w, const uint32_t* c) {
                      if (w[6] % 64 || w[6] < 64) contract_fail("gemm_residual: k must be a positive multiple of 64");
+                     need_a_shift("gemm_residual", w[7]);
                      need(c, 0, int64_t(w[4]) * w[6], "gemm_residual", "a");
                      need(c, 1, int64_t(w[5]) * w[6], "gemm_residual", "w");
                      need(c, 2, int64_t(w[4]) * w[5], "gemm_residual", "x");
                  }});
-    // 18 gemm_swiglu: a, w, y, m, inter, k
+    // 18 gemm_swiglu: a, w, y, m, inter, k, a_shift
     c.push_back({"gemm_swiglu", "fast", {256, 1, 1}, false,
                  [](const uint32_t* w) {
                      const dim3 g = swiglu_grid(w[4], w[5]);
                      return Grid3{g.x, g.y, 1};
                  },
-                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F16)), U32F("m"), U32F("inter"), U32F("k")},
+                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F16)), U32F("m"), U32F("inter"), U32F("k"),
+                  U32F("a_shift")},
                  [](const uint32_t* w, const uint32_t* c) {
                      if (w[6] % 64 || w[6] < 64) contract_fail("gemm_swiglu: k must be a positive multiple of 64");
+                     need_a_shift("gemm_swiglu", w[7]);
                      need(c, 0, int64_t(w[4]) * w[6], "gemm_swiglu", "a");
                      need(c, 1, 2 * int64_t(w[5]) * w[6], "gemm_swiglu", "w");
                      need(c, 2, int64_t(w[4]) * w[5], "gemm_swiglu", "y");
@@ -2758,16 +2787,22 @@ std::vector<KernelSpec> fast_catalog() {
                  },
                  {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F32)), U32F("m"), U32F("n"), U32F("k")},
                  [](const uint32_t* w, const uint32_t* c) { check_skinny("gemm_skinny_f32", w, c, w[5], w[5]); }});
-    // 33 gemm_skinny_residual: a, w, x, m, n, k
+    // 33 gemm_skinny_residual: a, w, x, m, n, k, a_shift
     c.push_back({"gemm_skinny_residual", "fast", {512, 1, 1}, false,
                  [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 15) / 16, 1, 1}; },
-                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_RW("x", DT(F32)), U32F("m"), U32F("n"), U32F("k")},
-                 [](const uint32_t* w, const uint32_t* c) { check_skinny("gemm_skinny_residual", w, c, w[5], w[5]); }});
-    // 34 gemm_skinny_swiglu: a, w (2 inter rows), y, m, inter, k
+                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_RW("x", DT(F32)), U32F("m"), U32F("n"), U32F("k"),
+                  U32F("a_shift")},
+                 [](const uint32_t* w, const uint32_t* c) {
+                     check_skinny("gemm_skinny_residual", w, c, w[5], w[5]);
+                     need_a_shift("gemm_skinny_residual", w[7]);
+                 }});
+    // 34 gemm_skinny_swiglu: a, w (2 inter rows), y, m, inter, k, a_shift
     c.push_back({"gemm_skinny_swiglu", "fast", {512, 1, 1}, false,
                  [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 15) / 16, 1, 1}; },
-                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F16)), U32F("m"), U32F("inter"), U32F("k")},
+                 {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F16)), U32F("m"), U32F("inter"), U32F("k"),
+                  U32F("a_shift")},
                  [](const uint32_t* w, const uint32_t* c) {
+                     need_a_shift("gemm_skinny_swiglu", w[7]);
                      check_skinny("gemm_skinny_swiglu", w, c, 2 * int64_t(w[5]), w[5]);
                  }});
     // 35 attention_combine_f16: partials, y (f16), state, q_heads, max_pos, batch
@@ -2832,8 +2867,9 @@ std::vector<KernelSpec> fast_catalog() {
                      need(c, 17, 2 * int64_t(persist::exchange_entries(int(L), sh)), "decode_step_persistent", "exchange");
                      need(c, 18, V * H, "decode_step_persistent", "embed16");
                  }});
-    // 39 gemm_residual_split: a, w, partials, m, n, k, splits. partials[z] = a[:, k range z] . w[:, k range z]^T, the k
-    // range split in `splits` equal parts of multiples of 64; residual_add_norm adds them to the residual stream. For
+    // 39 gemm_residual_split: a, w, partials, m, n, k, splits, a_shift. partials[z] = 2^a_shift a[:, k range z] .
+    // w[:, k range z]^T, the k range split in `splits` equal parts of multiples of 64; residual_add_norm adds them to
+    // the residual stream. For
     // m <= 16 with 1024-multiples per split it runs as a skinny GEMM (512 threads, one block per 16 columns and split).
     c.push_back({"gemm_residual_split", "fast", {256, 1, 1}, false,
                  [](const uint32_t* w) {
@@ -2843,9 +2879,10 @@ std::vector<KernelSpec> fast_catalog() {
                      return Grid3{gx, (int64_t(w[4]) + rows - 1) / rows, w[7]};
                  },
                  {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("partials", DT(F32)), U32F("m"), U32F("n"), U32F("k"),
-                  U32F("splits")},
+                  U32F("splits"), U32F("a_shift")},
                  [](const uint32_t* w, const uint32_t* c) {
                      const int64_t m = w[4], n = w[5], k = w[6], sp = w[7];
+                     need_a_shift("gemm_residual_split", w[8]);
                      if (sp != 1 && sp != 2 && sp != 4 && sp != 8)
                          contract_fail("gemm_residual_split: splits must be 1, 2, 4 or 8");
                      if (k < 64 * sp || k % (64 * sp))

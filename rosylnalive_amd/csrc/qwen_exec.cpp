@@ -453,6 +453,7 @@ void QwenExec::set_weight_bytes(const std::string& name, const uint8_t* data, ui
     for (uint32_t d : tt.dims) n *= d;
     if (tt.dtype != BF16 || n != elems) arg_fail("weight %s holds %llu bf16 elements, not %llu", name.c_str(), (unsigned long long)n, (unsigned long long)elems);
     const std::string base = f16_copy_.count(name) ? name : tt.view_of;  // the tensor with the fp16 copy, if any
+    set_swiglu_shift(0);  // new weights: the next forward finds the shift they need
     if (f16_copy_.count(base)) {
         // the fp16 copy must hold the same values: |w| >= 65536 has no fp16 counterpart
         for (uint64_t i = 0; i < elems; ++i) {
@@ -549,6 +550,28 @@ uint32_t QwenExec::forward(int seq, int pos0, const int32_t* ids, int t_, float*
         arg_fail("positions %d .. %d outside max_pos %d", pos0, pos0 + t_ - 1, c.max_pos);
     if (logits_rows < 0 || logits_rows > t_) arg_fail("logits_rows %d outside 0 .. %d", logits_rows, t_);
     uint32_t am = 0xFFFFFFFFu;
+    // Fast mode: a forward whose SwiGLU output left the fp16 range runs again with that output shifted down
+    // kSwigluShiftStep binades more (the overflow may have spread to the sites after it, so those bits are no verdict
+    // yet), up to kMaxSwigluShift; the shift then stays for later calls until a weight changes. Every rerun rewrites the
+    // same cache rows and logits.
+    for (;;) {
+        am = forward_chunks(seq, pos0, ids, t_, logits, logits_rows);
+        if (c.mode != 1) break;
+        const uint32_t bits = dev_.take_f16_range();
+        if ((bits & kF16SiteSwiglu) && swiglu_shift_ < kMaxSwigluShift) {
+            set_swiglu_shift(swiglu_shift_ + kSwigluShiftStep);
+            continue;
+        }
+        if (bits) throw_f16_range("forward", bits);
+        break;
+    }
+    last_t_ = t_;
+    return am;
+}
+
+uint32_t QwenExec::forward_chunks(int seq, int pos0, const int32_t* ids, int t_, float* logits, int logits_rows) {
+    const QwenConfig& c = cfg_;
+    uint32_t am = 0xFFFFFFFFu;
     // chunked prefill: max_tokens rows at a time, the cache carrying the earlier chunks
     for (int c0 = 0; c0 < t_; c0 += c.max_tokens) {
         const int n = std::min(c.max_tokens, t_ - c0);
@@ -567,16 +590,27 @@ uint32_t QwenExec::forward(int seq, int pos0, const int32_t* ids, int t_, float*
         else
             am = forward_fp32(pos0 + c0, n, lg, std::max(want, 1));
     }
-    last_t_ = t_;
-    if (c.mode == 1) check_f16_range("forward");
     return am;
 }
 
-void QwenExec::check_f16_range(const char* what) {
-    const uint32_t bits = dev_.take_f16_range();
-    if (bits)
-        throw RangeError(std::string(what) + ": a value stored as fp16 left the fp16 range (|x| > 65504, or NaN) at: " +
-                         f16_range_sites(bits) + "; the results of this call are not usable");
+void QwenExec::set_swiglu_shift(int s) {
+    if (s == swiglu_shift_) return;
+    swiglu_shift_ = s;
+    if (decode_list_) {  // the recorded batched step carries the shift in its words
+        dev_.release(decode_list_);
+        decode_list_ = nullptr;
+    }
+}
+
+void QwenExec::set_swiglu_shift_checked(int s) {
+    if (cfg_.mode != 1) arg_fail("the SwiGLU shift is a fast-mode setting");
+    if (s < 0 || s > kSwigluShiftLimit) arg_fail("SwiGLU shift %d outside 0 .. %d", s, kSwigluShiftLimit);
+    set_swiglu_shift(s);
+}
+
+void QwenExec::throw_f16_range(const char* what, uint32_t bits) {
+    throw RangeError(std::string(what) + ": a value stored as fp16 left the fp16 range (|x| > 65504, or NaN) at: " +
+                     f16_range_sites(bits) + "; the results of this call are not usable");
 }
 
 uint32_t QwenExec::forward_fp32(int pos0, int T, float* logits, int lr) {
@@ -706,6 +740,7 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
     const uint32_t scale = fbits(float(std::pow(double(HD), -0.5)));
     auto tk = [&](const std::string& n) { return token(n); };
     const uint32_t LC = dev_.table().row(tk("logits")).count() / V;
+    const uint32_t ash = uint32_t(swiglu_shift_);
     sync_f16();
     CommandList* l = dev_.begin();
     dispatch(l, "embed_gather_bf16", {tk("ids"), tk("model.embed_tokens.weight"), tk("x"), U, H, V});
@@ -713,13 +748,13 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
     // and normalises (the split fills the CUs: at 2048 rows the 128 x 64 tiles alone give one block per CU), or, with no
     // split, the residual GEMM and the norm
     const uint32_t MT = uint32_t(c.max_tokens);
-    auto residual_norm = [&](const std::string& a, const std::string& wname, uint32_t K, uint32_t nw) {
+    auto residual_norm = [&](const std::string& a, const std::string& wname, uint32_t K, uint32_t nw, uint32_t sh) {
         const uint32_t sp = resid_splits(U, H, K, MT);
         if (sp > 1) {
-            dispatch(l, "gemm_residual_split", {tk(a), tk(wname), tk("resid.partials"), U, H, K, sp});
+            dispatch(l, "gemm_residual_split", {tk(a), tk(wname), tk("resid.partials"), U, H, K, sp, sh});
             dispatch(l, "residual_add_norm", {tk("x"), tk("resid.partials"), nw, tk("h"), U, H, sp, eps});
         } else {
-            dispatch(l, "gemm_residual", {tk(a), tk(wname), tk("x"), U, H, K});
+            dispatch(l, "gemm_residual", {tk(a), tk(wname), tk("x"), U, H, K, sh});
             dispatch(l, "rmsnorm_rows_f16", {tk("x"), nw, tk("h"), U, H, eps, 0});
         }
     };
@@ -734,12 +769,12 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
         dispatch(l, "attention_prefill_f16", {tk("q"), tk(p + "k_cache" + sq), tk(p + "v_cache" + sq), tk("o"),
                                               tk("attn.ws"), U, uint32_t(pos0), uint32_t(c.heads),
                                               uint32_t(c.kv_heads), MP, scale});
-        residual_norm("o", p + "o_proj.f16", QC, w(7));
-        dispatch(l, "gemm_swiglu", {tk("h"), tk(p + "gate_up_proj.f16"), tk("a"), U, I, H});
+        residual_norm("o", p + "o_proj.f16", QC, w(7), 0);
+        dispatch(l, "gemm_swiglu", {tk("h"), tk(p + "gate_up_proj.f16"), tk("a"), U, I, H, ash});
         // the next layer's input norm (after the last layer: the final norm, which the lm_head pass below recomputes
         // on its rows)
         residual_norm("a", p + "down_proj.f16", I,
-                      i + 1 < c.layers ? tk(lname(i + 1, kLayerWeights[0])) : tk("model.norm.weight"));
+                      i + 1 < c.layers ? tk(lname(i + 1, kLayerWeights[0])) : tk("model.norm.weight"), ash);
     }
     // logits of the last lr rows, LC rows per lm_head dispatch
     hipEvent_t e0, e1;
@@ -849,12 +884,13 @@ void QwenExec::record_decode_batch(CommandList* l) {
     // x += a . W^T, then h = RMSNorm(x) with norm weights nw: the GEMM split over k in two (twice the blocks: one
     // block per 16 columns alone leaves half the CUs idle at hidden 2048) into partials, then one pass that adds them
     // and normalises; or, when k does not split in 1024-multiples, the residual GEMM and the norm
-    auto residual_norm = [&](const std::string& a, const std::string& wname, uint32_t K, uint32_t nw) {
+    const uint32_t ash = uint32_t(swiglu_shift_);
+    auto residual_norm = [&](const std::string& a, const std::string& wname, uint32_t K, uint32_t nw, uint32_t sh) {
         if (K % 2048 == 0 && add_norm_width(H)) {
-            dispatch(l, "gemm_residual_split", {tk(a), tk(wname), tk("resid.partials"), B, H, K, 2});
+            dispatch(l, "gemm_residual_split", {tk(a), tk(wname), tk("resid.partials"), B, H, K, 2, sh});
             dispatch(l, "residual_add_norm", {tk("dec.x"), tk("resid.partials"), nw, tk("dec.h16"), B, H, 2, eps});
         } else {
-            dispatch(l, "gemm_skinny_residual", {tk(a), tk(wname), tk("dec.x"), B, H, K});
+            dispatch(l, "gemm_skinny_residual", {tk(a), tk(wname), tk("dec.x"), B, H, K, sh});
             dispatch(l, "rmsnorm_rows_f16", {tk("dec.x"), nw, tk("dec.h16"), B, H, eps, 0});
         }
     };
@@ -871,11 +907,11 @@ void QwenExec::record_decode_batch(CommandList* l) {
                                              B, 0, splits});
         dispatch(l, "attention_combine_f16", {tk("dec.attn_partials"), tk("dec.o16"), tk("dec.state"),
                                               uint32_t(c.heads), MP, B, 0, splits});
-        residual_norm("dec.o16", p + "o_proj.f16", QC, w(7));
-        dispatch(l, "gemm_skinny_swiglu", {tk("dec.h16"), tk(p + "gate_up_proj.f16"), tk("dec.a16"), B, I, H});
+        residual_norm("dec.o16", p + "o_proj.f16", QC, w(7), 0);
+        dispatch(l, "gemm_skinny_swiglu", {tk("dec.h16"), tk(p + "gate_up_proj.f16"), tk("dec.a16"), B, I, H, ash});
         // the next layer's input norm (after the last layer: the final norm, the lm_head's input)
         residual_norm("dec.a16", p + "down_proj.f16", I,
-                      i + 1 < c.layers ? tk(lname(i + 1, kLayerWeights[0])) : tk("model.norm.weight"));
+                      i + 1 < c.layers ? tk(lname(i + 1, kLayerWeights[0])) : tk("model.norm.weight"), ash);
     }
     dispatch(l, "gemm_skinny_f32", {tk("dec.h16"), tk("embed.f16"), tk("logits"), B, V, H});
     dispatch(l, "argmax_rows_partial", {tk("logits"), tk("argmax.partials"), B, V});
@@ -947,7 +983,11 @@ void QwenExec::run_decode_steps(int steps) {
             throw std::runtime_error("decode_step_persistent: a workgroup waited past its bound at stage " +
                                      std::to_string(hdr[2]) + "; the decode state did not advance from there");
     }
-    check_f16_range("decode");
+    // A decode call cannot rerun (its steps advanced the state): it fails, and a SwiGLU overflow raises the shift
+    // for the calls after it.
+    const uint32_t bits = dev_.take_f16_range();
+    if (bits & kF16SiteSwiglu) set_swiglu_shift(std::min(kMaxSwigluShift, swiglu_shift_ + kSwigluShiftStep));
+    if (bits) throw_f16_range("decode", bits);
 }
 
 void QwenExec::read_decode_ids(int32_t* out, int count) {

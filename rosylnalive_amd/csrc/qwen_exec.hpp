@@ -82,15 +82,27 @@ class QwenExec {
     // false when it is the recorded list of per-stage kernels. The persistent step is used when the device has at least
     // 256 CUs, the kernel covers the shape and LRM_HIP_DECODE is not "kernels" at construction.
     bool persistent_decode() const { return persist_; }
+    // Fast mode: the binades s by which the SwiGLU output a is shifted down before it is stored as fp16 (a 2^-s; the
+    // down_proj GEMM multiplies its sums by 2^s). 0 until a forward overflows there, which then reruns with
+    // s = 8, then 16; any weight write sets it back to 0.
+    int swiglu_shift() const { return swiglu_shift_; }
+    // Sets s (0 .. kSwigluShiftLimit, the largest a_shift the kernels take) ahead of the next call: for a checkpoint
+    // whose SwiGLU range is known, which then needs no rerun.
+    void set_swiglu_shift_checked(int s);
+    static constexpr int kSwigluShiftLimit = 24;
+    static constexpr int kSwigluShiftStep = 8;
+    static constexpr int kMaxSwigluShift = 16;
 
   private:
     void plan();
     void upload_rope(const uint32_t* inv_freq_bits);
     uint32_t forward_fp32(int pos0, int t, float* logits, int logits_rows);
     uint32_t forward_fast(int seq, int pos0, int t, float* logits, int logits_rows);
+    uint32_t forward_chunks(int seq, int pos0, const int32_t* ids, int t, float* logits, int logits_rows);
+    void set_swiglu_shift(int s);
     void set_weight_bytes(const std::string& name, const uint8_t* data, uint64_t elems);
-    // Fast mode: fails the call (RangeError) when a kernel flagged an fp16 value out of range since the last check.
-    void check_f16_range(const char* what);
+    // Fast mode: fails the call (RangeError) naming the fp16 range sites in bits.
+    [[noreturn]] void throw_f16_range(const char* what, uint32_t bits);
     void record_decode_fast();
     void record_decode_batch(CommandList* l);
     void sync_f16();  // refreshes the fp16 copies of the matrices written since the last forward
@@ -120,6 +132,7 @@ class QwenExec {
     CommandList* decode_list_ = nullptr;
     bool persist_ = false;    // the decode step is decode_step_persistent (layer-stacked weights and caches)
     int persist_blocks_ = 0;  // its workgroups
+    int swiglu_shift_ = 0;
     std::map<std::string, std::string> f16_copy_;  // bf16 matrix -> its fp16 copy (Fast mode)
     std::set<std::string> f16_dirty_;
     void add(const std::string& name, uint32_t arena, uint32_t dtype, std::vector<uint32_t> dims, uint32_t flags = 0);

@@ -249,6 +249,15 @@ class QwenModel:
         LRM_HIP_DECODE=kernels before construction for the per-stage kernel list."""
         return lib().lrm_qwen_persistent_decode(self._h) == 1
 
+    def swiglu_shift(self) -> int:
+        """Fast mode: the binades s the SwiGLU output is shifted down by before its fp16 store (0 until a forward
+        overflowed there and ran again with s = 8, then 16; back to 0 when a weight is written)."""
+        return lib().lrm_qwen_swiglu_shift(self._h)
+
+    def set_swiglu_shift(self, shift: int) -> None:
+        """Sets the SwiGLU shift (0 .. 24) for the calls that follow (until a weight is written)."""
+        check(lib().lrm_qwen_set_swiglu_shift(self._h, int(shift)))
+
     def token(self, name: str) -> int:
         t = C.c_uint32()
         check(lib().lrm_qwen_token(self._h, name.encode(), C.byref(t)))

@@ -154,6 +154,24 @@ def test_attention_combine_splits_bound():
                                              max_pos=128, batch=1, chunks=0, splits=3))
 
 
+def test_a_shift_bound():
+    """The SwiGLU output's producers and consumers take its shift (a_shift, in binades) up to 24; past that the
+    dispatch is a contract error."""
+    sealed, _ = _table([("a", DType.F16, [16 * 1024], 0), ("w", DType.F16, [1024 * 1024], TensorFlags.READ_ONLY),
+                        ("x", DType.F32, [2 * 16 * 1024], 0), ("y", DType.F16, [16 * 512], 0)])
+    cases = [("gemm_residual", dict(a=1, w=2, x=3, m=16, n=1024, k=1024)),
+             ("gemm_swiglu", dict(a=1, w=2, y=4, m=16, inter=512, k=1024)),
+             ("gemm_skinny_residual", dict(a=1, w=2, x=3, m=16, n=1024, k=1024)),
+             ("gemm_skinny_swiglu", dict(a=1, w=2, y=4, m=16, inter=512, k=1024)),
+             ("gemm_residual_split", dict(a=1, w=2, partials=3, m=16, n=1024, k=1024, splits=2))]
+    for name, f in cases:
+        kid = Catalog.find(name).id
+        for s in (0, 8, 24):
+            prepare(sealed, kid, ArgBlock.encode(name, a_shift=s, **f))
+        with pytest.raises(GpuContractException, match="a_shift must be at most 24"):
+            prepare(sealed, kid, ArgBlock.encode(name, a_shift=25, **f))
+
+
 def test_tensor_row_vectors_T1_T2():
     out = (ctypes.c_uint32 * 16)()
     dims = (ctypes.c_uint32 * 2)(151936, 1024)

@@ -1,14 +1,15 @@
 """The fast path's fp16 range monitor: a value it narrows to fp16 (normed hidden rows, q, the K/V cache, the attention
 and SwiGLU outputs) that overflows makes the forward or decode call fail with Fp16RangeError naming the site, instead
-of passing inf on into logits the caller would take as results. The overflows are forced from the host through the
+of passing inf on into logits the caller would take as results; a forward whose SwiGLU output overflows first runs
+again with that output shifted down (stored as a 2^-s, the down_proj sums scaled by 2^s). The overflows are forced from the host through the
 weights (data only: every kernel still runs to its end), and the same model then runs clean again, bit for bit.
 """
 import numpy as np
 import pytest
 
-from oracle import cpuref
+from oracle import cpuref, metrics
 from rosylnalive_amd.gpu_core import Fp16RangeError, HipBackend
-from rosylnalive_amd.qwen import QwenConfig, QwenModel, synthetic_ids, synthetic_weights
+from rosylnalive_amd.qwen import QwenConfig, QwenModel, inv_freq_bits, synthetic_ids, synthetic_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -36,29 +37,93 @@ def _clean_forward(m, ids):
     return lg, am
 
 
-def test_swiglu_outlier_fails_the_forward_and_names_the_site(model):
-    """gate and up rows 0 .. 63 all +1 and rows 64 .. 127 all -1 in layer 1, after a post-attention norm of 30: for
-    either sign of a row's sum one half of those columns has gate = up ~ 30 * sum(normed x), so silu(gate) * up runs
-    far past 65,504 while h (|h| ~ 30) and the float32 reference stay finite."""
-    m, w = model
-    ids = synthetic_ids(23, "range/prompt", 48, CFG.vocab)
-    base, am = _clean_forward(m, ids)
+def _swiglu_outlier(w, value):
+    """gate and up rows 0 .. 63 all +value and rows 64 .. 127 all -value in layer 1, after a post-attention norm of 30:
+    for either sign of a row's sum one half of those columns has gate = up ~ 30 value sum(normed x), so silu(gate) up
+    runs far past 65,504 while h (|h| ~ 30) and the float32 reference stay finite."""
     gname, uname = "model.layers.1.mlp.gate_proj.weight", "model.layers.1.mlp.up_proj.weight"
     nname = "model.layers.1.post_attention_layernorm.weight"
     g, u = w[gname].copy(), w[uname].copy()
     for a in (g, u):
-        a[:64] = bf16(1.0, (64, CFG.hidden))
-        a[64:128] = bf16(-1.0, (64, CFG.hidden))
+        a[:64] = bf16(value, (64, CFG.hidden))
+        a[64:128] = bf16(-value, (64, CFG.hidden))
+    return {gname: g, uname: u, nname: bf16(30.0, (CFG.hidden,))}
+
+
+def _swiglu_spikes(w):
+    """Layer 1: post-attention norm weights of 500 on hidden columns 0 .. 63 (|h| there up to about 2,000), gate and
+    up rows 0 .. 63 the unit rows of those columns, and those columns zeroed in every other gate / up row. SwiGLU
+    outputs 0 .. 63 are then silu(h_c) h_c, about h_c^2 (up to ~4e6) for positive h_c: past 65,504 at shift 0 and
+    within range at shift 8, with no cancelling sum in front of them (every value keeps fp16's relative precision),
+    while the other outputs keep their usual size."""
+    gname, uname = "model.layers.1.mlp.gate_proj.weight", "model.layers.1.mlp.up_proj.weight"
+    nname = "model.layers.1.post_attention_layernorm.weight"
+    one = bf16(1.0, (1,))[0]
+    out = {}
+    for name in (gname, uname):
+        a = w[name].copy()
+        a[:, :64] = 0
+        a[np.arange(64), np.arange(64)] = one
+        out[name] = a
+    nw = w[nname].copy()
+    nw[:64] = bf16(500.0, (64,))
+    out[nname] = nw
+    return out
+
+
+def test_swiglu_outlier_reruns_the_forward_shifted(model):
+    """SwiGLU outputs past the fp16 range: the forward runs again with them stored 2^-8 scaled and the down_proj sums
+    scaled back, and its logits meet the fast path's bound against the float32 oracle on the same weights (max-abs
+    2e-2, top-1 >= 99 %). The shift stays for the next forward (same logits, bit for bit) and goes back to 0 when a
+    weight is written: the restored model runs as before, bit for bit."""
+    m, w = model
+    ids = synthetic_ids(23, "range/prompt", 48, CFG.vocab)
+    base, am = _clean_forward(m, ids)
+    assert m.swiglu_shift() == 0
+    bad = _swiglu_spikes(w)
+    w2 = dict(w)
+    w2.update(bad)
     try:
-        m.set_weight(gname, g)
-        m.set_weight(uname, u)
-        m.set_weight(nname, bf16(30.0, (CFG.hidden,)))
+        for n, v in bad.items():
+            m.set_weight(n, v)
+        lg, am2 = m.forward(ids, 0, logits_rows=48)
+        shift = m.swiglu_shift()
+        lg2, _ = m.forward(ids, 0, logits_rows=48)
+        assert m.swiglu_shift() == shift and lg2.tobytes() == lg.tobytes()
+    finally:
+        for n in bad:
+            m.set_weight(n, w[n])
+    assert m.swiglu_shift() == 0
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), CFG.max_pos)
+    orc = cpuref.QwenOracle(CFG.oracle_dict(), w2, cos, sin)
+    ol = orc.forward(orc.new_cache(), 0, ids)
+    err, top1 = metrics.max_abs(lg, ol), metrics.top1_agreement(lg, ol)
+    print(f"SwiGLU outlier: shift {shift}, max-abs {err:.4g} (logit range {ol.min():.3g}..{ol.max():.3g}), "
+          f"top-1 {top1:.4f}", flush=True)
+    assert shift == 8
+    assert err <= 2e-2 and top1 >= 0.99 and am2 == int(np.argmax(lg[-1]))
+    lg3, am3 = _clean_forward(m, ids)
+    assert lg3.tobytes() == base.tobytes() and am3 == am
+
+
+def test_swiglu_outlier_past_the_largest_shift_fails_and_names_the_site(model):
+    """Gate and up rows of 100 after a norm of 30 take the SwiGLU output to ~9e10, past 65,504 x 2^16: the forward
+    fails with Fp16RangeError naming the site after its reruns at shifts 8 and 16; the restored model runs as before,
+    bit for bit."""
+    m, w = model
+    ids = synthetic_ids(23, "range/prompt", 48, CFG.vocab)
+    base, am = _clean_forward(m, ids)
+    bad = _swiglu_outlier(w, 100.0)
+    try:
+        for n, v in bad.items():
+            m.set_weight(n, v)
         with pytest.raises(Fp16RangeError) as e:
             m.forward(ids, 0)
         print(e.value, flush=True)
         assert "SwiGLU output (a)" in str(e.value)
+        assert m.swiglu_shift() == 16
     finally:
-        for n in (gname, uname, nname):
+        for n in bad:
             m.set_weight(n, w[n])
     lg, am2 = _clean_forward(m, ids)  # the words were cleared: the same call runs clean, bit for bit
     assert lg.tobytes() == base.tobytes() and am2 == am
@@ -101,3 +166,76 @@ def test_cache_overflow_fails_the_decode(model):
     m.decode_set(am, ids.size)
     m.decode_run(4)
     assert np.isfinite(m.read_logits(1)).all()
+
+
+def test_batched_decode_overflow_raises_the_shift_for_the_steps_after_it():
+    """Batched decode (two sequences; its skinny SwiGLU GEMM stores fp16), prefilled on the clean weights, then the
+    spike weights set (layer 1's MLP only: the prefilled caches are those of the new weights too). The first step
+    fails naming the SwiGLU output and raises the shift to 8; that step again and the ones after it run shifted, each
+    sequence's logits against the float32 oracle on the new weights at that position."""
+    w = synthetic_weights(CFG, seed=23)
+    bad = _swiglu_spikes(w)
+    w2 = dict(w)
+    w2.update(bad)
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), CFG.max_pos)
+    orc = cpuref.QwenOracle(CFG.oracle_dict(), w2, cos, sin)
+    B, lens, steps = 2, [20, 33], 4
+    seqs = [synthetic_ids(60 + b, "range/batch", lens[b] + steps, CFG.vocab) for b in range(B)]
+    ref = [orc.forward(orc.new_cache(), 0, seqs[b]) for b in range(B)]
+    b_ = HipBackend(0)
+    m = QwenModel(b_, CFG, mode="fast", max_tokens=64, batch=B)
+    try:
+        m.load_weights(w)
+        for b in range(B):
+            m.forward(seqs[b][:lens[b]], 0, logits_rows=1, seq=b)
+        for n, v in bad.items():
+            m.set_weight(n, v)
+        with pytest.raises(Fp16RangeError) as e:
+            m.decode_batch([int(seqs[b][lens[b]]) for b in range(B)], lens, 1)
+        print(e.value, flush=True)
+        assert "SwiGLU output (a)" in str(e.value) and m.swiglu_shift() == 8
+        worst, agree = 0.0, 0
+        for s in range(steps):
+            pos = [lens[b] + s for b in range(B)]
+            ids = m.decode_batch([int(seqs[b][pos[b]]) for b in range(B)], pos, 1)
+            lg = m.read_logits(B)
+            for b in range(B):
+                o = ref[b][pos[b]]
+                worst = max(worst, metrics.max_abs(lg[b], o))
+                agree += int(np.argmax(lg[b]) == np.argmax(o))
+                assert int(ids[0, b]) == int(np.argmax(lg[b]))
+        print(f"shifted batched decode vs the oracle: worst max-abs {worst:.4g}, top-1 {agree}/{B * steps}",
+              flush=True)
+        assert m.swiglu_shift() == 8 and worst <= 2e-2 and agree >= B * steps - 1
+    finally:
+        m.close()
+        b_.close()
+
+
+def test_set_swiglu_shift_ahead(model):
+    """A shift set ahead (for a checkpoint whose range is known): on the clean model shift 8 changes only the SwiGLU
+    outputs under 2^-6 (kept to 2^-17 absolute instead of fp16's relative precision), so the logits move by a small
+    part of the fast path's bound and stay within it against the float32 oracle; the setter refuses values outside
+    0 .. 24, and writing a weight sets it back to 0."""
+    m, w = model
+    ids = synthetic_ids(23, "range/prompt4", 48, CFG.vocab)
+    base, _ = m.forward(ids, 0, logits_rows=48)
+    m.set_swiglu_shift(8)
+    assert m.swiglu_shift() == 8
+    lg, _ = m.forward(ids, 0, logits_rows=48)
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), CFG.max_pos)
+    orc = cpuref.QwenOracle(CFG.oracle_dict(), w, cos, sin)
+    ol = orc.forward(orc.new_cache(), 0, ids)
+    d, e0, e8 = (float(np.abs(lg - base).max()), metrics.max_abs(base, ol), metrics.max_abs(lg, ol))
+    print(f"clean model, shift 8 against shift 0: max-abs {d:.3g}; against the oracle: {e0:.4g} (shift 0), "
+          f"{e8:.4g} (shift 8)", flush=True)
+    assert 0 < d <= 5e-3 and e8 <= 2e-2 and metrics.top1_agreement(lg, ol) >= 0.99
+    for bad in (-1, 25):
+        with pytest.raises(Exception, match="outside 0 .. 24"):
+            m.set_swiglu_shift(bad)
+    assert m.swiglu_shift() == 8
+    name = "model.layers.0.mlp.down_proj.weight"
+    m.set_weight(name, w[name])
+    assert m.swiglu_shift() == 0
+    lg0, _ = m.forward(ids, 0, logits_rows=48)
+    assert lg0.tobytes() == base.tobytes()

@@ -140,6 +140,66 @@ def test_gemm_swiglu(m, inter, k):
         s.close()
 
 
+@pytest.mark.parametrize("kernel,m,inter,k", [("gemm_swiglu", 2048, 3072, 1024), ("gemm_swiglu", 200, 192, 128),
+                                              ("gemm_skinny_swiglu", 16, 3072, 1024)])
+def test_swiglu_a_shift(kernel, m, inter, k):
+    """a_shift s makes the SwiGLU producers store a 2^-s. Where a 2^-s is still a normal fp16 number (here: where
+    |a| >= 2^-5) the stored value times 2^s is the unshifted store bit for bit; below that the two differ by at most
+    two half-ulps of the subnormal grid (2^-17 each after rescaling)."""
+    r = np.random.default_rng(11)
+    a = f16(r.standard_normal((m, k)))
+    w = f16(r.standard_normal((2 * inter, k)) * 0.1)
+    s = Session({"a": (F16, (m, k), 0, a), "w": (F16, (2 * inter, k), RO, w), "y": (F16, (m, inter), 0, None)})
+    try:
+        y0 = hwiden(s.run(kernel, ["y"], a="a", w="w", y="y", m=m, inter=inter, k=k, a_shift=0)["y"])
+        y8 = hwiden(s.run(kernel, ["y"], a="a", w="w", y="y", m=m, inter=inter, k=k, a_shift=8)["y"])
+        big = np.abs(y0) >= 2.0 ** -5
+        assert big.mean() > 0.5
+        assert np.array_equal(y8[big] * 256, y0[big])
+        assert np.abs(y8[~big] * 256 - y0[~big]).max() <= 2.0 ** -16
+    finally:
+        s.close()
+
+
+@pytest.mark.parametrize("kernel,m,n,k,splits", [("gemm_residual", 512, 1024, 1024, 0),
+                                                 ("gemm_residual", 2048, 2048, 1024, 0),
+                                                 ("gemm_skinny_residual", 16, 1024, 3072, 0),
+                                                 ("gemm_residual_split", 2048, 1024, 3072, 2),
+                                                 ("gemm_residual_split", 300, 256, 512, 4),
+                                                 ("gemm_residual_split", 77, 1024, 1024, 2),
+                                                 ("gemm_residual_split", 16, 1024, 4096, 4)])
+def test_residual_a_shift_is_exact(kernel, m, n, k, splits):
+    """The SwiGLU output's consumers multiply their sums by 2^a_shift: a 2^-8 in with a_shift 8 gives the bits of a in
+    with a_shift 0 (a power-of-two scale commutes with every float32 rounding of the sums), on every loop the kernels
+    choose (narrow and wide residual tiles, the skinny form, the split GEMM's direct-to-LDS, register, 64-row and
+    skinny forms)."""
+    r = np.random.default_rng(m + n + k + splits)
+    a_lo = f16(r.standard_normal((m, k)) * 0.01)
+    a_hi = f16(hwiden(a_lo) * 256)
+    assert np.array_equal(hwiden(a_hi), hwiden(a_lo) * 256)  # exact: no fp16 overflow
+    w = f16(r.standard_normal((n, k)) * 0.05)
+    x0 = r.standard_normal((m, n)).astype(np.float32)
+    out = (F32, (max(splits, 1), m, n), 0, None)
+    s = Session({"lo": (F16, (m, k), 0, a_lo), "hi": (F16, (m, k), 0, a_hi), "w": (F16, (n, k), RO, w),
+                 "x": (F32, (m, n), 0, x0), "p": out})
+    try:
+        def run(a, shift):
+            if kernel == "gemm_residual_split":
+                return s.run(kernel, ["p"], a=a, w="w", partials="p", m=m, n=n, k=k, splits=splits,
+                             a_shift=shift)["p"]
+            s.write("x", x0)
+            cl = s.backend.begin()
+            cl.dispatch(kernel, s.fields(kernel, a=a, w="w", x="x", m=m, n=n, k=k, a_shift=shift))
+            s.backend.wait(s.backend.submit(cl))
+            cl.release()
+            return s.read("x")
+        y0, y8 = run("hi", 0), run("lo", 8)
+        assert np.isfinite(y0).all()
+        assert np.array_equal(y0.view(np.uint32), y8.view(np.uint32))
+    finally:
+        s.close()
+
+
 @pytest.mark.parametrize("T,pos0,max_pos", [(100, 37, 256), (300, 64, 512), (512, 64, 640), (1100, 37, 1152),
                                            (2048, 37, 2112), (2048, 64, 2112)])
 def test_gemm_qkv_rope_epilogue(T, pos0, max_pos):
