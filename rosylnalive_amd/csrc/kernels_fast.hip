@@ -258,8 +258,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     // q ^ (r % 8)), so a fragment read (16 rows, one chunk) spreads over the banks (padded 144-byte rows measured
     // 14 % of the register path's cycles stalled on bank conflicts)
     constexpr int STAGE = (BM + BN) * GBK;  // halves: the A tile then the W tile
-    // the two stages, or what the QKV epilogue needs after them (x32 32 KiB + the V^T tile 128 x 136 halves)
-    constexpr int LDS_HALVES = EPI == EPI_QKV ? (2 * STAGE > 33792 ? 2 * STAGE : 33792) : 2 * STAGE;
+    // LDS stages of the direct-to-LDS loop: three for 128 x 64 tiles (72 KiB, two blocks per CU still fit), else two
+    constexpr int NST = DMA && BN == 64 ? 3 : 2;
+    // the stages, or what the QKV epilogue needs after them (x32 32 KiB + the V^T tile 128 x 136 halves)
+    constexpr int LDS_HALVES = EPI == EPI_QKV ? (NST * STAGE > 33792 ? NST * STAGE : 33792) : NST * STAGE;
     __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALVES];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1, g = lane >> 4, c16 = lane & 15;
     // XCD-aware tile order. Blocks are dispatched round-robin over the 8 XCDs (block L, x fastest, on XCD L % 8), each
@@ -306,6 +308,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         // issues instructions i = 0, 1, ... for the 1 KiB blocks 4 i + w. A row past the matrix is clamped to its last row
         // (it only feeds outputs that are never stored); the k offset is a scalar.
         constexpr int NA = BM / 32, NB = BN / 32;  // load instructions per wave per stage
+        static_assert(NA + NB < 16, "vmcnt's low field");
         int aoff[NA], boff[NB];
     #pragma unroll
         for (int i = 0; i < NA; ++i) {
@@ -359,19 +362,25 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
             }
         };
-        // Two stages: step kt waits for its tile (this wave's loads, then the barrier for everyone's, which also means
-        // every wave is done reading the other stage), queues tile kt + 1 into the other stage and multiplies tile kt.
+        // NST stages: step kt waits for its tile (this wave's loads, then the barrier for everyone's, which also means
+        // every wave is done reading the stage of tile kt - 1), queues tile kt + NST - 1 into that stage and multiplies
+        // tile kt; NST - 1 tiles are in flight while it does. With three stages the wait leaves tile kt + 1's loads
+        // (the younger NA + NB of this wave's) outstanding: loads complete in issue order.
         // The LDS-only barrier: __syncthreads() would also make every wave wait for the loads just queued.
         const int nk = KE / GBK;
         issue(0, 0);
+        if (NST == 3 && nk > 1) issue(1, GBK);
         for (int kt = 0; kt < nk; ++kt) {
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile kt have landed in LDS
+            if (NST == 3 && kt + 1 < nk)
+                __builtin_amdgcn_s_waitcnt(0x0F70 | (NA + NB));  // vmcnt(NA + NB): tile kt has landed in LDS
+            else
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             lds_barrier();
 #if defined(LRM_GEMM_STAMPS)
             if (kt < kGemmStampSteps) GSTAMP(2 + kt);
 #endif
-            if (kt + 1 < nk) issue((kt + 1) & 1, (kt + 1) * GBK);  // uniform
-            compute(kt & 1);
+            if (kt + NST - 1 < nk) issue((kt + NST - 1) % NST, (kt + NST - 1) * GBK);  // uniform
+            compute(kt % NST);
         }
         GSTAMP(30);
     } else {
