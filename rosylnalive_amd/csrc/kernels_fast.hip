@@ -206,11 +206,12 @@ struct GemmArgs {
 // The stage-timing build (LRM_GEMM_STAMPS): wave 0 of every block of the direct-to-LDS loop records constant-clock
 // stamps, per GEMM kind (the epilogue), of the last launch of that kind: word 0 the hardware CU (HW_ID) and XCD
 // (XCC_ID) ids, 1 the block's start, 2 + kt tile kt landed (after the step's wait and barrier, kt < kGemmStampSteps),
+// 26 and 27 points inside the q|k|v epilogue (its tile staged in LDS; its rows read back and their squares summed),
 // 30 the main loop's end, 31 the epilogue's end. Lane k of wave 0 keeps stamp k in a register (one select per stamp)
 // and the lanes store them once, at the end, so no stamp store is in flight while the block runs; the shipped build
 // has none.
 #if defined(LRM_GEMM_STAMPS)
-constexpr int kGemmStampWords = 32, kGemmStampSteps = 28, kGemmStampBlocks = 4096, kGemmStampKinds = 5;
+constexpr int kGemmStampWords = 32, kGemmStampSteps = 24, kGemmStampBlocks = 4096, kGemmStampKinds = 5;
 __device__ uint64_t g_gemm_stamps[kGemmStampKinds][kGemmStampBlocks * kGemmStampWords];
 struct GemmStampEnd {  // the epilogue's end, at whichever return the lane leaves by
     uint64_t* at;
@@ -581,6 +582,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                         tile[rw * 128 + (col ^ ((rw & 15) << 2))] = acc[i][j][r];
                     }
             lds_barrier();  // LDS only: the loads above stay in flight
+            GSTAMP(26);
             if (row >= BM) return;  // 64-row tiles: threads 128 .. 255 have no row
             float x[2][32];
 #pragma unroll
@@ -596,6 +598,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
 #pragma unroll
             for (int k = 0; k < 32; ++k) ss = fmaf(x[1][k], x[1][k], fmaf(x[0][k], x[0][k], ss));
             ss += dpp_f<0xB1>(ss);  // + the other half of the row (lane t ^ 1)
+            GSTAMP(27);
             if (m >= p.M) return;
             const float rr = 1.0f / sqrtf(ss / 128.0f + p.eps);
             uint16_t* out = is_q ? p.q_out + size_t(m) * (p.qh * 128) + head * 128

@@ -7,7 +7,8 @@ Runs the Qwen3-0.6B-shaped fast forward of T synthetic tokens (random N(0, 0.02)
 stamps of the last launch of each GEMM kind (layer 27's: the q|k|v GEMM with its norm / RoPE / cache epilogue, gate/up
 with SwiGLU, and down_proj's k-split partials). Thread 0 of every workgroup stamps its start, the moment each k tile
 has landed in LDS (after the step's wait and barrier), the main loop's end and the epilogue's end (100 MHz constant
-clock). Printed per kernel: the launch's span, and over its workgroups the start offset, the time to the first tile,
+clock), and in the q|k|v epilogue of the q and k head tiles two points between (the tile staged in LDS; the rows read
+back and their squares summed). Printed per kernel: the launch's span, and over its workgroups the start offset, the time to the first tile,
 the k steps, the epilogue and the end offset, plus the median time of every k step.
 """
 import ctypes as C
@@ -36,8 +37,8 @@ def summarize(name, st):
     st = st[used]
     t0 = st[:, 1].min()
     us = lambda v: v / 100.0
-    # k steps recorded: words 2 .. 2 + n - 1 (the same n for every block of a launch)
-    nk = int(np.max(np.sum(st[:, 2:30] > 0, axis=1)))
+    # k steps recorded: words 2 .. 2 + n - 1 (the same n for every block of a launch, at most 24)
+    nk = int(np.max(np.sum(st[:, 2:26] > 0, axis=1)))
     landed = st[:, 2:2 + nk]
     start, first, loop_end, end = st[:, 1], landed[:, 0], st[:, 30], st[:, 31]
     steps = np.diff(landed, axis=1)  # tile kt landed -> tile kt + 1 landed: one step of MFMAs plus the wait
@@ -48,6 +49,11 @@ def summarize(name, st):
             ("k step (mean per block)", steps.mean(axis=1) if steps.size else np.zeros(len(st))),
             ("last tile's MFMAs", last), ("epilogue", end - loop_end), ("block total", end - start),
             ("end offset", end - t0)]
+    inner = (st[:, 26] > 0) & (st[:, 27] > 0)  # the q|k|v epilogue's points (q and k head tiles)
+    if inner.any():
+        e = st[inner]
+        rows[5:5] = [("  epilogue: tile to LDS", e[:, 26] - e[:, 30]), ("  epilogue: rows back, sums", e[:, 27] - e[:, 26]),
+                     ("  epilogue: norm, RoPE, stores", e[:, 31] - e[:, 27])]
     print(f"{name}: {len(st)} workgroups, {nk} k steps each, {len(per_cu)} distinct CUs "
           f"(workgroups per CU: {np.bincount(per_cu).nonzero()[0].tolist()}), launch span {us(end.max() - t0):.2f} us")
     print(f"  {'':28s} {'median':>8s} {'p10':>8s} {'p90':>8s} {'max':>8s}  (us)")
