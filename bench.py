@@ -8,7 +8,8 @@ step, replayed as a HIP graph, position and token in device memory). Defaults K 
 Also measured in the same run (extra keys, skipped by --no-extras): 512-token prefill with all 512 x 151936 logits,
 2048-token prefill with last-row logits, decode at 4096 context, the isolated GQA prefill attention at T = 2048, and the
 batched decode of 16 sequences of a Qwen3-1.7B-shaped model at 8K context, and the same decode through the per-stage
-kernel list (LRM_HIP_DECODE=kernels). The roofline is that of the dominant decode kernel (decode_step_persistent, timed
+kernel list (LRM_HIP_DECODE=kernels). The prefill and attention extras warm up for a second of back-to-back runs, then
+report the fastest of seven runs (ms / us) and their median (ms_median / us_median). The roofline is that of the dominant decode kernel (decode_step_persistent, timed
 with HIP events on the device stream). cpu_baseline is the oracle on the
 host cores on a bounded sample of the decode workload (--no-cpu skips it); cpu_configs times the oracle on the other
 workloads (tiny model, attention, 512-token prefill, a sample of the batched decode).
@@ -33,6 +34,7 @@ ROOFLINE_POS0 = 392                   # the roofline launches run at context ROO
 COPY_BYTES = 1 << 30                  # the reference copy of the traffic calibration: 4 x the last-level cache
 CPU_DECODE_STEPS = 128                # the bounded CPU decode sample (about 10 s on 16 host cores)
 CTX4K_CHECK_STEPS = 8                 # decode steps of the 4K-context leg whose ids the oracle checks
+WARM_S, RUNS = 1.0, 7                 # the prefill and attention extras: seconds of warm-up, then timed runs
 
 
 def reference_copy() -> float:
@@ -187,16 +189,25 @@ def main():
     def kv_bytes(ctx):
         return 2 * L * KVH * ctx * HD * 2
 
+    def timed_runs(run):
+        """Warm-up for WARM_S seconds of back-to-back runs, then RUNS more: (fastest, median) of their device times."""
+        t_end = time.time() + WARM_S
+        while time.time() < t_end:
+            run()
+        times = sorted(run() for _ in range(RUNS))
+        return times[0], times[RUNS // 2]
+
     def prefill(T, rows, name):
-        """The forward of T synthetic tokens, logits of the last `rows` rows: the best of three warm runs."""
+        """The forward of T synthetic tokens, logits of the last `rows` rows: the fastest of the timed runs (device
+        time), with their median."""
         ids = synthetic_ids(args.seed, name, T, V)
-        model.forward(ids, 0, logits_rows=rows)
-        best = min((model.forward(ids, 0, logits_rows=rows), model.last_ms())[1] for _ in range(3))
+        best, med = timed_runs(lambda: (model.forward(ids, 0, logits_rows=rows), model.last_ms())[1])
         fl = 2 * T * L * lin_params_layer + 2 * rows * V * H + L * QH * (T * (T + 1) // 2) * (4 * HD + 3)
-        return {"ms": round(best, 3), "tok_s": round(T / (best / 1e3), 1), "tflops": round(fl / (best / 1e3) / 1e12, 1),
+        return {"ms": round(best, 3), "ms_median": round(med, 3), "tok_s": round(T / (best / 1e3), 1),
+                "tflops": round(fl / (best / 1e3) / 1e12, 1),
                 "mfma_frac": round(fl / (best / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flop": fl}
 
-    def attention_2048():
+    def attention_2048_us():
         """The isolated GQA prefill attention at T = 2048 on the caches a 2048-token prefill wrote, each layer's in
         turn, 28 launches in one list timed with HIP events."""
         tok = model.token
@@ -210,14 +221,18 @@ def main():
         cl.end_timer(tm)
         comp = backend.wait(backend.submit(cl))
         cl.release()
-        a_us = comp.timers[0].duration_ns / 1e3 / L
+        return comp.timers[0].duration_ns / 1e3 / L
+
+    def attention_2048():
+        """attention_2048_us's fastest timed run, with their median."""
+        a_us, med = timed_runs(attention_2048_us)
         a_fl = QH * (2048 * 2049 // 2) * (4 * HD + 3)
-        return {"us": round(a_us, 2), "tflops": round(a_fl / (a_us * 1e-6) / 1e12, 1),
+        return {"us": round(a_us, 2), "us_median": round(med, 2), "tflops": round(a_fl / (a_us * 1e-6) / 1e12, 1),
                 "mfma_frac": round(a_fl / (a_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4), "flop": a_fl}
 
     if args.only == "attention_2048":
         prefill(2048, 1, "bench/prefill2048")
-        res = min((attention_2048() for _ in range(3)), key=lambda r: r["us"])
+        res = attention_2048()
         log(args.only, res)
         print(json.dumps({"workload": args.only, **res}), flush=True)
         model.close()
