@@ -206,7 +206,8 @@ struct GemmArgs {
 // The stage-timing build (LRM_GEMM_STAMPS): wave 0 of every block of the direct-to-LDS loop records constant-clock
 // stamps, per GEMM kind (the epilogue), of the last launch of that kind: word 0 the hardware CU (HW_ID) and XCD
 // (XCC_ID) ids, 1 the block's start, 2 + kt tile kt landed (after the step's wait and barrier, kt < kGemmStampSteps),
-// 26 and 27 points inside the q|k|v epilogue (its tile staged in LDS; its rows read back and their squares summed),
+// 28, 29, 26 and 27 points inside the q|k|v epilogue (past the barrier that ends the main loop; its global loads
+// issued; its tile staged in LDS; its rows read back and their squares summed),
 // 30 the main loop's end, 31 the epilogue's end. Lane k of wave 0 keeps stamp k in a register (one select per stamp)
 // and the lanes store them once, at the end, so no stamp store is in flight while the block runs; the shipped build
 // has none.
@@ -550,6 +551,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     if constexpr (EPI == EPI_QKV) {
         const int head = tx;
         if (head < p.qh + p.kvh) {
+            GSTAMP(28);
             const bool is_q = head < p.qh;
             const int row = t >> 1, hf = t & 1, m = m0 + row;
             // Every global load of the epilogue first: the norm weights and this row's cos / sin (the row clamped to
@@ -571,6 +573,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
                 s0v[u] = *reinterpret_cast<const f32x4*>(snt + 8 * u);
                 s1v[u] = *reinterpret_cast<const f32x4*>(snt + 8 * u + 4);
             }
+            GSTAMP(29);
             float* tile = reinterpret_cast<float*>(lds);
 #pragma unroll
             for (int i = 0; i < MI; ++i)

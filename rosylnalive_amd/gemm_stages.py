@@ -7,8 +7,9 @@ Runs the Qwen3-0.6B-shaped fast forward of T synthetic tokens (random N(0, 0.02)
 stamps of the last launch of each GEMM kind (layer 27's: the q|k|v GEMM with its norm / RoPE / cache epilogue, gate/up
 with SwiGLU, and down_proj's k-split partials). Thread 0 of every workgroup stamps its start, the moment each k tile
 has landed in LDS (after the step's wait and barrier), the main loop's end and the epilogue's end (100 MHz constant
-clock), and in the q|k|v epilogue of the q and k head tiles two points between (the tile staged in LDS; the rows read
-back and their squares summed). Printed per kernel: the launch's span, and over its workgroups the start offset, the time to the first tile,
+clock), and in the q|k|v epilogue of the q and k head tiles four points between (past the barrier that ends the main
+loop; the cos / sin and norm weight loads issued; the tile staged in LDS; the rows read back and their squares
+summed). Printed per kernel: the launch's span, and over its workgroups the start offset, the time to the first tile,
 the k steps, the epilogue and the end offset, plus the median time of every k step.
 """
 import ctypes as C
@@ -52,7 +53,9 @@ def summarize(name, st):
     inner = (st[:, 26] > 0) & (st[:, 27] > 0)  # the q|k|v epilogue's points (q and k head tiles)
     if inner.any():
         e = st[inner]
-        rows[5:5] = [("  epilogue: tile to LDS", e[:, 26] - e[:, 30]), ("  epilogue: rows back, sums", e[:, 27] - e[:, 26]),
+        rows[5:5] = [("  epilogue: end-of-loop barrier", e[:, 28] - e[:, 30]),
+                     ("  epilogue: issue table loads", e[:, 29] - e[:, 28]),
+                     ("  epilogue: tile to LDS", e[:, 26] - e[:, 29]), ("  epilogue: rows back, sums", e[:, 27] - e[:, 26]),
                      ("  epilogue: norm, RoPE, stores", e[:, 31] - e[:, 27])]
     print(f"{name}: {len(st)} workgroups, {nk} k steps each, {len(per_cu)} distinct CUs "
           f"(workgroups per CU: {np.bincount(per_cu).nonzero()[0].tolist()}), launch span {us(end.max() - t0):.2f} us")
