@@ -1902,9 +1902,10 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* part, uint32_t
 
 // ================================================================ 32-34 skinny GEMMs (batched decode)
 // Y[r, n] = sum_k A[r, k] W[n, k] for M <= 16 rows (the sequences of a batched decode step), on f16 operands: the
-// weights are read once for all rows. A block owns NT 16-column MFMA tiles (SwiGLU: gate columns j0 .. j0 + 15 and
-// the matching up columns; two tiles also for the plain GEMM, whose wide N (the lm_head) would otherwise read the A
-// rows from L2 once per 16 columns; one for the residual GEMMs, whose N = hidden needs the blocks) and its 8 waves
+// weights are read once for all rows. A block owns NT 16-column MFMA tiles (SwiGLU: 8 NT gate columns j0 .. and the
+// matching up columns, so the block's 16 NT columns hold 8 NT pairs; two tiles also for the plain GEMM, whose wide N
+// (the lm_head) would otherwise read the A rows from L2 once per 16 columns; one for the residual GEMMs, whose
+// N = hidden needs the blocks) and its 8 waves
 // split K in eight. Each wave streams its slice of the W rows straight into MFMA B operands (lane: row c16, 8 halves at
 // k + 8g, so 64 contiguous bytes per row per 32-k step) with the A rows from L2, 128 k per iteration, and the next
 // iteration's loads in flight while the current one multiplies (two named register sets). The partial tiles of the 8
@@ -1917,47 +1918,55 @@ enum SkEpi { SK_F32 = 0, SK_RESID = 1, SK_SWIGLU = 2, SK_PART = 3 };
 template <int EPI, int NT>
 __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const uint16_t* w, float* y32, uint16_t* y16,
                                                      int M, int N, int K, int inter, float ascale) {
-    static_assert(NT == 1 || NT == 2, "MFMA column tiles per block");
-    static_assert(EPI != SK_SWIGLU || NT == 2, "SwiGLU pairs a gate and an up tile");
+    static_assert(NT >= 1 && NT <= 3, "MFMA column tiles per block");
+    static_assert(EPI != SK_SWIGLU || NT >= 2, "SwiGLU: gate and up columns of 8 NT pairs");
+    static_assert(EPI == SK_SWIGLU || NT <= 2, "one output per thread: 256 NT <= 512");
     __shared__ float red[kSkWaves][NT][256];
     // the k range of this block (a part of k for SK_PART); the A and W rows are still K long
     const int KS = EPI == SK_PART ? K / int(gridDim.y) : K, kz = EPI == SK_PART ? int(blockIdx.y) * KS : 0;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6, g = lane >> 4, c16 = lane & 15;
-    int n0, n1 = 0;
-    if (EPI == SK_SWIGLU) {
-        const int j = min(int(blockIdx.x) * 16 + c16, inter - 1);
-        n0 = j;
-        n1 = inter + j;
-    } else {
-        n0 = min(int(blockIdx.x) * (16 * NT) + c16, N - 1);
-        n1 = min(int(blockIdx.x) * (16 * NT) + 16 + c16, N - 1);
+    // the W row of block column 16 u + c16 in tile u: SwiGLU blocks own P = 8 NT gate / up pairs, columns 0 .. P - 1
+    // the gate rows j0 .. j0 + P - 1, columns P .. 2 P - 1 the matching up rows (clamped to the last pair)
+    constexpr int P = 8 * NT;
+    int nr[NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        const int lc = 16 * u + c16;
+        if (EPI == SK_SWIGLU) {
+            const int j = min(int(blockIdx.x) * P + (lc < P ? lc : lc - P), inter - 1);
+            nr[u] = lc < P ? j : inter + j;
+        } else {
+            nr[u] = min(int(blockIdx.x) * (16 * NT) + lc, N - 1);
+        }
     }
     const int kper = KS / kSkWaves, niter = kper / 128;  // kper a multiple of 128
     const int kb = kz + wv * kper + 8 * g;
     const uint16_t* ap = a + size_t(min(c16, M - 1)) * K + kb;
-    const uint16_t* w0 = w + size_t(n0) * K + kb;
-    const uint16_t* w1 = w + size_t(n1) * K + kb;
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    const uint16_t* wp[NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) wp[u] = w + size_t(nr[u]) * K + kb;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
     u32x4 av[2][4], bw[2][NT][4];
     auto load = [&](auto set, int it) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value;
         const int k = it * 128;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            bw[S][0][s] = *reinterpret_cast<const u32x4*>(w0 + k + 32 * s);
-            if constexpr (NT == 2) bw[S][NT - 1][s] = *reinterpret_cast<const u32x4*>(w1 + k + 32 * s);
+#pragma unroll
+            for (int u = 0; u < NT; ++u) bw[S][u][s] = *reinterpret_cast<const u32x4*>(wp[u] + k + 32 * s);
             av[S][s] = *reinterpret_cast<const u32x4*>(ap + k + 32 * s);
         }
     };
     auto mma = [&](auto set) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av[S][s]), as_f16x8(bw[S][0][s]), acc0, 0, 0, 0);
-            if constexpr (NT == 2)
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av[S][s]), as_f16x8(bw[S][NT - 1][s]), acc1, 0, 0,
-                                                              0);
-        }
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int u = 0; u < NT; ++u)
+                acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av[S][s]), as_f16x8(bw[S][u][s]), acc[u], 0, 0,
+                                                                0);
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
@@ -1987,20 +1996,22 @@ __global__ __launch_bounds__(512) void k_gemm_skinny(const uint16_t* a, const ui
         mma(S0{});
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        red[wv][0][lane * 4 + i] = acc0[i];
-        if constexpr (NT == 2) red[wv][NT - 1][lane * 4 + i] = acc1[i];
-    }
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int u = 0; u < NT; ++u) red[wv][u][lane * 4 + i] = acc[u][i];
     __syncthreads();
     // element e of a tile: lane e / 4, register e % 4 -> row 4 (lane / 16) + e % 4, column lane % 16
     if (EPI == SK_SWIGLU) {
-        if (t >= 256) return;
-        const int l = t >> 2, row = 4 * (l >> 4) + (t & 3), col = int(blockIdx.x) * 16 + (l & 15);
+        // thread t < 16 P: row t / P, pair jl = t % P (its gate at block column jl, its up at P + jl)
+        if (t >= 16 * P) return;
+        const int row = t / P, jl = t - row * P, col = int(blockIdx.x) * P + jl;
+        auto elem = [&](int c) { return ((row >> 2) * 16 + (c & 15)) * 4 + (row & 3); };
+        const int gt = jl >> 4, ge = elem(jl), ut = (P + jl) >> 4, ue = elem(P + jl);
         float gv = 0.f, uv = 0.f;
 #pragma unroll
         for (int i = 0; i < kSkWaves; ++i) {
-            gv += red[i][0][t];
-            uv += red[i][NT - 1][t];
+            gv += red[i][gt][ge];
+            uv += red[i][ut][ue];
         }
         if (row < M && col < inter) {
             const uint16_t hv = f2h(gv / (1.0f + __expf(-gv)) * uv * ascale);
@@ -2417,11 +2428,21 @@ static void l_gemm_skinny_resid(const PreparedDispatch& pd, void* const* p, hipS
                        (const uint16_t*)p[1], (float*)p[2], (uint16_t*)nullptr, int(w[4]), int(w[5]), int(w[6]), 0,
                        a_unscale(w[7]));
 }
+// gate / up pairs per skinny SwiGLU block: 16 (two MFMA column tiles), or 24 (three) where that takes the grid from
+// over one round of 256 blocks (one per CU) to one. A block's time barely depends on its k loop at these sizes, so a
+// round costs about the same either way: the Qwen3-1.7B gate/up (6144 pairs at 16 rows) 384 blocks took 12.6 us, 256
+// blocks of 16 pairs (4096) 7.3 us.
+static int skinny_swiglu_pairs(uint32_t inter) { return (inter + 15) / 16 > 256 && (inter + 23) / 24 <= 256 ? 24 : 16; }
 static void l_gemm_skinny_swiglu(const PreparedDispatch& pd, void* const* p, hipStream_t s) {
     const uint32_t* w = pd.words.data();
-    hipLaunchKernelGGL((k_gemm_skinny<SK_SWIGLU, 2>), dim3((w[5] + 15) / 16), dim3(512), 0, s, (const uint16_t*)p[0],
-                       (const uint16_t*)p[1], (float*)nullptr, (uint16_t*)p[2], int(w[4]), 0, int(w[6]), int(w[5]),
-                       a_scale(w[7]));
+    if (skinny_swiglu_pairs(w[5]) == 24)
+        hipLaunchKernelGGL((k_gemm_skinny<SK_SWIGLU, 3>), dim3((w[5] + 23) / 24), dim3(512), 0, s,
+                           (const uint16_t*)p[0], (const uint16_t*)p[1], (float*)nullptr, (uint16_t*)p[2], int(w[4]), 0,
+                           int(w[6]), int(w[5]), a_scale(w[7]));
+    else
+        hipLaunchKernelGGL((k_gemm_skinny<SK_SWIGLU, 2>), dim3((w[5] + 15) / 16), dim3(512), 0, s,
+                           (const uint16_t*)p[0], (const uint16_t*)p[1], (float*)nullptr, (uint16_t*)p[2], int(w[4]), 0,
+                           int(w[6]), int(w[5]), a_scale(w[7]));
 }
 
 // 36 decode_advance: argmax, state, out_ids, batch, max_steps
@@ -2813,7 +2834,10 @@ std::vector<KernelSpec> fast_catalog() {
                  }});
     // 34 gemm_skinny_swiglu: a, w (2 inter rows), y, m, inter, k, a_shift
     c.push_back({"gemm_skinny_swiglu", "fast", {512, 1, 1}, false,
-                 [](const uint32_t* w) { return Grid3{(int64_t(w[5]) + 15) / 16, 1, 1}; },
+                 [](const uint32_t* w) {
+                     const int64_t pairs = skinny_swiglu_pairs(w[5]);
+                     return Grid3{(int64_t(w[5]) + pairs - 1) / pairs, 1, 1};
+                 },
                  {TOK_R("a", DT(F16)), TOK_R("w", DT(F16)), TOK_W("y", DT(F16)), U32F("m"), U32F("inter"), U32F("k"),
                   U32F("a_shift")},
                  [](const uint32_t* w, const uint32_t* c) {

@@ -625,18 +625,26 @@ def test_gemm_skinny(m, n, k):
         s.close()
 
 
-@pytest.mark.parametrize("m,inter,k", [(11, 3072, 1024), (16, 6144, 2048), (3, 100, 1024)])
+@pytest.mark.parametrize("m,inter,k", [(11, 3072, 1024), (16, 6144, 2048), (3, 100, 1024), (7, 6010, 1024)])
 def test_gemm_skinny_swiglu(m, inter, k):
-    """Each block pairs 16 gate columns with the matching 16 up columns; inter 100 ends in a partial block."""
+    """Each block pairs 16 gate columns with the matching 16 up columns, or 24 with 24 where that makes one round of
+    256 blocks (6144 and 6010 pairs: 256 and 251 blocks); inter 100 and 6010 end in a partial block. The 24-pair
+    blocks give the bits of the 16-pair ones: the first 4096 pairs again as a 4096-pair GEMM (256 blocks of 16)."""
     r = np.random.default_rng(21)
     a = f16(r.standard_normal((m, k)))
     w = f16(r.standard_normal((2 * inter, k)) * 0.05)
-    s = Session({"a": (F16, (m, k), RO, a), "w": (F16, w.shape, RO, w), "y": (F16, (m, inter), 0, None)})
+    n16 = min(inter, 4096)
+    w16 = np.concatenate([w[:n16], w[inter:inter + n16]])
+    s = Session({"a": (F16, (m, k), RO, a), "w": (F16, w.shape, RO, w), "y": (F16, (m, inter), 0, None),
+                 "w16": (F16, w16.shape, RO, w16), "y16": (F16, (m, n16), 0, None)})
     try:
-        y = hwiden(s.run("gemm_skinny_swiglu", ["y"], a="a", w="w", y="y", m=m, inter=inter, k=k)["y"])
+        yb = s.run("gemm_skinny_swiglu", ["y"], a="a", w="w", y="y", m=m, inter=inter, k=k)["y"]
+        y = hwiden(yb)
         h = hwiden(a).astype(np.float64) @ hwiden(w).astype(np.float64).T
         g, u = h[:, :inter], h[:, inter:]
         assert metrics.rel_l2(y, g / (1 + np.exp(-g)) * u) < 2e-3
+        y16 = s.run("gemm_skinny_swiglu", ["y16"], a="a", w="w16", y="y16", m=m, inter=n16, k=k)["y16"]
+        assert np.array_equal(y16, yb[:, :n16])
     finally:
         s.close()
 
