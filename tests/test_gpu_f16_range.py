@@ -239,3 +239,38 @@ def test_set_swiglu_shift_ahead(model):
     assert m.swiglu_shift() == 0
     lg0, _ = m.forward(ids, 0, logits_rows=48)
     assert lg0.tobytes() == base.tobytes()
+
+
+def test_chunked_shifted_prefill_then_decode_match_the_oracle(model):
+    """The spike weights with a 150-token prompt (three chunks of max_tokens 64): the whole call reruns shifted and its
+    logits meet the bound against the oracle; then one-sequence decode steps (whose SwiGLU output stays float32),
+    teacher-forced, against the oracle's rows at those positions. The restored model runs as before."""
+    m, w = model
+    prompt = synthetic_ids(23, "range/chunked", 150, CFG.vocab)
+    cont = synthetic_ids(23, "range/chunked/cont", 6, CFG.vocab)
+    bad = _swiglu_spikes(w)
+    w2 = dict(w)
+    w2.update(bad)
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), CFG.max_pos)
+    orc = cpuref.QwenOracle(CFG.oracle_dict(), w2, cos, sin)
+    ol = orc.forward(orc.new_cache(), 0, np.concatenate([prompt, cont]))
+    try:
+        for n, v in bad.items():
+            m.set_weight(n, v)
+        lg, _ = m.forward(prompt, 0, logits_rows=150)
+        assert m.swiglu_shift() == 8
+        err, top1 = metrics.max_abs(lg, ol[:150]), metrics.top1_agreement(lg, ol[:150])
+        worst = 0.0
+        for i, tok in enumerate(cont):
+            pos = prompt.size + i
+            m.decode_set(int(tok), pos)
+            m.decode_run(1)
+            worst = max(worst, metrics.max_abs(m.read_logits(1), ol[pos:pos + 1]))
+        print(f"chunked shifted prefill: max-abs {err:.4g}, top-1 {top1:.4f}; decode after it: worst max-abs "
+              f"{worst:.4g}", flush=True)
+        assert err <= 2e-2 and top1 >= 0.99 and worst <= 2e-2
+    finally:
+        for n in bad:
+            m.set_weight(n, w[n])
+    assert m.swiglu_shift() == 0
+    _clean_forward(m, prompt[:48])
