@@ -3,6 +3,7 @@
 - Qwen3-0.6B shape (28 layers, hidden 1024, 16/8 heads, head_dim 128, SwiGLU 3072, vocab 151,936, tied embeddings),
   random N(0, 0.02) bf16 weights, norms 1:
   * a 512-token prefill, every one of the 512 x 151,936 logits against the oracle;
+  * a 2048-token prefill, the last 64 rows' logits and a sample of the K / V cache rows against the oracle;
   * a 128-token prompt then 256 greedy tokens: the device's greedy ids are the oracle's greedy ids (the oracle's
     argmax along the device's sequence equals the device's id at every step, up to near-ties), and teacher-forced
     decode steps along that sequence match the oracle's logits.
@@ -106,6 +107,39 @@ def _row_err(dev, ref):
     cache rows against the oracle's float32 rows."""
     scale = np.maximum(1.0, np.max(np.abs(ref), axis=-1, keepdims=True))
     return float(np.max(np.abs(dev - ref) / scale))
+
+
+def test_qwen3_0_6b_prefill_2048_against_the_oracle():
+    """The 2048-token prefill the MFMA bar is quoted at (one 2048-row forward from position 0: every GEMM on the
+    direct-to-LDS loop, the k-split residual GEMMs on three stages, the attention's long tiles split over two
+    workgroups): the last 64 rows' logits and the K / V cache rows of layers 0, 14 and 27 (every 64th row and the last
+    eight) against the oracle's prefill of the same 2048 ids."""
+    cfg = QwenConfig.qwen3_0_6b(max_pos=2048)
+    T, rows = 2048, 64
+    w = synthetic_weights(cfg, seed=41)
+    ids = synthetic_ids(41, "fullsize/prefill2048", T, cfg.vocab)
+    b = HipBackend(0)
+    m = QwenModel(b, cfg, mode="fast", max_tokens=T)
+    try:
+        m.load_weights(w)
+        lg, am = m.forward(ids, 0, logits_rows=rows)
+        picked = np.r_[np.arange(0, T, 64), np.arange(T - 8, T)]
+        dev = {(l, which): m.read_cache(l, which, 0, T)[picked] for l in (0, 14, 27) for which in ("k", "v")}
+    finally:
+        m.close()
+        b.close()
+    cos, sin = cpuref.rope_table(inv_freq_bits(128), cfg.max_pos)
+    orc = cpuref.QwenOracle(cfg.oracle_dict(), w, cos, sin)
+    kc, vc = orc.new_cache()
+    ol = orc.forward((kc, vc), 0, ids)[-rows:]
+    err, top1 = metrics.max_abs(lg, ol), metrics.top1_agreement(lg, ol)
+    ok, gaps = _near_ties(lg, ol, err)
+    cache = max(_row_err(dev[(l, which)], (kc if which == "k" else vc)[l][picked]) for (l, which) in dev)
+    print(f"0.6B prefill 2048, last {rows} rows: max-abs {err:.4g} (range {ol.min():.3g}..{ol.max():.3g}), top-1 "
+          f"{top1:.4f}, flip gaps {np.round(gaps, 5).tolist()}; cache rows within {cache:.3g}", flush=True)
+    assert np.isfinite(lg).all()
+    assert err <= MAX_ABS and top1 >= TOP1 and ok
+    assert am == int(np.argmax(lg[-1])) and cache <= 1e-2
 
 
 def test_qwen3_0_6b_decode_at_4k_context():
