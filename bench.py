@@ -158,7 +158,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill_2048", "prefill_512", "attention_2048", "roofline"],
+    ap.add_argument("--only", choices=["prefill_2048", "prefill_512", "attention_2048", "roofline", "decode_batch16",
+                                       "decode_4k"],
                     help="run only this workload (for profiling runs) and print its figures as the JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -230,6 +231,75 @@ def main():
         return {"us": round(a_us, 2), "us_median": round(med, 2), "tflops": round(a_fl / (a_us * 1e-6) / 1e12, 1),
                 "mfma_frac": round(a_fl / (a_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4), "flop": a_fl}
 
+    def decode_batch16(sample):
+        """Config E: Qwen3-1.7B shape, 16 sequences whose caches hold 8192 positions of bf16-valued N(0, 1) (stored
+        fp16), 2 warmup + 64 timed steps of all 16 sequences. Returns its figures and, when `sample`, sequence 0's
+        caches and ids for the oracle's check."""
+        cfg_e = QwenConfig.qwen3_1_7b(max_pos=8192 + 128)
+        w_e = synthetic_weights(cfg_e, seed=args.seed)
+        be_e = HipBackend(0)
+        m_e = QwenModel(be_e, cfg_e, mode="fast", max_tokens=16, batch=16)
+        try:
+            m_e.load_weights(w_e)
+            del w_e
+            m_e.fill_cache_random(args.seed, 8192)
+            toks = synthetic_ids(args.seed, "bench/batch16", 16, cfg_e.vocab)
+            e_ids = m_e.decode_batch(toks, [8192] * 16, 2)
+            m_e.decode_batch(toks, [8192] * 16, 64)
+            e_ms = m_e.last_ms()
+            e_w = cfg_e.param_count() * 2
+            e_bytes = sum(e_w + 16 * 2 * cfg_e.layers * cfg_e.kv_heads * (8192 + s + 1) * cfg_e.head_dim * 2
+                          for s in range(64))
+            res = {"tok_s": round(16 * 64 / (e_ms / 1e3), 1), "ms_per_step": round(e_ms / 64, 4),
+                   "gbs": round(e_bytes / (e_ms / 1e3) / 1e9, 1),
+                   "hbm_frac": round(e_bytes / (e_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "bytes_per_step": int(e_bytes / 64),
+                   "workload": "Qwen3-1.7B shape, 16 sequences, context 8193..8256, greedy, skinny MFMA GEMMs over "
+                               "fp16 weight copies"}
+            smp = None
+            if sample:  # sequence 0's caches, for the oracle's sample of this workload
+                smp = {"cfg": cfg_e, "tok": int(toks[0]), "ids": e_ids[:, 0].tolist(),
+                       "k": [m_e.read_cache(l, "k", 0, 8192, seq=0) for l in range(cfg_e.layers)],
+                       "v": [m_e.read_cache(l, "v", 0, 8192, seq=0) for l in range(cfg_e.layers)]}
+            return res, smp
+        finally:
+            m_e.close()
+            be_e.close()
+
+    def decode_4k(sample):
+        """Decode at 4096 context: a real 4096-token prefill (two chunks), then 4 + 64 decode steps (context 4101 ..
+        4164), the 64 timed. Returns its figures and, when `sample`, the prefill's caches and the first ids for the
+        oracle's check."""
+        ids = synthetic_ids(args.seed, "bench/ctx4k", 4096, V)
+        _, nxt = model.forward(ids, 0, logits_rows=1)
+        model.decode_set(int(nxt), 4096)
+        model.decode_run(4)
+        model.decode_run(64)
+        d_ms = model.last_ms()
+        smp = None
+        if sample:  # the prefill's caches and the first ids, for the oracle's check of this leg
+            smp = {"first": int(nxt), "ids": model.decode_ids(CTX4K_CHECK_STEPS).tolist(),
+                   "k": [model.read_cache(l_, "k", 0, 4096) for l_ in range(L)],
+                   "v": [model.read_cache(l_, "v", 0, 4096) for l_ in range(L)]}
+        b4 = sum(weight_bytes + kv_bytes(4096 + 4 + s + 1) for s in range(64))
+        return {"tok_s": round(64 / (d_ms / 1e3), 1), "ms_per_token": round(d_ms / 64, 4),
+                "gbs": round(b4 / (d_ms / 1e3) / 1e9, 1), "hbm_frac": round(b4 / (d_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                "bytes_per_token": int(b4 / 64)}, smp
+
+    if args.only == "decode_4k":
+        res, _ = decode_4k(False)
+        log(args.only, res)
+        print(json.dumps({"workload": args.only, **res}), flush=True)
+        model.close()
+        backend.close()
+        return
+    if args.only == "decode_batch16":
+        res, _ = decode_batch16(False)
+        log(args.only, res)
+        print(json.dumps({"workload": args.only, **res}), flush=True)
+        model.close()
+        backend.close()
+        return
     if args.only == "attention_2048":
         prefill(2048, 1, "bench/prefill2048")
         res = attention_2048()
@@ -408,22 +478,7 @@ def main():
         # the isolated GQA prefill attention at T = 2048 on the caches the prefill just wrote
         out["attention_prefill_2048"] = attention_2048()
         log("attention 2048:", out["attention_prefill_2048"])
-        # decode at 4096 context: a real 4096-token prefill (two chunks), then 64 decode steps
-        ids = synthetic_ids(args.seed, "bench/ctx4k", 4096, V)
-        _, nxt = model.forward(ids, 0, logits_rows=1)
-        model.decode_set(int(nxt), 4096)
-        model.decode_run(4)
-        model.decode_run(64)
-        d_ms = model.last_ms()
-        if not args.no_cpu:  # the prefill's caches and the first ids, for the oracle's check of this leg
-            ctx4k_sample = {"first": int(nxt), "ids": model.decode_ids(CTX4K_CHECK_STEPS).tolist(),
-                            "k": [model.read_cache(l_, "k", 0, 4096) for l_ in range(L)],
-                            "v": [model.read_cache(l_, "v", 0, 4096) for l_ in range(L)]}
-        b4 = sum(weight_bytes + kv_bytes(4096 + 4 + s + 1) for s in range(64))
-        out["decode_4k"] = {"tok_s": round(64 / (d_ms / 1e3), 1), "ms_per_token": round(d_ms / 64, 4),
-                            "gbs": round(b4 / (d_ms / 1e3) / 1e9, 1),
-                            "hbm_frac": round(b4 / (d_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-                            "bytes_per_token": int(b4 / 64)}
+        out["decode_4k"], ctx4k_sample = decode_4k(not args.no_cpu)
         log("decode 4k:", out["decode_4k"])
 
         # the same decode workload through the per-stage kernel list (171 launches per token in one HIP graph)
@@ -446,36 +501,8 @@ def main():
             m_k.close()
             be_k.close()
 
-        # batched decode: Qwen3-1.7B shape, 16 sequences whose caches hold 8192 positions of bf16-valued N(0, 1)
-        # (stored fp16), 2 warmup + 64 timed steps of all 16 sequences
-        cfg_e = QwenConfig.qwen3_1_7b(max_pos=8192 + 128)
-        w_e = synthetic_weights(cfg_e, seed=args.seed)
-        be_e = HipBackend(0)
-        m_e = QwenModel(be_e, cfg_e, mode="fast", max_tokens=16, batch=16)
-        m_e.load_weights(w_e)
-        del w_e
-        m_e.fill_cache_random(args.seed, 8192)
-        toks = synthetic_ids(args.seed, "bench/batch16", 16, cfg_e.vocab)
-        e_ids = m_e.decode_batch(toks, [8192] * 16, 2)
-        m_e.decode_batch(toks, [8192] * 16, 64)
-        e_ms = m_e.last_ms()
-        e_w = cfg_e.param_count() * 2
-        e_bytes = sum(e_w + 16 * 2 * cfg_e.layers * cfg_e.kv_heads * (8192 + s + 1) * cfg_e.head_dim * 2
-                      for s in range(64))
-        out["decode_batch16_1.7b_8k"] = {
-            "tok_s": round(16 * 64 / (e_ms / 1e3), 1), "ms_per_step": round(e_ms / 64, 4),
-            "gbs": round(e_bytes / (e_ms / 1e3) / 1e9, 1),
-            "hbm_frac": round(e_bytes / (e_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-            "bytes_per_step": int(e_bytes / 64),
-            "workload": "Qwen3-1.7B shape, 16 sequences, context 8193..8256, greedy, skinny MFMA GEMMs over fp16 "
-                        "weight copies"}
+        out["decode_batch16_1.7b_8k"], e_sample = decode_batch16(not args.no_cpu)
         log("decode batch 16 (1.7B, 8K):", out["decode_batch16_1.7b_8k"])
-        if not args.no_cpu:  # sequence 0's caches, for the oracle's sample of this workload
-            e_sample = {"cfg": cfg_e, "tok": int(toks[0]), "ids": e_ids[:, 0].tolist(),
-                        "k": [m_e.read_cache(l, "k", 0, 8192, seq=0) for l in range(cfg_e.layers)],
-                        "v": [m_e.read_cache(l, "v", 0, 8192, seq=0) for l in range(cfg_e.layers)]}
-        m_e.close()
-        be_e.close()
 
     if not args.no_cpu:
         # The oracle (CpuRef F32 restated in C, parallel over independent outputs) on the host's cores.
