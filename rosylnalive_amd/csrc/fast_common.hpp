@@ -125,6 +125,50 @@ __device__ __forceinline__ float cross_rows_max(float v) {
 
 __device__ __forceinline__ float wave_sum(float v) { return cross_rows_sum(row_sum16(v)); }
 
+// The wave sums of R = 2, 4 or 8 values per lane at once (row k = v[k] over the 64 lanes), each exchange step swapping
+// half of the rows instead of reducing every row alone: with v_permlane32_swap(A = v[i], B = v[R/2 + i]) lanes 0-31
+// get the upper lane's v[i] and lanes 32-63 the lower lane's v[R/2 + i], so the sum of the two results is row i's pair
+// sum in the lower half and row R/2 + i's in the upper (R/2 swaps for R rows; v_permlane16_swap likewise across the
+// 16-lane rows, then one row_mirror exchange for R = 8). Returns row k's sum in lanes (64 / R) k .. + 64 / R - 1, the
+// same bits in each of them.
+template <int R>
+__device__ __forceinline__ float wave_sum_rows(const float (&v)[R]) {
+    static_assert(R == 2 || R == 4 || R == 8, "2, 4 or 8 rows");
+    float a[R / 2];
+#pragma unroll
+    for (int i = 0; i < R / 2; ++i) {
+        const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[R / 2 + i]), false,
+                                                        false);
+        a[i] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+    }
+    if constexpr (R == 2) {
+        return row_sum16(
+            [&] {
+                const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[0]), __float_as_uint(a[0]), false,
+                                                                false);
+                return __uint_as_float(x[0]) + __uint_as_float(x[1]);
+            }());
+    } else {
+        float b[R / 4];
+#pragma unroll
+        for (int i = 0; i < R / 4; ++i) {
+            const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[i]), __float_as_uint(a[R / 4 + i]), false,
+                                                            false);
+            b[i] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+        }
+        if constexpr (R == 4) {
+            return row_sum16(b[0]);
+        } else {
+            // lanes 0-7 of a 16-lane row keep b[0] and take b[0] of lane 15 - l; lanes 8-15 keep b[1] and take b[1]
+            const bool hi = (threadIdx.x & 8) != 0;
+            float c = (hi ? b[1] : b[0]) + dpp_f<0x140>(hi ? b[0] : b[1]);
+            c += dpp_f<0xB1>(c);
+            c += dpp_f<0x4E>(c);
+            return c + dpp_f<0x141>(c);
+        }
+    }
+}
+
 __device__ __forceinline__ float wave_max(float v) { return cross_rows_max(row_max16(v)); }
 
 // ---------------------------------------------------------------- the fp16 range monitor

@@ -365,11 +365,8 @@ __device__ __forceinline__ void rows_dot(const u32x4 (&wr)[NC], const float* vec
         for (int qq = 0; qq < kRowsW; ++qq)
             if (qq == q) acc[qq] += d;
     }
-#pragma unroll
-    for (int q = 0; q < kRowsW; ++q) {
-        const float s = wave_sum(acc[q]);
-        if (lane == 0) red[w * kRowsW + q] = s;
-    }
+    const float s = wave_sum_rows<kRowsW>(acc);  // row q in lanes 16 q .. + 15
+    if ((lane & (64 / kRowsW - 1)) == 0) red[w * kRowsW + lane / (64 / kRowsW)] = s;
 }
 
 // Stage stamps of the timing build (persist.hpp, LRM_PERSIST_STAMPS); nothing in the shipped build. Thread 0 keeps
@@ -539,14 +536,15 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             float xv[kNCH][8];
             norm_lane<kNCH>(xres, na, a.eps, xv);
             PSUB(0);
+            float acc[kRA];
 #pragma unroll
             for (int r = 0; r < kRA; ++r) {
-                float acc = 0.f;
+                acc[r] = 0.f;
 #pragma unroll
-                for (int c = 0; c < kNCH; ++c) acc = dot8(wa[r][c], xv[c], acc);
-                acc = wave_sum(acc);
-                if (lane == 0) red[r * kWaves + w] = acc;
+                for (int c = 0; c < kNCH; ++c) acc[r] = dot8(wa[r][c], xv[c], acc[r]);
             }
+            const float sr = wave_sum_rows<kRA>(acc);  // row r in lanes 32 r .. + 31
+            if ((lane & (64 / kRA - 1)) == 0) red[(lane / (64 / kRA)) * kWaves + w] = sr;
             PSUB(1);
         }
         // one wave stores the workgroup's rows (runs of kWaves consecutive entries), so each run is one write of whole
@@ -818,13 +816,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             PSUB(8);
             norm_lane<kNCH>(xres, nd, a.eps, xv);
             PSUB(9);
+            // unit jj's sum goes to red[(row ri) kNCH + chunk c] = red[w kUD + jj] (kUD is even)
+            float acc[8];
 #pragma unroll
-            for (int jj = 0; jj < kUD; ++jj) {
-                const int ri = (w * kUD + jj) / kNCH, c = jj % kNCH;
-                float acc = dot8(wd[jj], xv[c], 0.f);
-                acc = wave_sum(acc);
-                if (lane == 0) red[ri * kNCH + c] = acc;
-            }
+            for (int jj = 0; jj < 8; ++jj) acc[jj] = jj < kUD ? dot8(wd[jj % kUD], xv[jj % kNCH], 0.f) : 0.f;
+            const float su = wave_sum_rows<8>(acc);  // unit jj in lanes 8 jj .. + 7
+            if ((lane & 7) == 0 && (lane >> 3) < kUD) red[w * kUD + (lane >> 3)] = su;
             PSUB(10);
         }
         lds_barrier();
