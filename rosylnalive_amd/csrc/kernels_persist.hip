@@ -503,15 +503,23 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     // of a chunk, dims 8 (t % 16) .. + 7; V^T: dim t / 4, keys 16 (t % 4) .. + 15. Past the last chunk: re-read it
     // (never used).
     u32x4 kr[2][2], vr[2][2];
-    auto fetch = [&](auto set, int l, int c) __attribute__((always_inline)) {
+    auto fetch_k = [&](auto set, int l, int c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set)::value;
         const uint16_t* kb = a.kc + ((size_t(l) * kKVH + hk) * MP + k0) * 128 + 8 * (t & 15);
-        const uint16_t* vb = a.vc + ((size_t(l) * kKVH + hk) * 128 + (t >> 2)) * MP + k0 + 16 * (t & 3);
         const int cc = min(c, nch - 1) * 64;
 #pragma unroll
         for (int i = 0; i < 2; ++i) kr[SET][i] = ld16(kb + size_t(cc + (t >> 4) + 32 * i) * 128);
+    };
+    auto fetch_v = [&](auto set, int l, int c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set)::value;
+        const uint16_t* vb = a.vc + ((size_t(l) * kKVH + hk) * 128 + (t >> 2)) * MP + k0 + 16 * (t & 3);
+        const int cc = min(c, nch - 1) * 64;
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) vr[SET][jj] = ld16(vb + cc + 8 * jj);
+    };
+    auto fetch = [&](auto set, int l, int c) __attribute__((always_inline)) {
+        fetch_k(set, l, c);
+        fetch_v(set, l, c);
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
@@ -616,7 +624,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             const float vn = vnew[t >> 2];
             float m_run = -INFINITY, l_run = 0.f;  // waves 0 and 1: the running statistics of head w
             float o0 = 0.f, o1 = 0.f;              // dim t / 4 of both heads over keys 16 (t % 4) .. + 15
-            auto chunk = [&](auto set, auto tailc, int c) __attribute__((always_inline)) {
+            // chunk c from register set SET; with refill >= 0 the set's K registers take chunk refill's keys as soon as
+            // the scores are taken and its V^T registers after P V, so the refill's K load has the softmax and P V to
+            // land in
+            auto chunk = [&](auto set, auto tailc, int c, int refill) __attribute__((always_inline)) {
                 constexpr int SET = decltype(set)::value;
                 constexpr bool tail = decltype(tailc)::value;
                 const int cb = c * 64;
@@ -644,6 +655,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                         ps[1][key] = ok ? a1 * a.scale_log2 : -INFINITY;
                     }
                 }
+                if (refill >= 0) fetch_k(set, l, refill);
                 lds_barrier();
                 if (w < 2) {  // online softmax of head w over the chunk (its key 0 is always valid)
                     const float v = ps[w][lane];
@@ -677,6 +689,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 }
                 o0 = fmaf(o0, alpha_s[0], a0);
                 o1 = fmaf(o1, alpha_s[1], a1);
+                if (refill >= 0) fetch_v(set, l, refill);
                 if constexpr (!tail) lds_barrier();  // ps and alpha_s are rewritten by the next chunk
             };
             using Body = std::false_type;
@@ -684,16 +697,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
             PSUB(4);
             int c = 0;
             for (; c + 2 < nch; c += 2) {  // whole pairs before the last chunk
-                chunk(C0{}, Body{}, c);
-                fetch(C0{}, l, c + 2);
-                chunk(C1{}, Body{}, c + 1);
-                fetch(C1{}, l, c + 3);
+                chunk(C0{}, Body{}, c, c + 2);
+                chunk(C1{}, Body{}, c + 1, c + 3);
             }
             if (c + 1 < nch) {
-                chunk(C0{}, Body{}, c);
-                chunk(C1{}, Tail{}, c + 1);
+                chunk(C0{}, Body{}, c, -1);
+                chunk(C1{}, Tail{}, c + 1, -1);
             } else {
-                chunk(C0{}, Tail{}, c);
+                chunk(C0{}, Tail{}, c, -1);
             }
             PSUB(5);
             // reduce the four key groups of each dim, then the partial rows of both heads, (out[128], max, sum) and
