@@ -425,6 +425,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     __shared__ float lmv[kWaves];
     __shared__ uint32_t lmi[kWaves];
     __shared__ int s_fail;
+    // the odd chunks' scores and rescale factors (the even ones use ps and alpha_s)
+    __shared__ float ps_odd[2][64];
+    __shared__ float alpha_odd[2];
 
     const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: row offsets stay scalar
@@ -651,21 +654,21 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                     a1 = row_sum16(a1);
                     if ((t & 15) == 0) {
                         const bool ok = !tail || cb + key < nk;
-                        ps[0][key] = ok ? a0 * a.scale_log2 : -INFINITY;
-                        ps[1][key] = ok ? a1 * a.scale_log2 : -INFINITY;
+                        (SET ? ps_odd : ps)[0][key] = ok ? a0 * a.scale_log2 : -INFINITY;
+                        (SET ? ps_odd : ps)[1][key] = ok ? a1 * a.scale_log2 : -INFINITY;
                     }
                 }
                 if (refill >= 0) fetch_k(set, l, refill);
                 lds_barrier();
                 if (w < 2) {  // online softmax of head w over the chunk (its key 0 is always valid)
-                    const float v = ps[w][lane];
+                    const float v = (SET ? ps_odd : ps)[w][lane];
                     const float m_new = fmaxf(m_run, wave_max(v));
                     const float e = exp2f(v - m_new);
                     const float al = exp2f(m_run - m_new);  // 0 on the first chunk
                     l_run = l_run * al + wave_sum(e);
                     m_run = m_new;
-                    ps[w][lane] = e;
-                    if (lane == 0) alpha_s[w] = al;
+                    (SET ? ps_odd : ps)[w][lane] = e;
+                    if (lane == 0) (SET ? alpha_odd : alpha_s)[w] = al;
                 }
                 lds_barrier();
                 const int kg = 16 * (t & 3);
@@ -683,14 +686,15 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                     }
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        a0 = fmaf(ps[0][kg + 8 * jj + e], vf[e], a0);
-                        a1 = fmaf(ps[1][kg + 8 * jj + e], vf[e], a1);
+                        a0 = fmaf((SET ? ps_odd : ps)[0][kg + 8 * jj + e], vf[e], a0);
+                        a1 = fmaf((SET ? ps_odd : ps)[1][kg + 8 * jj + e], vf[e], a1);
                     }
                 }
-                o0 = fmaf(o0, alpha_s[0], a0);
-                o1 = fmaf(o1, alpha_s[1], a1);
+                o0 = fmaf(o0, (SET ? alpha_odd : alpha_s)[0], a0);
+                o1 = fmaf(o1, (SET ? alpha_odd : alpha_s)[1], a1);
                 if (refill >= 0) fetch_v(set, l, refill);
-                if constexpr (!tail) lds_barrier();  // ps and alpha_s are rewritten by the next chunk
+                // no barrier before the next chunk: it writes the other parity's ps and alpha_s, and the chunk after
+                // it writes these only past its first barrier, which every wave reaches after this P V
             };
             using Body = std::false_type;
             using Tail = std::true_type;
