@@ -13,7 +13,8 @@
 //   weights                    bf16 [n, k] (PyTorch Linear) for decode, f16 copies for prefill; q|k|v rows fused into
 //                              one [QC + 2 KC, hidden], gate|up rows fused into one [2 I, hidden]
 //   K cache                    f16  [kv_heads, max_pos, head_dim]   (head-major: one head's keys are contiguous)
-//   V cache                    f16  [kv_heads, head_dim, max_pos]   (transposed: the A operand of O^T = V^T P^T)
+//   V cache                    f16  [kv_heads, max_pos / 64, head_dim, 64]   (64-position blocks, each transposed: the
+//                              A operand of O^T = V^T P^T, and one contiguous 16 KiB per key block; kv_layout.hpp)
 //
 // MFMA: v_mfma_f32_16x16x32_f16. Operand layout (lane l, g = l / 16, c = l % 16): A supplies row c, k = 8g .. 8g + 7;
 // B supplies column c, k = 8g .. 8g + 7; D holds rows 4g .. 4g + 3 of column c.
@@ -29,6 +30,7 @@
 #include "device.hpp"
 #include "attn_prefill.hpp"
 #include "fast_common.hpp"
+#include "kv_layout.hpp"
 #include "persist.hpp"
 
 namespace lrm {
@@ -193,7 +195,7 @@ struct GemmArgs {
     const float* sin_t;
     uint16_t* q_out;      // [M, qh * 128] f16
     uint16_t* kc;         // [kvh, max_pos, 128] f16
-    uint16_t* vc;         // [kvh, 128, max_pos] f16
+    uint16_t* vc;         // [kvh, max_pos / 64, 128, 64] f16 (kv::v_at)
     int qh, kvh, pos0, max_pos;
     float eps;
     // PART: block z multiplies k range [z ksplit, (z + 1) ksplit) and writes its f32 partial to y32 + z M N
@@ -754,26 +756,26 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
         }
         __syncthreads();
         const int p0 = p.pos0 + m0;
-        const bool whole = (p0 & 7) == 0 && m0 + BM <= p.M;  // 16-byte aligned, every row of the tile present
+        // 16-byte aligned (8 positions in one 64-position block of the cache), every row of the tile present
+        const bool whole = (p0 & 7) == 0 && m0 + BM <= p.M;
         constexpr int CHV = BM / 8, RPP = 256 / CHV;  // 16-byte chunks per V^T row, rows per pass
         const int ch = t % CHV;
         uint32_t bad = 0;
-        uint16_t* vbase = p.vc + size_t(head - p.qh - p.kvh) * 128 * p.max_pos + p0 + ch * 8;
+        uint16_t* vhead = p.vc + size_t(head - p.qh - p.kvh) * 128 * p.max_pos;
 #pragma unroll
         for (int k = 0; k < 128 / RPP; ++k) {
             const int d = t / CHV + RPP * k;
             const u32x4 v = *reinterpret_cast<const u32x4*>(Vs + d * 136 + ch * 8);
-            uint16_t* dst = vbase + size_t(d) * p.max_pos;
             if (whole) {
                 bad |= f16_bad8(v);
-                *reinterpret_cast<u32x4*>(dst) = v;
+                *reinterpret_cast<u32x4*>(vhead + kv::v_at(p0 + ch * 8, d)) = v;
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
                     if (m0 + ch * 8 + e < p.M) {
                         const uint16_t h = uint16_t(v[e >> 1] >> (16 * (e & 1)));
                         bad |= f16_bad2(h);
-                        dst[e] = h;
+                        vhead[kv::v_at(p0 + ch * 8 + e, d)] = h;
                     }
             }
         }
@@ -835,13 +837,14 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
     const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kc + size_t(kvhead) * max_pos * 128, max_pos * 256);
     const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc + size_t(kvhead) * 128 * max_pos, max_pos * 256);
     // thread t moves chunks t + 256 i of a block: K row c / 16, dims 8 (c % 16) ..; V^T row (dim) c / 8, keys 8 (c % 8) ..
+    // (a 64-key block of either cache is 16 KiB contiguous at 256 bytes per key)
     int koff[4], voff[4], kst[4], vst[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int c = t + 256 * i;
         const int kr = c >> 4, kq = c & 15, vd = c >> 3, vq = c & 7;
         koff[i] = (kr * 128 + kq * 8) * 2;
-        voff[i] = (vd * max_pos + vq * 8) * 2;
+        voff[i] = (vd * 64 + vq * 8) * 2;
         kst[i] = kr * kKRow + 16 * kq;
         vst[i] = kVtOff + vd * kVRow + 16 * vq;
     }
@@ -890,7 +893,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(const uint16_t* q, cons
 #pragma unroll
         for (int i = 0; i < 4; ++i) rk[S][i] = __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, koff[i], kbk * 256, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rv[S][i] = __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, voff[i], kbv * 2, 0);
+        for (int i = 0; i < 4; ++i) rv[S][i] = __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, voff[i], kbv * 256, 0);
     };
     auto store_k = [&](auto set, auto stage) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value, G = decltype(stage)::value;
@@ -1373,7 +1376,7 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
     // keys (8 sub ..)
     const int d0 = 8 * (lane & 15), sub = t & 7, rg = t >> 3;
     const uint16_t* kb = kc + (size_t(kvhead) * max_pos + key0) * 128 + d0;
-    const uint16_t* vb = vc + size_t(kvhead) * 128 * max_pos + key0 + sub * 8;
+    const uint16_t* vb = vc + size_t(kvhead) * 128 * max_pos + sub * 8;  // + the chunk's block, + dim 64
     u32x4 kv4[2][ITS], vv[2][DD];
     auto fetch = [&](auto set, int c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set)::value;
@@ -1384,7 +1387,7 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
                 *reinterpret_cast<const u32x4*>(kb + size_t(c + wv * 4 * ITS + it * 4 + (lane >> 4)) * 128);
 #pragma unroll
         for (int dd = 0; dd < DD; ++dd)
-            vv[SET][dd] = *reinterpret_cast<const u32x4*>(vb + size_t(rg + RG * dd) * max_pos + c);
+            vv[SET][dd] = *reinterpret_cast<const u32x4*>(vb + kv::v_at(key0 + c, rg + RG * dd));
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
@@ -1432,7 +1435,7 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
             } else {
                 const uint16_t vh = f2h(kvv);
                 vnew[d] = h2f(vh);
-                vc[(size_t(kvhead) * 128 + d) * max_pos + pos] = vh;
+                vc[size_t(kvhead) * 128 * max_pos + kv::v_at(pos, d)] = vh;
                 f16_note(f16_bad2(vh), kF16Cache);
             }
         }
@@ -2618,6 +2621,7 @@ std::vector<KernelSpec> fast_catalog() {
                  [](const uint32_t* w, const uint32_t* c) {
                      const int64_t m = w[10], hid = w[11], qh = w[12], kvh = w[13], pos0 = w[14], mp = w[15];
                      need_group2("gemm_qkv_rope", w[12], w[13]);
+                     need_max_pos("gemm_qkv_rope", w[15]);  // the V cache's 64-position blocks
                      if (hid % 64 || hid < 64) contract_fail("gemm_qkv_rope: hidden must be a positive multiple of 64");
                      if (pos0 + m > mp) contract_fail("gemm_qkv_rope: positions past max_pos");
                      need(c, 0, m * hid, "gemm_qkv_rope", "h");

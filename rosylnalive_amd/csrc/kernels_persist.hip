@@ -58,6 +58,7 @@
 
 #include "device.hpp"
 #include "fast_common.hpp"
+#include "kv_layout.hpp"
 #include "persist.hpp"
 
 namespace lrm {
@@ -100,7 +101,7 @@ struct PArgs {
     const uint16_t* gate_up;     // [L, 2 I, H] f16 (gate rows, then up rows)
     const uint16_t* down;        // [L, H, I] f16
     uint16_t* kc;                // [L, KVH, MP, 128] f16
-    uint16_t* vc;                // [L, KVH, 128, MP] f16
+    uint16_t* vc;                // [L, KVH, MP / 64, 128, 64] f16 (kv::v_at)
     const float* cos_t;          // [MP, 64]
     const float* sin_t;          // [MP, 64]
     float* logits;               // [V]
@@ -515,10 +516,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
     };
     auto fetch_v = [&](auto set, int l, int c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set)::value;
-        const uint16_t* vb = a.vc + ((size_t(l) * kKVH + hk) * 128 + (t >> 2)) * MP + k0 + 16 * (t & 3);
+        const uint16_t* vb = a.vc + (size_t(l) * kKVH + hk) * 128 * MP + 16 * (t & 3);
         const int cc = min(c, nch - 1) * 64;
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) vr[SET][jj] = ld16(vb + cc + 8 * jj);
+        for (int jj = 0; jj < 2; ++jj) vr[SET][jj] = ld16(vb + kv::v_at(k0 + cc, t >> 2) + 8 * jj);
     };
     auto fetch = [&](auto set, int l, int c) __attribute__((always_inline)) {
         fetch_k(set, l, c);
@@ -608,7 +609,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persist(PArgs a) {
                 const uint16_t vh = f2h(val);
                 vnew[d] = h2f(vh);
                 if (has_pos) {
-                    a.vc[((size_t(l) * kKVH + hk) * 128 + d) * MP + pos] = vh;
+                    a.vc[(size_t(l) * kKVH + hk) * 128 * MP + kv::v_at(pos, d)] = vh;
                     f16_note(f16_bad2(vh), kF16Cache);
                 }
             }

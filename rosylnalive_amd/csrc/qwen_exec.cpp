@@ -3,6 +3,7 @@
 #include "safetensors.hpp"
 
 #include "attn_prefill.hpp"
+#include "kv_layout.hpp"
 #include "persist.hpp"
 
 #include <omp.h>
@@ -1100,7 +1101,7 @@ void QwenExec::read_cache(int seq, int layer, int which, int row0, int rows, flo
     for (int r = 0; r < rows; ++r)
         for (int h = 0; h < c.kv_heads; ++h)
             for (int d = 0; d < HD; ++d) {
-                size_t src = which ? (size_t(h) * HD + d) * MP + row0 + r : (size_t(h) * MP + row0 + r) * HD + d;
+                size_t src = which ? size_t(h) * HD * MP + kv::v_at(row0 + r, d) : (size_t(h) * MP + row0 + r) * HD + d;
                 out[size_t(r) * KC + h * HD + d] = half_to_float(all[src]);
             }
 }
@@ -1121,7 +1122,7 @@ void QwenExec::write_cache(int seq, int layer, int which, int row0, int rows, co
     for (int r = 0; r < rows; ++r)
         for (int h = 0; h < c.kv_heads; ++h)
             for (int d = 0; d < HD; ++d) {
-                size_t dst = which ? (size_t(h) * HD + d) * MP + row0 + r : (size_t(h) * MP + row0 + r) * HD + d;
+                size_t dst = which ? size_t(h) * HD * MP + kv::v_at(row0 + r, d) : (size_t(h) * MP + row0 + r) * HD + d;
                 all[dst] = float_to_half(in[size_t(r) * KC + h * HD + d]);
             }
     upload_tensor(n, all.data(), all.size() * 2);

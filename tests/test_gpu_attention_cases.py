@@ -22,6 +22,7 @@ import numpy as np
 import pytest
 
 from gpu_session import POISON_F32, Session
+from kv_layout import v_block, v_unblock
 from oracle import cpuref, metrics
 from rosylnalive_amd.gpu_core import DType, TensorFlags, attention_prefill_workspace_words
 from rosylnalive_amd.qwen import inv_freq_bits
@@ -208,9 +209,10 @@ def test_attention_prefill_f16_adversarial(name, gen, T, past):
     qb = _f16(q.reshape(T, 2048))
     kb, vb = _f16(k.reshape(keys, 1024)), _f16(v.reshape(keys, 1024))
     kc = np.full((8, mp, 128), 0x7E00, np.uint16)
-    vc = np.full((8, 128, mp), 0x7E00, np.uint16)
+    vt = np.full((8, 128, mp), 0x7E00, np.uint16)
     kc[:, :keys] = kb.reshape(keys, 8, 128).transpose(1, 0, 2)
-    vc[:, :, :keys] = vb.reshape(keys, 8, 128).transpose(1, 2, 0)
+    vt[:, :, :keys] = vb.reshape(keys, 8, 128).transpose(1, 2, 0)
+    vc = v_block(vt)  # the cache's 64-position blocks
     nws = attention_prefill_workspace_words(T, 8)
     s = Session({"q": (F16, qb.shape, 0, qb), "k": (F16, kc.shape, 0, kc), "v": (F16, vc.shape, 0, vc),
                  "y": (F16, qb.shape, 0, None), "ws": (U32, (nws,), 0, np.zeros(nws, np.uint32))})
@@ -242,9 +244,10 @@ def test_attention_decode_f16_adversarial(name, gen, pos, chunks):
     kr, vr = k.reshape(pos + 1, 1024), v.reshape(pos + 1, 1024)
     kb, vb = _f16(kr[:pos]), _f16(vr[:pos])
     kc = np.full((8, mp, 128), 0x7E00, np.uint16)
-    vc = np.full((8, 128, mp), 0x7E00, np.uint16)
+    vt = np.full((8, 128, mp), 0x7E00, np.uint16)
     kc[:, :pos] = kb.reshape(pos, 8, 128).transpose(1, 0, 2)
-    vc[:, :, :pos] = vb.reshape(pos, 8, 128).transpose(1, 2, 0)
+    vt[:, :, :pos] = vb.reshape(pos, 8, 128).transpose(1, 2, 0)
+    vc = v_block(vt)  # the cache's 64-position blocks
     rms = lambda x: float(np.sqrt(np.mean(np.asarray(x, np.float64) ** 2)))
     qn = cpuref.bf16_narrow(np.full(128, rms(q), np.float32))
     kn = cpuref.bf16_narrow(np.full(128, rms(kr[pos]), np.float32))
@@ -267,7 +270,7 @@ def test_attention_decode_f16_adversarial(name, gen, pos, chunks):
                                                    batch=1, chunks=chunks))], ["y"], reset={"kc": kc, "vc": vc})["y"]
         q64 = qkv[None].astype(np.float64)
         qr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, :2048].copy(), qn, 1e-6), 16, pos)
-        kc2, vc2 = s.read("kc"), s.read("vc")
+        kc2, vc2 = s.read("kc"), v_unblock(s.read("vc"), 8, mp)
         k_new = _hw(kc2[:, pos, :]).reshape(1, 1024)
         v_new = _hw(vc2[:, :, pos]).reshape(1, 1024)
         kf = np.concatenate([_hw(kb), k_new]).astype(np.float64)

@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 
 from gpu_session import POISON_16, Session, written_everywhere
+from kv_layout import v_block, v_unblock
 from oracle import cpuref, metrics
 from rosylnalive_amd.gpu_core import (ATTN_PREFILL_RECORD_WORDS, DType, TensorFlags,
                                       attention_prefill_workspace_words)
@@ -227,12 +228,13 @@ def test_gemm_qkv_rope_epilogue(T, pos0, max_pos):
         qr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(proj[:, :2048].copy(), qn, 1e-6), 16, pos0)
         kr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(proj[:, 2048:3072].copy(), kn, 1e-6), 8, pos0)
         v = proj[:, 3072:]
+        vt = v_unblock(out["vc"], 8, max_pos)  # the cache's 64-position blocks -> [head, dim, position]
         kc = hwiden(out["kc"][:, pos0:pos0 + T, :]).transpose(1, 0, 2).reshape(T, 1024)
-        vc = hwiden(out["vc"][:, :, pos0:pos0 + T]).transpose(2, 0, 1).reshape(T, 1024)
+        vc = hwiden(vt[:, :, pos0:pos0 + T]).transpose(2, 0, 1).reshape(T, 1024)
         for got, ref in [(hwiden(out["q"]), qr), (kc, kr), (vc, v)]:
             assert metrics.max_abs(got, ref) <= 2e-3 * max(1.0, np.abs(ref).max()), metrics.max_abs(got, ref)
         # rows outside [pos0, pos0 + T) are untouched
-        for c in (out["kc"][:, :pos0, :], out["kc"][:, pos0 + T:, :], out["vc"][:, :, :pos0], out["vc"][:, :, pos0 + T:]):
+        for c in (out["kc"][:, :pos0, :], out["kc"][:, pos0 + T:, :], vt[:, :, :pos0], vt[:, :, pos0 + T:]):
             assert np.all(c == POISON_16)
     finally:
         s.close()
@@ -252,14 +254,14 @@ def _qkv_inputs(T, pos0, max_pos, seed):
 
 
 def _caches(kb, vb, max_pos, fill=0):
-    """Token-major [pos, kvh * 128] fp16 rows -> the fast path's head-major K and transposed V caches; positions past
-    the rows hold `fill`."""
+    """Token-major [pos, kvh * 128] fp16 rows -> the fast path's head-major K cache and its V cache (64-position blocks
+    of [dim][position] tiles); positions past the rows hold `fill`."""
     P = kb.shape[0]
     kc = np.full((8, max_pos, 128), fill, np.uint16)
-    vc = np.full((8, 128, max_pos), fill, np.uint16)
+    vt = np.full((8, 128, max_pos), fill, np.uint16)
     kc[:, :P, :] = kb.reshape(P, 8, 128).transpose(1, 0, 2)
-    vc[:, :, :P] = vb.reshape(P, 8, 128).transpose(1, 2, 0)
-    return kc, vc
+    vt[:, :, :P] = vb.reshape(P, 8, 128).transpose(1, 2, 0)
+    return kc, v_block(vt)
 
 
 def test_attention_prefill_f16_split_across_xcds():
@@ -273,9 +275,10 @@ def test_attention_prefill_f16_split_across_xcds():
     kb = f16(r.standard_normal((T, kvh * 128)))
     vb = f16(r.standard_normal((T, kvh * 128)))
     kc = np.full((kvh, max_pos, 128), 0x7E00, np.uint16)
-    vc = np.full((kvh, 128, max_pos), 0x7E00, np.uint16)
+    vt = np.full((kvh, 128, max_pos), 0x7E00, np.uint16)
     kc[:, :T, :] = kb.reshape(T, kvh, 128).transpose(1, 0, 2)
-    vc[:, :, :T] = vb.reshape(T, kvh, 128).transpose(1, 2, 0)
+    vt[:, :, :T] = vb.reshape(T, kvh, 128).transpose(1, 2, 0)
+    vc = v_block(vt)
     nws = attention_prefill_workspace_words(T, kvh)
     s = Session({"q": (F16, qb.shape, 0, qb), "k": (F16, kc.shape, 0, kc), "v": (F16, vc.shape, 0, vc),
                  "y": (F16, qb.shape, 0, None), "ws": (U32, (nws,), 0, np.zeros(nws, np.uint32))})
@@ -546,14 +549,14 @@ def test_attention_decode_f16(pos, chunks):
         q64 = qkv[None].astype(np.float64)
         qr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, :2048].copy(), qn, 1e-6), 16, pos)
         kr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, 2048:3072].copy(), kn, 1e-6), 8, pos)
-        kc2, vc2 = s.read("kc"), s.read("vc")
+        kc2, vc2 = s.read("kc"), v_unblock(s.read("vc"), 8, max_pos)
         k_new = hwiden(kc2[:, pos, :]).reshape(1, 1024)
         v_new = vc2[:, :, pos].reshape(1, 1024)
         assert np.all(np.abs(k_new - kr) <= np.abs(kr) * 2.0 ** -10 + 2.0 ** -24), "appended key"
         assert v_new.tobytes() == f16(qkv[3072:]).reshape(1, 1024).tobytes(), "appended value"
         # other positions are untouched
         assert np.array_equal(np.delete(kc2, pos, axis=1), np.delete(kc, pos, axis=1))
-        assert np.array_equal(np.delete(vc2, pos, axis=2), np.delete(vc, pos, axis=2))
+        assert np.array_equal(np.delete(vc2, pos, axis=2), np.delete(v_unblock(vc, 8, max_pos), pos, axis=2))
         kf = np.concatenate([hwiden(kb[:pos]), k_new]).astype(np.float64)
         vf = np.concatenate([hwiden(vb[:pos]), hwiden(v_new)]).astype(np.float64)
         ref = cpuref.attention(qr, kf, vf, 16, 8, 128, pos, scale)
@@ -671,7 +674,7 @@ def test_attention_decode_batched_f16_combine(chunks, splits):
     s = Session({"qkv": (F32, qkv.shape, RO, qkv), "qn": (BF16, (128,), RO, qn), "kn": (BF16, (128,), RO, kn),
                  "cos": (F32, cos.shape, RO, cos), "sin": (F32, sin.shape, RO, sin),
                  "kc": (F16, (B * 8, max_pos, 128), 0, np.concatenate(kcs)),
-                 "vc": (F16, (B * 8, 128, max_pos), 0, np.concatenate(vcs)),
+                 "vc": (F16, (B * 8 * max_pos // 64, 128, 64), 0, np.concatenate(vcs).reshape(-1, 128, 64)),
                  "part": (F32, (B * 16 * S * 130,), 0, None), "y": (F16, (B, 2048), 0, None),
                  "state": (U32, state.shape, RO, state)})
     try:
@@ -686,7 +689,7 @@ def test_attention_decode_batched_f16_combine(chunks, splits):
                                                               splits=splits))],
                               ["y"])["y"])
         kc2 = s.read("kc").reshape(B, 8, max_pos, 128)
-        vc2 = s.read("vc").reshape(B, 8, 128, max_pos)
+        vc2 = v_unblock(s.read("vc"), B * 8, max_pos).reshape(B, 8, 128, max_pos)
         for b, pos in enumerate(positions):
             q64 = qkv[b][None].astype(np.float64)
             qr = cpuref.rope_apply(cos, sin, cpuref.rmsnorm(q64[:, :2048].copy(), qn, 1e-6), 16, pos)
