@@ -736,8 +736,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs p) {
     };
 
     if (EPI == EPI_QKV) {
-        // V: the cache is V^T ([dim][position]), so the tile is transposed through LDS (after the 32 KiB of x32, rows
-        // of 128 positions padded to 136) and written as whole 256-byte rows of 16-byte stores, not 2-byte ones
+        // V: the cache holds [dim][position] tiles of 64 positions (kv::v_at), so the tile is transposed through LDS
+        // (after the 32 KiB of x32, rows of 128 positions padded to 136) and written as 16-byte runs of 8 positions,
+        // not 2-byte stores
         uint16_t* Vs = lds + 16384;
         if (wn == 0) {
 #pragma unroll
