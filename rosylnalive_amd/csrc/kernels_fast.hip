@@ -1354,8 +1354,8 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
     __shared__ float qs[2][128];
     __shared__ float knew[128];
     __shared__ float vnew[128];
-    __shared__ float ps[2][64];
-    __shared__ float alpha_s[2];
+    __shared__ float ps[2][2][64];  // [chunk parity][query head][key]
+    __shared__ float alpha_s[2][2];
     __shared__ float redq[4], redk[4];
     const int s = blockIdx.x, S = gridDim.x, kvhead = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int b = blockIdx.z;  // the sequence: its projections, caches and partials follow the previous ones
@@ -1485,30 +1485,30 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
             a1 = row_sum16(a1);
             if ((lane & 15) == 0) {
                 const bool ok = !tail || cb + key < nkeys;
-                ps[0][key] = ok ? a0 * scale_log2 : -INFINITY;
-                ps[1][key] = ok ? a1 * scale_log2 : -INFINITY;
+                ps[SET][0][key] = ok ? a0 * scale_log2 : -INFINITY;
+                ps[SET][1][key] = ok ? a1 * scale_log2 : -INFINITY;
             }
         }
         __syncthreads();
         if (wv < 2) {  // online softmax of head wv over this chunk (key 0 of a chunk is always valid)
-            const float v = ps[wv][lane];
+            const float v = ps[SET][wv][lane];
             const float m_new = fmaxf(m_run, wave_max(v));
             const float e = exp2f(v - m_new);
             const float al = exp2f(m_run - m_new);  // 0 on the first chunk
             l_run = l_run * al + wave_sum(e);
             m_run = m_new;
-            ps[wv][lane] = e;
-            if (lane == 0) alpha_s[wv] = al;
+            ps[SET][wv][lane] = e;
+            if (lane == 0) alpha_s[SET][wv] = al;
         }
         __syncthreads();
         // P V: thread t covers V^T rows rg + RG dd and keys 8 sub .. + 7 of the chunk
         float e0[8], e1[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            e0[e] = ps[0][sub * 8 + e];
-            e1[e] = ps[1][sub * 8 + e];
+            e0[e] = ps[SET][0][sub * 8 + e];
+            e1[e] = ps[SET][1][sub * 8 + e];
         }
-        const float al0 = alpha_s[0], al1 = alpha_s[1];
+        const float al0 = alpha_s[SET][0], al1 = alpha_s[SET][1];
 #pragma unroll
         for (int dd = 0; dd < DD; ++dd) {
             float vf[8];
@@ -1529,7 +1529,8 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
             o0[dd] = fmaf(o0[dd], al0, a0);
             o1[dd] = fmaf(o1[dd], al1, a1);
         }
-        __syncthreads();  // ps and alpha_s are rewritten by the next chunk
+        // no barrier before the next chunk: it writes the other parity's ps and alpha_s, and the chunk after it
+        // writes these only past its first barrier, which every wave reaches after this P V
     };
     using Body = std::false_type;
     using Tail = std::true_type;
