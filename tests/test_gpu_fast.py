@@ -652,11 +652,14 @@ def test_gemm_skinny_swiglu(m, inter, k):
         s.close()
 
 
-@pytest.mark.parametrize("chunks,splits", [(1, 0), (4, 0), (0, 3), (0, 16)])
+@pytest.mark.parametrize("chunks,splits", [(1, 0), (4, 0), (8, 0), (0, 1), (0, 2), (0, 3), (0, 16)])
 def test_attention_decode_batched_f16_combine(chunks, splits):
     """Three sequences at positions 5, 64 and 700 in one dispatch (batch on the grid), then the fp16 combine; each
     sequence against CpuRef F64 on its own cache. splits > 0: each sequence's keys spread evenly over that many
-    splits (3: 64, 64 and 256 keys per split; 16: one chunk each, 1, 2 and 11 splits holding keys)."""
+    splits (3: 64, 64 and 256 keys per split; 16: one chunk each, 1, 2 and 11 splits holding keys). The streaming
+    form holds four chunks in flight: position 700 runs 8 + 3 chunks per split at chunks = 8, 11 in one split, and
+    6 + 5 in two, so its loop of four-chunk groups runs once or twice and every length of the last group (1 .. 4)
+    occurs."""
     max_pos, S = 1024, 16
     positions = [5, 64, 700]
     B = len(positions)
