@@ -1339,6 +1339,8 @@ __global__ __launch_bounds__(256) void k_gemv_norm_dec(const float* x, const uin
 // ahead loading meanwhile; the 8 key groups are reduced once at the end. Each block writes, per head, (max, sum,
 // unnormalised output[128]); splits past pos do nothing. Positions past pos are loaded (they lie inside max_pos) but
 // masked by selects: the scores to -inf, the values to 0 (unwritten positions may hold anything).
+// Every barrier orders LDS only (lds_barrier): a __syncthreads() would also wait for the chunks in flight, so each
+// chunk would drain the next one's loads at its first barrier.
 // MULTI = false is the one-chunk form (chunks == 1): 256 threads, no second register set and no loop, so the
 // registers stay low enough for many blocks per CU, which the one-sequence decode needs (its splits are its only
 // parallelism). MULTI = true streams chunks with 512 threads: a chunk's scores and P V spread over 8 waves, halving
@@ -1400,21 +1402,25 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
+
+    // the raw projections, the norm weights and the rotation of pos (threads 0 .. 255; the rest wait at the barriers),
+    // loaded ahead of the first chunks: loads return in issue order, so the norm, rotation and append below run while
+    // the chunks are in flight instead of after they land (1.7B, 16 sequences x 8K: 4283 -> 4310 tok/s)
+    const int hh = (t >> 7) & 1, d = t & 127;  // thread t: q head 2 kvhead + hh; new key (hh = 0) or value (hh = 1)
+    const bool pro = t < 256;
+    const int QC = qh * 128, KC = kvh * 128;
+    const float qv = qkv[(kvhead * 2 + hh) * 128 + d];
+    const float kvv = qkv[QC + hh * KC + kvhead * 128 + d];
+    const float cs = cos_t[size_t(pos) * 64 + (d & 63)], sn = sin_t[size_t(pos) * 64 + (d & 63)];
+    const uint16_t qwb = qn[d], kwb = kn[d];
+    __builtin_amdgcn_sched_barrier(0);
     fetch(C0{}, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (MULTI) {
         fetch(C1{}, 1);
         __builtin_amdgcn_sched_barrier(0);
     }
-
-    // the raw projections, the norm weights and the rotation of pos (threads 0 .. 255; the rest wait at the barriers)
-    const int hh = (t >> 7) & 1, d = t & 127;  // thread t: q head 2 kvhead + hh; new key (hh = 0) or value (hh = 1)
-    const bool pro = t < 256;
-    const int QC = qh * 128, KC = kvh * 128;
-    const float qv = pro ? qkv[(kvhead * 2 + hh) * 128 + d] : 0.f;
-    const float kvv = pro && has_pos ? qkv[QC + hh * KC + kvhead * 128 + d] : 0.f;
-    const float cs = cos_t[size_t(pos) * 64 + (d & 63)], sn = sin_t[size_t(pos) * 64 + (d & 63)];
-    const float qw = bf2f(qn[d]), kw = bf2f(kn[d]);
+    const float qw = bf2f(qwb), kw = bf2f(kwb);
 
     // per-head RMSNorm (head hh = waves 2 hh, 2 hh + 1; the new key = waves 0, 1), then the rotation of (d, d + 64)
     const float sq = wave_sum(qv * qv), sk = wave_sum(kvv * kvv);
@@ -1422,17 +1428,17 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
         redq[wv] = sq;
         redk[wv] = sk;
     }
-    __syncthreads();
+    lds_barrier();
     const float qr = qw * (qv * (1.0f / sqrtf((redq[2 * hh] + redq[2 * hh + 1]) / 128.0f + eps)));
     const float kr = kw * (kvv * (1.0f / sqrtf((redk[0] + redk[1]) / 128.0f + eps)));
     if (pro) {
         qs[hh][d] = qr;
         if (hh == 0) knew[d] = kr;
     }
-    __syncthreads();
+    lds_barrier();
     const float qrot = d < 64 ? qr * cs - qs[hh][d + 64] * sn : qr * cs + qs[hh][d - 64] * sn;
     const float krot = d < 64 ? kr * cs - knew[d + 64] * sn : kr * cs + knew[d - 64] * sn;
-    __syncthreads();
+    lds_barrier();
     if (pro) {
         qs[hh][d] = qrot;
         if (has_pos) {
@@ -1449,7 +1455,7 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
     // this thread's query dims and, for the split holding pos, its slices of the new key and value (read
     // unconditionally, used only through selects: a conditional LDS read would become a branch per element)
     float q0[8], q1[8], kn8[8], vnd[DD];
@@ -1497,7 +1503,7 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
                 ps[SET][1][key] = ok ? a1 * scale_log2 : -INFINITY;
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (wv < 2) {  // online softmax of head wv over this chunk (key 0 of a chunk is always valid)
             const float v = ps[SET][wv][lane];
             const float m_new = fmaxf(m_run, wave_max(v));
@@ -1508,7 +1514,7 @@ __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv
             ps[SET][wv][lane] = e;
             if (lane == 0) alpha_s[SET][wv] = al;
         }
-        __syncthreads();
+        lds_barrier();
         // P V: thread t covers V^T rows rg + RG dd and keys 8 sub .. + 7 of the chunk
         float e0[8], e1[8];
 #pragma unroll
