@@ -1331,10 +1331,11 @@ __global__ __launch_bounds__(256) void k_gemv_norm_dec(const float* x, const uin
 // 64 C) for the two query heads of the group, 64 keys at a time. C = chunks per split: given by the caller (1 for one
 // sequence, whose splits are its only parallelism), or, with chunks = 0, the fewest that cover 0 .. pos in the grid's
 // S splits, C = ceil((pos + 1) / 64 S): every sequence's keys then spread evenly over its S blocks, so a grid sized to
-// one round of resident blocks ends with them all instead of a partly filled last round. It issues the loads of its first two
-// chunks, then applies the q RMSNorm and RoPE to the raw projection; the block whose split holds pos also computes the
-// new key (k RMSNorm + RoPE) and value, appends them (fp16) to the caches and uses the same rounded values in place of
-// the stale slot it loaded. Per chunk: scores (each key's dot over 16 lanes), an online softmax per head in the log2
+// one round of resident blocks ends with them all instead of a partly filled last round. It loads the raw projections,
+// issues the loads of its first two chunks, then applies the q RMSNorm and RoPE; the block whose split holds pos also
+// computes the
+// new key (k RMSNorm + RoPE) and value, appends them (fp16) to the caches and uses the same rounded values in place
+// of the stale slot it loaded. Per chunk: scores (each key's dot over 16 lanes), an online softmax per head in the log2
 // domain, and P V accumulated per thread (its 4 dims x 8 keys, rescaled when the maximum moves), with the chunk two
 // ahead loading meanwhile; the 8 key groups are reduced once at the end. Each block writes, per head, (max, sum,
 // unnormalised output[128]); splits past pos do nothing. Positions past pos are loaded (they lie inside max_pos) but
@@ -1344,7 +1345,7 @@ __global__ __launch_bounds__(256) void k_gemv_norm_dec(const float* x, const uin
 // MULTI = false is the one-chunk form (chunks == 1): 256 threads, no second register set and no loop, so the
 // registers stay low enough for many blocks per CU, which the one-sequence decode needs (its splits are its only
 // parallelism). MULTI = true streams chunks with 512 threads: a chunk's scores and P V spread over 8 waves, halving
-// each wave's share of the per-chunk chain (scores, softmax, P V, three barriers) that bounds a block's rate.
+// each wave's share of the per-chunk chain (scores, softmax, P V, two barriers) that bounds a block's rate.
 template <bool MULTI>
 __global__ __launch_bounds__(MULTI ? 512 : 256) void k_attn_dec(const float* qkv, const uint16_t* qn,
                                                                 const uint16_t* kn, const float* cos_t,
