@@ -139,7 +139,10 @@ def test_fast_rejects_weights_outside_fp16(fast_setup):
     m.set_weight(name, w[name])
 
 
-def test_fast_prefill_logits_within_north_star_bound(fast_setup):
+def test_fast_prefill_logits_within_tolerance_of_cpuref(fast_setup):
+    """A 200-token fast-mode prefill against CpuRef F32: logits within 2e-2 max-abs, top-1 agreement at least 0.99,
+    every top-1 disagreement a near tie (gap at most twice the max-abs error), and the returned id the last row's
+    argmax."""
     cfg, w, orc, m = fast_setup
     ids = synthetic_ids(5, "fast/prompt", 200, cfg.vocab)
     lg, am = m.forward(ids, 0)
