@@ -777,28 +777,43 @@ uint32_t QwenExec::forward_fast(int seq, int pos0, int T, float* logits, int lr)
         residual_norm("a", p + "down_proj.f16", I,
                       i + 1 < c.layers ? tk(lname(i + 1, kLayerWeights[0])) : tk("model.norm.weight"), ash);
     }
-    // logits of the last lr rows, LC rows per lm_head dispatch
+    // logits of the last lr rows, LC rows per lm_head dispatch: the final norm over rows r0 .. r0 + n - 1, the lm_head
+    // GEMM, and after the last rows the argmax of the last one (the forward returns the last row's id)
+    auto lm_head = [&](CommandList* L, int r0, uint32_t n) {
+        dispatch(L, "rmsnorm_rows_f16", {tk("x"), tk("model.norm.weight"), tk("h"), n, H, eps, uint32_t(r0)});
+        dispatch(L, "gemm_f32", {tk("h"), tk("embed.f16"), tk("logits"), n, V, H});
+        if (r0 + int(n) == T) {
+            dispatch(L, "argmax_rows_partial", {tk("logits"), tk("argmax.partials"), 1, V, n - 1});
+            dispatch(L, "argmax_rows_final", {tk("argmax.partials"), tk("argmax"), 1});
+        }
+    };
+    // rows that fit one dispatch ride in the layers' list: one submission, so the GPU does not wait for the host
+    // between the last layer and the lm_head (2048-token prefill, last row: 4.11 -> 4.09 ms; 512-token forward with
+    // all its logits: 2.22 -> 2.19 ms)
+    const bool one = uint32_t(lr) <= LC;
+    if (one) lm_head(l, T - lr, uint32_t(lr));
     hipEvent_t e0, e1;
     hip_check(hipEventCreate(&e0), "event");
     hip_check(hipEventCreate(&e1), "event");
     hip_check(hipEventRecord(e0, dev_.stream()), "event");
     uint64_t f = dev_.submit(l);
+    if (one) hip_check(hipEventRecord(e1, dev_.stream()), "event");
     dev_.wait(f);
     dev_.release(l);
     uint32_t am = 0;
-    for (int r0 = T - lr; r0 < T; r0 += int(LC)) {
+    if (one) {
+        hip_check(hipEventSynchronize(e1), "event");
+        download_tensor("argmax", &am, 4, 0);
+        if (logits) download_tensor("logits", logits, uint64_t(lr) * V * 4);
+    }
+    for (int r0 = T - lr; !one && r0 < T; r0 += int(LC)) {
         const uint32_t n = uint32_t(std::min(int(LC), T - r0));
         CommandList* l2 = dev_.begin();
-        dispatch(l2, "rmsnorm_rows_f16", {tk("x"), tk("model.norm.weight"), tk("h"), n, H, eps, uint32_t(r0)});
-        dispatch(l2, "gemm_f32", {tk("h"), tk("embed.f16"), tk("logits"), n, V, H});
-        const bool last = r0 + int(n) == T;
-        if (last) {  // the forward returns the last row's id: reduce that row alone
-            dispatch(l2, "argmax_rows_partial", {tk("logits"), tk("argmax.partials"), 1, V, n - 1});
-            dispatch(l2, "argmax_rows_final", {tk("argmax.partials"), tk("argmax"), 1});
-        }
+        lm_head(l2, r0, n);
         uint64_t f2 = dev_.submit(l2);
         dev_.wait(f2);
         dev_.release(l2);
+        const bool last = r0 + int(n) == T;
         if (last) {
             hip_check(hipEventRecord(e1, dev_.stream()), "event");
             hip_check(hipEventSynchronize(e1), "event");
